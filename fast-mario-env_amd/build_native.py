@@ -1,0 +1,48 @@
+"""Builds libmario_hip.so (gfx950 code objects + host C ABI) in-tree with hipcc.
+
+    python fast-mario-env_amd/build_native.py
+
+Flags: -ffp-contract=off keeps the INTER_AREA float sums unfused (bit-exact with the reference's
+-ffp-contract=off CPU build); packed FP32 instructions are disabled for every HIP translation unit.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SRC = os.path.join(HERE, "csrc", "mario_hip.hip")
+OUT = os.path.join(HERE, "fast_mario_env_amd", "libmario_hip.so")
+ARCH = os.environ.get("MARIO_HIP_ARCH", "gfx950")
+FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC)")
+
+
+def build(verbose: bool = True) -> str:
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", *FLAGS, SRC, "-o", tmp]
+    if verbose:
+        print("building:", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "not a recognized feature"
+    msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l and l.strip())
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{msgs}")
+    if msgs and verbose:
+        print(msgs, flush=True)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build())
+    sys.exit(0)

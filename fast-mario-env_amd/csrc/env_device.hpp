@@ -1,0 +1,243 @@
+// Device-side env layer: gym-super-mario-bros reward / done / info, the wrapper stack (sticky actions,
+// frame skip, 2-frame max-pool, early termination, life loss, no-op starts, time limit) and the level
+// boot, as in the reference's csrc/fastmario.cpp:204-445.
+#pragma once
+#include "nes_device.hpp"
+
+namespace mh {
+
+// Per-env words beside the console state, interleaved as EV[w * NP + e].
+enum EnvWord : int {
+    E_XLAST_LO = 0, E_XLAST_HI, E_TLAST_LO, E_TLAST_HI, E_PREV, E_LIVES, E_T, E_EP_LEN,
+    E_EPRET_LO, E_EPRET_HI, E_SHOWS_BOOT, E_POOLED, E_LEVEL, E_FRAMES_LO, E_FRAMES_HI,
+    E_BAD, E_INSTR_LO, E_INSTR_HI,
+    E_RNG_S0, E_RNG_S1, E_RNG_S2, E_RNG_S3, E_RNG_I0, E_RNG_I1, E_RNG_I2, E_RNG_I3,   // little-endian u32 limbs
+    E_RNG_HAS32, E_RNG_HALF, E_DONE, E_RESET_IDX, E_COUNT
+};
+
+constexpr int MAX_SKIP = 16;
+constexpr int HACK_FRAME_LIMIT = 20000;   // guard against a game stuck in a busy state (the reference loops forever)
+constexpr uint32_t ERR_HACK_LIMIT = 1u << 24;
+
+__device__ __constant__ static const uint8_t kButtons[8] = {0x00, 0x80, 0x81, 0x82, 0x83, 0x01, 0x40, 0x00};
+
+// numpy PCG64 (XSL-RR 128/64) with Generator.random() and the 32-bit Lemire integers() path
+// (fastmario.cpp:39-78; numpy's bit generator and `random_bounded_uint64` for ranges < 2^32).
+struct Pcg {
+    unsigned __int128 state, inc;
+    uint32_t has32, half;
+    __device__ uint64_t next64() {
+        const unsigned __int128 mul = ((unsigned __int128)0x2360ED051FC65DA4ULL << 64) | 0x4385DF649FCCF645ULL;
+        state = state * mul + inc;
+        uint64_t xs = (uint64_t)(state >> 64) ^ (uint64_t)state;
+        unsigned r = (unsigned)(state >> 122);
+        return (xs >> r) | (xs << ((64 - r) & 63));
+    }
+    __device__ uint32_t next32() {
+        if (has32) { has32 = 0; return half; }
+        uint64_t w = next64();
+        has32 = 1; half = (uint32_t)(w >> 32);
+        return (uint32_t)w;
+    }
+    __device__ double random() { return (double)(next64() >> 11) * (1.0 / 9007199254740992.0); }
+    __device__ int64_t integers(int64_t high) {
+        uint64_t rng = (uint64_t)(high - 1);
+        if (rng == 0) return 0;
+        if (rng == 0xffffffffULL) return next32();
+        uint32_t excl = (uint32_t)rng + 1;
+        uint64_t prod = (uint64_t)next32() * excl;
+        uint32_t left = (uint32_t)prod;
+        if (left < excl) {
+            uint32_t thr = (uint32_t)((0xffffffffu - (uint32_t)rng) % excl);
+            while (left < thr) { prod = (uint64_t)next32() * excl; left = (uint32_t)prod; }
+        }
+        return (int64_t)(prod >> 32);
+    }
+    __device__ void load(const uint32_t* ev, uint32_t np, uint32_t e) {
+        auto w = [&](int k) { return (unsigned __int128)ev[(size_t)k * np + e]; };
+        state = w(E_RNG_S0) | (w(E_RNG_S1) << 32) | (w(E_RNG_S2) << 64) | (w(E_RNG_S3) << 96);
+        inc = w(E_RNG_I0) | (w(E_RNG_I1) << 32) | (w(E_RNG_I2) << 64) | (w(E_RNG_I3) << 96);
+        has32 = ev[(size_t)E_RNG_HAS32 * np + e];
+        half = ev[(size_t)E_RNG_HALF * np + e];
+    }
+    __device__ void store(uint32_t* ev, uint32_t np, uint32_t e) const {
+        for (int k = 0; k < 4; k++) {
+            ev[(size_t)(E_RNG_S0 + k) * np + e] = (uint32_t)(state >> (32 * k));
+            ev[(size_t)(E_RNG_I0 + k) * np + e] = (uint32_t)(inc >> (32 * k));
+        }
+        ev[(size_t)E_RNG_HAS32 * np + e] = has32;
+        ev[(size_t)E_RNG_HALF * np + e] = half;
+    }
+};
+
+// ------------------------------------------------------------------ SMB RAM protocol (fastmario.cpp:204-250)
+struct Info { int64_t v[10]; };   // x_pos flag_get life score time world stage coins y_pos status
+
+__device__ __forceinline__ int64_t dec_digits(const Console& c, uint32_t ad, int n) {
+    int64_t val = 0;
+    for (int i = 0; i < n; i++) {
+        int b = c.ram(ad + i);
+        val = val * (b >= 100 ? 1000 : b >= 10 ? 100 : 10) + b;
+    }
+    return val;
+}
+__device__ __forceinline__ int64_t smb_x(const Console& c) { return (int64_t)c.ram(0x6d) * 256 + c.ram(0x86); }
+__device__ __forceinline__ int64_t smb_time(const Console& c) { return dec_digits(c, 0x7f8, 3); }
+__device__ __forceinline__ bool smb_busy(const Console& c) { uint8_t s = c.ram(0x0e); return s <= 5 || s == 7; }
+__device__ __forceinline__ bool smb_world_over(const Console& c) { return c.ram(0x770) == 2; }
+__device__ __forceinline__ bool smb_stage_over(const Console& c) {
+    for (uint32_t ad = 0x16; ad <= 0x1a; ad++) {
+        uint8_t id = c.ram(ad);
+        if (id == 0x2d || id == 0x31) return c.ram(0x1d) == 3;
+    }
+    return false;
+}
+__device__ Info smb_info(const Console& c) {
+    Info i;
+    i.v[0] = smb_x(c);
+    i.v[1] = smb_world_over(c) || smb_stage_over(c);
+    i.v[2] = c.ram(0x75a);
+    i.v[3] = dec_digits(c, 0x7de, 6);
+    i.v[4] = smb_time(c);
+    i.v[5] = c.ram(0x75f) + 1;
+    i.v[6] = c.ram(0x75c) + 1;
+    i.v[7] = dec_digits(c, 0x7ed, 2);
+    uint8_t yp = c.ram(0x3b8);
+    i.v[8] = c.ram(0xb5) < 1 ? 255 + (255 - yp) : 255 - yp;
+    uint8_t st = c.ram(0x756);
+    i.v[9] = st == 0 ? 0 : st == 1 ? 1 : 2;
+    return i;
+}
+
+struct Cfg {
+    int skip, max_steps, noop_max, maxpool;
+    double sticky;
+};
+
+// Memory region of consoles with the same layout as the live state (used for snapshots / caches).
+struct Region {
+    uint8_t* mem;       // row-major [row * np + idx]
+    uint32_t* sc;       // [word * np + idx]
+    uint32_t np;
+    uint32_t idx;
+};
+
+__device__ inline void copy_console(const Region& dst, const Region& src) {
+    for (uint32_t r = 0; r < MEM_ROWS; r++)
+        dst.mem[(size_t)r * dst.np + dst.idx] = src.mem[(size_t)r * src.np + src.idx];
+    for (int w = 0; w < S_COUNT; w++) dst.sc[(size_t)w * dst.np + dst.idx] = src.sc[(size_t)w * src.np + src.idx];
+}
+
+// One env's layer state in registers.
+struct EnvRegs {
+    int64_t x_last, time_last;
+    int prev, lives, t, ep_len;
+    double ep_ret;
+    bool shows_boot, pooled;
+    uint64_t frames;
+    uint32_t draws;     // sticky draws taken (counted by the reset-cache builder)
+    Info info;
+};
+
+struct Stepper {
+    Console& c;
+    EnvRegs& ev;
+    const Cfg& cfg;
+    Pcg* rng;             // null: draws are counted, not taken (reset cache: action 0 == prev 0)
+    uint8_t* gray0;       // frame K-1 (and every early-termination final frame)
+    uint8_t* gray1;       // frame K-2 (max-pool partner)
+    Region live, snap;    // the console's own region and its step-start snapshot
+    bool snapped;
+
+    __device__ void nes_frame(uint8_t buttons, bool render, uint8_t* slot) {
+        c.joy_buttons[0] = buttons;
+        c.render = render;
+        c.gray = slot;
+        c.frame();
+        ev.frames++;
+        if (render) ev.shows_boot = false;
+    }
+    // _skip_change_area / _skip_occupied_states of a not-done env (fastmario.cpp:297-308)
+    __device__ void skip_busy(bool render, uint8_t* slot) {
+        uint8_t cat = c.ram(0x6de);
+        if (cat > 1 && cat < 255) c.st(ROW_RAM + 0x6de, 1);
+        int guard = 0;
+        while (smb_busy(c) || smb_world_over(c)) {
+            if (++guard > HACK_FRAME_LIMIT) { c.bad_ops |= ERR_HACK_LIMIT; break; }
+            c.st(ROW_RAM + 0x7a0, 0);
+            nes_frame(0, render, slot);
+        }
+    }
+    // reward, done, info, hacks (fastmario.cpp:310-334)
+    __device__ double frame_step(uint8_t buttons, bool render, uint8_t* slot, bool* done) {
+        nes_frame(buttons, render, slot);
+        int64_t xx = smb_x(c), dx = xx - ev.x_last;
+        ev.x_last = xx;
+        if (dx < -5 || dx > 5) dx = 0;
+        int64_t tm = smb_time(c), dt = tm - ev.time_last;
+        ev.time_last = tm;
+        if (dt > 0) dt = 0;
+        uint8_t ps = c.ram(0x0e);
+        bool die = ps == 0x0b || c.ram(0xb5) > 1 || ps == 0x06;
+        int64_t r = dx + dt + (die ? -25 : 0);
+        if (r < -15) r = -15;
+        if (r > 15) r = 15;
+        ev.info = smb_info(c);
+        *done = die || ev.info.v[1];
+        if (!*done) skip_busy(render, slot);
+        return (double)r;
+    }
+    // sticky + skip + max-pool + early termination + life loss (fastmario.cpp:336-374). On early
+    // termination the frames that were not rendered are re-emulated from the step-start snapshot.
+    __device__ double agent_step(int act0, bool want_obs, bool* term) {
+        const int K = cfg.skip;
+        const bool mp = cfg.maxpool != 0;
+        uint64_t acts = 0;
+        double total = 0.0;
+        bool done = false;
+        int i;
+        for (i = 0; i < K; i++) {
+            int act = act0;
+            if (cfg.sticky != 0.0) {
+                if (rng) { if (rng->random() < cfg.sticky) act = ev.prev; }
+                else ev.draws++;
+            }
+            ev.prev = act;
+            bool last_frame = i == K - 1, pool_frame = mp && i == K - 2;
+            bool render = want_obs && (last_frame || pool_frame);
+            acts |= (uint64_t)act << (3 * i);
+            total += frame_step(kButtons[act], render, last_frame ? gray0 : gray1, &done);
+            if (done) break;
+        }
+        int last = done ? i : K - 1;
+        if (want_obs && done && last < K - 1) {
+            // the reference re-emulates frame last-1 (+ its hack frames) and frame last from per-frame
+            // snapshots (fastmario.cpp:354-365); the same frames are reached here by replaying the step
+            copy_console(live, snap);
+            c.load(snap.sc, snap.idx);
+            for (int j = 0; j < last; j++) {
+                const bool r = mp && j == last - 1;
+                const uint64_t f0 = ev.frames;
+                const uint32_t i0 = c.instructions, b0 = c.bad_ops;
+                nes_frame(kButtons[(acts >> (3 * j)) & 7], r, gray1);
+                skip_busy(r, gray1);
+                if (!r) {   // count only the frames the reference re-emulates
+                    ev.frames = f0;
+                    c.instructions = i0;
+                    c.bad_ops = b0 | (c.bad_ops & ERR_HACK_LIMIT);
+                }
+            }
+            nes_frame(kButtons[(acts >> (3 * last)) & 7], true, gray0);
+        }
+        if (want_obs) ev.pooled = mp && last >= 1;
+        bool tm = done;
+        int life = (int)ev.info.v[2];
+        if (ev.lives >= 0 && life < ev.lives) tm = true;
+        ev.lives = life;
+        if (ev.info.v[1]) tm = true;
+        *term = tm;
+        return total;
+    }
+};
+
+}  // namespace mh

@@ -1,0 +1,894 @@
+// mario_hip: batched Super Mario Bros env stepping on gfx950 — kernels and the C-ABI (include/mario_hip.h).
+//
+// One agent step of N envs is four launches on the caller's stream:
+//   hipMemcpyAsync  MEM/SC -> SNAP         step-start snapshot (early termination re-renders from it)
+//   k_step          one lane per env: sticky draw, K frames of 6502 + catch-up PPU, reward/done/info,
+//                   hack frames, gray rendering of the observed frame(s) into GRAY (lane-interleaved)
+//   k_obs           one thread per (env, output pixel): 2-frame max + INTER_AREA 256x240 -> 84x84
+//   k_reset         one lane per env: finished envs take a cached (level, no-op count) start state
+//   k_stack         LDS-transposed frame-stack shift, final_obs, reset observation
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/mario_hip.h"
+#include "env_device.hpp"
+
+using namespace mh;
+
+namespace {
+
+constexpr int OBS_PIX = 84 * 84;
+constexpr int TAPS = 6;                  // max area-filter taps per output row / column
+
+// ------------------------------------------------------------------ INTER_AREA tables (host)
+// OpenCV computeResizeAreaTab in double precision (fastmario.cpp:83-100): per output index the
+// source indices and float weights in the order the float sums are taken.
+struct AreaTables {
+    int32_t xs[84 * TAPS], ys[84 * TAPS];
+    float xw[84 * TAPS], yw[84 * TAPS];
+    int32_t xn[84], yn[84];
+};
+
+static void area_taps(int ssize, int dsize, int32_t* idx, float* w, int32_t* cnt) {
+    double scale = 1.0 / ((double)dsize / ssize);
+    for (int d = 0; d < dsize; d++) cnt[d] = 0;
+    auto add = [&](int d, int s, float a) { idx[d * TAPS + cnt[d]] = s; w[d * TAPS + cnt[d]] = a; cnt[d]++; };
+    for (int d = 0; d < dsize; d++) {
+        double f1 = d * scale, f2 = f1 + scale;
+        double cell = scale < ssize - f1 ? scale : ssize - f1;
+        int s1 = (int)std::ceil(f1), s2 = (int)std::floor(f2);
+        if (s2 > ssize - 1) s2 = ssize - 1;
+        if (s1 > s2) s1 = s2;
+        if (s1 - f1 > 1e-3) add(d, s1 - 1, (float)((s1 - f1) / cell));
+        for (int s = s1; s < s2; s++) add(d, s, (float)(1.0 / cell));
+        if (f2 - s2 > 1e-3) {
+            double ww = f2 - s2 < 1.0 ? f2 - s2 : 1.0;
+            if (cell < ww) ww = cell;
+            add(d, s2, (float)(ww / cell));
+        }
+    }
+}
+
+// ------------------------------------------------------------------ device helpers
+struct RomArgs {
+    const uint8_t* rom;      // 0x8000 PRG (mirrored) + 0x2000 CHR, device
+    const uint8_t* lut;      // 256, device
+    uint16_t nt[4];
+};
+
+// Stage PRG + CHR (40 KB) and the gray LUT in LDS; every thread of the block must call this.
+__device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint8_t* s_lut) {
+    const uint4* src = (const uint4*)R.rom;
+    uint4* dst = (uint4*)s_rom;
+    for (int i = threadIdx.x; i < 0xa000 / 16; i += blockDim.x) dst[i] = src[i];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) s_lut[i] = R.lut[i];
+    __syncthreads();
+}
+
+__device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom) {
+    Cart c;
+    c.prg = s_rom;
+    c.chr = s_rom + 0x8000;
+    for (int i = 0; i < 4; i++) c.nt[i] = R.nt[i];
+    return c;
+}
+
+__device__ __forceinline__ uint8_t round_sat(float v) {
+    float r = __builtin_rintf(v);           // round half to even, like lrintf
+    int iv = (int)r;
+    return (uint8_t)(iv < 0 ? 0 : iv > 255 ? 255 : iv);
+}
+
+// INTER_AREA output pixel o of one image. g0/g1: pixel p at g[p * stride]; g1 == nullptr: no max-pool.
+__device__ __forceinline__ uint8_t area_pixel(const uint8_t* g0, const uint8_t* g1, uint32_t stride, int o,
+                                              const AreaTables* T) {
+    const int dy = o / 84, dx = o - dy * 84;
+    const int ny = T->yn[dy], nx = T->xn[dx];
+    float acc = 0.f;
+    for (int j = 0; j < ny; j++) {
+        const int sy = T->ys[dy * TAPS + j];
+        float row = 0.f;
+        for (int k = 0; k < nx; k++) {
+            const uint32_t p = (uint32_t)(sy * 256 + T->xs[dx * TAPS + k]);
+            uint8_t s = g0[(size_t)p * stride];
+            if (g1) { uint8_t s1 = g1[(size_t)p * stride]; s = s1 > s ? s1 : s; }
+            row += (float)s * T->xw[dx * TAPS + k];
+        }
+        const float term = T->yw[dy * TAPS + j] * row;
+        acc = j == 0 ? term : acc + term;
+    }
+    return round_sat(acc);
+}
+
+// ------------------------------------------------------------------ kernels
+struct BootArgs {
+    RomArgs R;
+    int nl;
+    uint32_t nlp;
+    const int* levels;       // 3 * nl
+    uint8_t* mem; uint32_t* sc;  // boot consoles [row * nlp + l]
+    uint8_t* gray;           // [pix * nlp + l]
+    int64_t* x0; int64_t* t0;
+    uint32_t* err;
+};
+
+// Power-on and title sequence with the target level written into RAM (fastmario.cpp:414-445).
+__global__ void __launch_bounds__(64) k_boot(BootArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
+    __shared__ uint8_t s_lut[256];
+    stage_rom(A.R, s_rom, s_lut);
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= A.nl) return;
+    Console c;
+    c.mem = A.mem + l; c.np = A.nlp; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
+    c.gray = A.gray + l; c.render = true; c.bad_ops = 0; c.instructions = 0;
+    c.power_on();
+    auto fr = [&](uint8_t b) { c.joy_buttons[0] = b; c.frame(); };
+    const int w = A.levels[3 * l], s = A.levels[3 * l + 1], ar = A.levels[3 * l + 2];
+    fr(8); fr(0);
+    int guard = 0;
+    while (smb_time(c) == 0) {
+        if (++guard > HACK_FRAME_LIMIT) { atomicOr(A.err, 1u); break; }
+        fr(8);
+        c.st(ROW_RAM + 0x75f, (uint8_t)(w - 1)); c.st(ROW_RAM + 0x75c, (uint8_t)(s - 1));
+        c.st(ROW_RAM + 0x760, (uint8_t)(ar - 1));
+        fr(0);
+        c.st(ROW_RAM + 0x7a0, 0);
+    }
+    int64_t tl = smb_time(c);
+    guard = 0;
+    while (smb_time(c) >= tl) {
+        if (++guard > HACK_FRAME_LIMIT) { atomicOr(A.err, 2u); break; }
+        tl = smb_time(c); fr(8); fr(0);
+    }
+    c.store(A.sc, l);
+    A.x0[l] = smb_x(c);
+    A.t0[l] = smb_time(c);
+}
+
+struct CacheArgs {
+    RomArgs R;
+    Cfg cfg;
+    int nl, nk, nc;
+    uint32_t nlp, ncp;
+    const uint8_t* boot_mem; const uint32_t* boot_sc; const int64_t* x0; const int64_t* t0;
+    uint8_t* mem; uint32_t* sc;          // cache consoles [row * ncp + c]
+    uint8_t* snap_mem; uint32_t* snap_sc;
+    uint8_t* gray;                       // [(slot * GRAY_PIX + pix) * ncp + c]
+    int64_t* cx; int64_t* ct; int32_t* clives; int32_t* cdraws; uint8_t* cboot;
+    uint64_t* cframes; uint64_t* cinstr; uint32_t* cbad;
+};
+
+// Reset cache: the state after k no-op agent steps from the boot state of a level, for k in
+// 0..noop_max (fastmario.cpp:389-401). Restarts on termination exactly like the reference; the
+// sticky draws only decide between action 0 and prev == 0, so their count is recorded, not their values.
+__global__ void __launch_bounds__(64) k_cache(CacheArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
+    __shared__ uint8_t s_lut[256];
+    stage_rom(A.R, s_rom, s_lut);
+    const int ci = blockIdx.x * blockDim.x + threadIdx.x;
+    if (ci >= A.nc) return;
+    const int lvl = ci / A.nk, k = ci - lvl * A.nk;
+    Region boot{(uint8_t*)A.boot_mem, (uint32_t*)A.boot_sc, A.nlp, (uint32_t)lvl};
+    Region live{A.mem, A.sc, A.ncp, (uint32_t)ci};
+    Region snap{A.snap_mem, A.snap_sc, A.ncp, (uint32_t)ci};
+    copy_console(live, boot);
+    Console c;
+    c.mem = A.mem + ci; c.np = A.ncp; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
+    c.bad_ops = 0; c.instructions = 0;
+    c.load(A.sc, ci);
+    EnvRegs ev{};
+    ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
+    ev.prev = 0; ev.lives = -1; ev.shows_boot = true; ev.frames = 0; ev.draws = 0;
+    Stepper stp{c, ev, A.cfg, nullptr, A.gray + ci, A.gray + (size_t)GRAY_PIX * A.ncp + ci, live, snap, false};
+    for (int j = 0; j < k; j++) {
+        const bool want = j == k - 1;
+        if (want) { c.store(A.sc, ci); copy_console(snap, live); }
+        bool term;
+        stp.agent_step(0, want, &term);
+        if (term) {
+            copy_console(live, boot);
+            c.load(A.sc, ci);
+            ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
+            ev.prev = 0; ev.lives = -1; ev.shows_boot = true;
+        }
+    }
+    c.store(A.sc, ci);
+    A.cx[ci] = ev.x_last; A.ct[ci] = ev.time_last; A.clives[ci] = ev.lives;
+    A.cdraws[ci] = (int32_t)ev.draws; A.cboot[ci] = ev.shows_boot;
+    A.cframes[ci] = ev.frames; A.cinstr[ci] = c.instructions; A.cbad[ci] = c.bad_ops;
+}
+
+// Observation of a reset-cache entry or a boot state: the boot observation, or the resized last frame.
+struct SmallObsArgs {
+    const uint8_t* gray; uint32_t stride;     // pixel p of entry i at gray[p * stride + i]
+    const uint8_t* use_boot;                  // per entry (nullable): take boot_obs[level(i)]
+    const uint8_t* boot_obs; int nk;          // boot observations [level * OBS_PIX]
+    uint8_t* out; int count;                  // [i * OBS_PIX + o]
+    const AreaTables* T;
+};
+__global__ void k_small_obs(SmallObsArgs A) {
+    const int i = blockIdx.y;
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= A.count || o >= OBS_PIX) return;
+    uint8_t v;
+    if (A.use_boot && A.use_boot[i]) v = A.boot_obs[(size_t)(i / A.nk) * OBS_PIX + o];
+    else v = area_pixel(A.gray + i, nullptr, A.stride, o, A.T);
+    A.out[(size_t)i * OBS_PIX + o] = v;
+}
+
+struct StepArgs {
+    RomArgs R;
+    Cfg cfg;
+    int n;
+    uint32_t np;
+    uint8_t* mem; uint32_t* sc;
+    uint8_t* snap_mem; uint32_t* snap_sc;
+    uint32_t* ev;                 // env words [w * np + e]
+    uint8_t* gray;                // [(slot * GRAY_PIX + pix) * np + e]
+    const int64_t* actions;
+    float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
+};
+
+__device__ __forceinline__ void load_env(EnvRegs& ev, const uint32_t* E, uint32_t np, uint32_t e) {
+    auto w = [&](int k) { return E[(size_t)k * np + e]; };
+    ev.x_last = (int64_t)((uint64_t)w(E_XLAST_LO) | ((uint64_t)w(E_XLAST_HI) << 32));
+    ev.time_last = (int64_t)((uint64_t)w(E_TLAST_LO) | ((uint64_t)w(E_TLAST_HI) << 32));
+    ev.prev = (int)w(E_PREV); ev.lives = (int)w(E_LIVES); ev.t = (int)w(E_T); ev.ep_len = (int)w(E_EP_LEN);
+    uint64_t r = (uint64_t)w(E_EPRET_LO) | ((uint64_t)w(E_EPRET_HI) << 32);
+    ev.ep_ret = __longlong_as_double((long long)r);
+    ev.shows_boot = w(E_SHOWS_BOOT) != 0; ev.pooled = w(E_POOLED) != 0;
+    ev.frames = 0; ev.draws = 0;
+}
+__device__ __forceinline__ void store_env(const EnvRegs& ev, uint32_t* E, uint32_t np, uint32_t e) {
+    auto w = [&](int k, uint32_t v) { E[(size_t)k * np + e] = v; };
+    w(E_XLAST_LO, (uint32_t)ev.x_last); w(E_XLAST_HI, (uint32_t)((uint64_t)ev.x_last >> 32));
+    w(E_TLAST_LO, (uint32_t)ev.time_last); w(E_TLAST_HI, (uint32_t)((uint64_t)ev.time_last >> 32));
+    w(E_PREV, (uint32_t)ev.prev); w(E_LIVES, (uint32_t)ev.lives); w(E_T, (uint32_t)ev.t);
+    w(E_EP_LEN, (uint32_t)ev.ep_len);
+    uint64_t r = (uint64_t)__double_as_longlong(ev.ep_ret);
+    w(E_EPRET_LO, (uint32_t)r); w(E_EPRET_HI, (uint32_t)(r >> 32));
+    w(E_SHOWS_BOOT, ev.shows_boot); w(E_POOLED, ev.pooled);
+}
+__device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e, int lo_word, uint64_t add) {
+    uint64_t v = (uint64_t)E[(size_t)lo_word * np + e] | ((uint64_t)E[(size_t)(lo_word + 1) * np + e] << 32);
+    v += add;
+    E[(size_t)lo_word * np + e] = (uint32_t)v;
+    E[(size_t)(lo_word + 1) * np + e] = (uint32_t)(v >> 32);
+}
+
+// One agent step of every env (fastmario.cpp:403-411 + 336-374).
+__global__ void __launch_bounds__(64) k_step(StepArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
+    __shared__ uint8_t s_lut[256];
+    stage_rom(A.R, s_rom, s_lut);
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (uint32_t)A.n) return;
+    Console c;
+    c.mem = A.mem + e; c.np = A.np; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
+    c.bad_ops = 0; c.instructions = 0;
+    c.load(A.sc, e);
+    EnvRegs ev;
+    load_env(ev, A.ev, A.np, e);
+    Pcg rng;
+    rng.load(A.ev, A.np, e);
+    int64_t a64 = A.actions[e];
+    const int act = (a64 >= 0 && a64 < 7) ? (int)a64 : 0;
+    Region live{A.mem, A.sc, A.np, e}, snap{A.snap_mem, A.snap_sc, A.np, e};
+    Stepper stp{c, ev, A.cfg, &rng, A.gray + e, A.gray + (size_t)GRAY_PIX * A.np + e, live, snap, true};
+    bool tm;
+    double r = stp.agent_step(act, true, &tm);
+    ev.t++;
+    const bool tr = ev.t >= A.cfg.max_steps;
+    ev.ep_ret += r; ev.ep_len++;
+    A.rew[e] = (float)r;
+    A.term[e] = tm;
+    A.trunc[e] = tr;
+    for (int k = 0; k < 10; k++) A.info[(size_t)e * 10 + k] = (int32_t)ev.info.v[k];
+    const bool done = tm || tr;
+    if (done) { A.ep_ret_out[e] = ev.ep_ret; A.ep_len_out[e] = ev.ep_len; }
+    c.store(A.sc, e);
+    store_env(ev, A.ev, A.np, e);
+    rng.store(A.ev, A.np, e);
+    A.ev[(size_t)E_DONE * A.np + e] = done;
+    add_counter(A.ev, A.np, e, E_FRAMES_LO, ev.frames);
+    add_counter(A.ev, A.np, e, E_INSTR_LO, c.instructions);
+    A.ev[(size_t)E_BAD * A.np + e] += c.bad_ops;
+}
+
+struct ObsArgs {
+    int n; uint32_t np;
+    const uint32_t* ev;
+    const uint8_t* gray;          // [(slot * GRAY_PIX + pix) * np + e]
+    const uint8_t* boot_obs;      // [level * OBS_PIX + o]
+    uint8_t* out;                 // [o * np + e]
+    const AreaTables* T;
+};
+// New observation of every env: boot observation right after a reset, else INTER_AREA of the last
+// frame, max-pooled with its partner frame (fastmario.cpp:377-386). Threads: x = env, y = pixel.
+__global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
+    const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int o = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (e >= (uint32_t)A.n || o >= OBS_PIX) return;
+    uint8_t v;
+    if (A.ev[(size_t)E_SHOWS_BOOT * A.np + e]) {
+        v = A.boot_obs[(size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + o];
+    } else {
+        const bool pool = A.ev[(size_t)E_POOLED * A.np + e] != 0;
+        v = area_pixel(A.gray + e, pool ? A.gray + (size_t)GRAY_PIX * A.np + e : nullptr, A.np, o, A.T);
+    }
+    A.out[(size_t)o * A.np + e] = v;
+}
+
+struct ResetArgs {
+    int n; uint32_t np;
+    Cfg cfg;
+    int nk; uint32_t ncp;
+    uint8_t* mem; uint32_t* sc; uint32_t* ev;
+    const uint8_t* cmem; const uint32_t* csc;
+    const int64_t* cx; const int64_t* ct; const int32_t* clives; const int32_t* cdraws; const uint8_t* cboot;
+    const uint64_t* cframes; const uint64_t* cinstr; const uint32_t* cbad;
+    int all;
+};
+// Auto-reset (fastmario.cpp:389-401): k = integers(noop_max + 1) from the env's stream, the draws the
+// k no-op steps would take are skipped, and the cached state of (level, k) is installed.
+__global__ void __launch_bounds__(64) k_reset(ResetArgs A) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (uint32_t)A.n) return;
+    uint32_t* E = A.ev;
+    const size_t np = A.np;
+    if (!A.all && !E[E_DONE * np + e]) { E[E_RESET_IDX * np + e] = 0xffffffffu; return; }
+    Pcg rng;
+    rng.load(E, A.np, e);
+    int k = 0;
+    if (A.cfg.noop_max) k = (int)rng.integers(A.cfg.noop_max + 1);
+    const int lvl = (int)E[E_LEVEL * np + e];
+    const int ci = lvl * A.nk + k;
+    if (A.cfg.sticky != 0.0)
+        for (int d = 0; d < A.cdraws[ci]; d++) rng.next64();
+    rng.store(E, A.np, e);
+    Region dst{A.mem, A.sc, A.np, e}, src{(uint8_t*)A.cmem, (uint32_t*)A.csc, A.ncp, (uint32_t)ci};
+    copy_console(dst, src);
+    EnvRegs ev{};
+    ev.x_last = A.cx[ci]; ev.time_last = A.ct[ci]; ev.lives = A.clives[ci]; ev.prev = 0;
+    ev.t = 0; ev.ep_len = 0; ev.ep_ret = 0.0; ev.shows_boot = A.cboot[ci] != 0; ev.pooled = false;
+    store_env(ev, E, A.np, e);
+    E[E_RESET_IDX * np + e] = (uint32_t)ci;
+    // the no-op steps count as emulated work, as on the reference CPU path
+    add_counter(E, A.np, e, E_FRAMES_LO, A.cframes[ci]);
+    add_counter(E, A.np, e, E_INSTR_LO, A.cinstr[ci]);
+    E[E_BAD * np + e] += A.cbad[ci];
+}
+
+struct StackArgs {
+    int n; uint32_t np; int K;
+    uint8_t* obs; uint8_t* fin;   // [e][K][OBS_PIX]
+    const uint8_t* fresh;         // [o * np + e]
+    const uint32_t* ev;
+    const uint8_t* cobs;          // [ci * OBS_PIX + o]
+    int mode;                     // 0 step, 1 reset
+};
+// Frame stack, final_obs, reset observation (fastmario.cpp:477-504). Block: 64 envs x 64 words of
+// one frame; the fresh frame is read lane-interleaved and transposed through LDS.
+__global__ void __launch_bounds__(256) k_stack(StackArgs A) {
+    __shared__ uint32_t tile[64][65];
+    const uint32_t e0 = blockIdx.y * 64;
+    const int w0 = blockIdx.x * 64;             // word index within a frame (OBS_PIX / 4 = 1764 words)
+    const int nw = OBS_PIX / 4;
+    // fresh bytes: 256 byte rows (4 per word) x 64 envs
+    if (A.mode == 0) {
+        for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
+            const int wl = idx >> 6, j = idx & 63;
+            const uint32_t e = e0 + j;
+            uint32_t val = 0;
+            if (w0 + wl < nw && e < (uint32_t)A.n)
+                for (int b = 0; b < 4; b++)
+                    val |= (uint32_t)A.fresh[(size_t)(4 * (w0 + wl) + b) * A.np + e] << (8 * b);
+            tile[wl][j] = val;
+        }
+    }
+    __syncthreads();
+    const size_t fw = (size_t)OBS_PIX / 4 * A.K;   // words per env stack
+    for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
+        const int j = idx >> 6, wl = idx & 63;
+        const uint32_t e = e0 + j;
+        const int w = w0 + wl;
+        if (w >= nw || e >= (uint32_t)A.n) continue;
+        uint32_t* st = (uint32_t*)A.obs + e * fw;
+        const uint32_t ri = A.ev[(size_t)E_RESET_IDX * A.np + e];
+        if (A.mode == 1) {
+            for (int s = 0; s < A.K - 1; s++) st[(size_t)s * nw + w] = 0;
+            st[(size_t)(A.K - 1) * nw + w] = ((const uint32_t*)A.cobs)[(size_t)ri * nw + w];
+            continue;
+        }
+        const uint32_t fresh = tile[wl][j];
+        if (ri != 0xffffffffu) {
+            uint32_t* fo = (uint32_t*)A.fin + e * fw;
+            for (int s = 0; s < A.K - 1; s++) { fo[(size_t)s * nw + w] = st[(size_t)(s + 1) * nw + w]; st[(size_t)s * nw + w] = 0; }
+            fo[(size_t)(A.K - 1) * nw + w] = fresh;
+            st[(size_t)(A.K - 1) * nw + w] = ((const uint32_t*)A.cobs)[(size_t)ri * nw + w];
+        } else {
+            for (int s = 0; s < A.K - 1; s++) st[(size_t)s * nw + w] = st[(size_t)(s + 1) * nw + w];
+            st[(size_t)(A.K - 1) * nw + w] = fresh;
+        }
+    }
+}
+
+// Canonical state dump (layout in include/mario_hip.h): one thread per console.
+__global__ void k_canon(const uint8_t* mem, const uint32_t* sc, uint32_t np, int n, uint8_t* out) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (uint32_t)n) return;
+    uint8_t* o = out + (size_t)e * MH_CANON_BYTES;
+    auto w = [&](int k) { return sc[(size_t)k * np + e]; };
+    auto put = [&](int off, uint64_t v, int bytes) { for (int b = 0; b < bytes; b++) o[off + b] = (uint8_t)(v >> (8 * b)); };
+    for (int i = 0; i < 80; i++) o[i] = 0;
+    const uint64_t iter = (uint64_t)w(S_ITER_LO) | ((uint64_t)w(S_ITER_HI) << 32);
+    put(0, iter, 8);
+    put(8, iter + (int64_t)(int32_t)w(S_EXEC_REL), 8);
+    put(16, 3 * iter, 8);
+    put(24, w(S_PCYC), 4); put(28, w(S_SCANLINE), 4);
+    put(32, w(S_PC), 2); put(34, w(S_V), 2); put(36, w(S_T), 2); put(38, w(S_INC), 2);
+    const int order[] = {S_SP, S_A, S_X, S_Y, S_P, S_ZERO_SKIP, S_JOY_STROBE0, S_JOY_STROBE1, S_JOY_BUTTONS0,
+                         S_JOY_BUTTONS1, S_JOY_BITS0, S_JOY_BITS1, S_PSTATE, S_EVEN, S_VBLANK, S_S0HIT,
+                         S_FIRST_WRITE, S_DATA_BUFFER, S_OAM_ADDR, S_FINE_X, S_SHOW_BG, S_SHOW_SPR,
+                         S_HIDE_EDGE_BG, S_HIDE_EDGE_SPR, S_LONG_SPR, S_NMI_EN, S_BG_PAGE, S_SPR_PAGE, S_NSL};
+    for (int i = 0; i < 29; i++) o[40 + i] = (uint8_t)w(order[i]);
+    const uint32_t nsl = w(S_NSL);
+    const uint64_t sl = (uint64_t)w(S_SL_LO) | ((uint64_t)w(S_SL_HI) << 32);
+    for (uint32_t i = 0; i < 8; i++) o[69 + i] = i < nsl ? (uint8_t)(sl >> (8 * i)) : 0;
+    const uint32_t rows[4][3] = {{80, ROW_OAM, 256}, {336, ROW_PAL, 32}, {368, ROW_VRAM, 2048}, {2416, ROW_RAM, 2048}};
+    for (int k = 0; k < 4; k++)
+        for (uint32_t i = 0; i < rows[k][2]; i++) o[rows[k][0] + i] = mem[(size_t)(rows[k][1] + i) * np + e];
+}
+
+// RAM of every console, env-major (n x 2048). Threads: x = env, y = address.
+__global__ void k_ram_out(const uint8_t* mem, uint32_t np, int n, uint8_t* out) {
+    const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
+    const uint32_t ad = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (e >= (uint32_t)n || ad >= 2048) return;
+    out[(size_t)e * 2048 + ad] = mem[(size_t)(ROW_RAM + ad) * np + e];
+}
+
+struct RawArgs {
+    RomArgs R;
+    int n; uint32_t np;
+    uint8_t* mem; uint32_t* sc;
+    uint8_t* screen;             // [pix * np + e], palette values
+    const uint8_t* buttons;      // n
+    int render;
+    uint32_t* bad; uint32_t* instr;   // per env accumulators
+    int power_on;
+};
+// One nes-py frame of every raw console (fastmario.cpp:656-661); power_on != 0 boots them instead.
+__global__ void __launch_bounds__(64) k_raw(RawArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
+    __shared__ uint8_t s_lut[256];
+    stage_rom(A.R, s_rom, s_lut);
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (uint32_t)A.n) return;
+    Console c;
+    c.mem = A.mem + e; c.np = A.np; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
+    c.gray = A.screen + e; c.bad_ops = 0; c.instructions = 0;
+    if (A.power_on) {
+        c.power_on();
+    } else {
+        c.load(A.sc, e);
+        c.joy_buttons[0] = A.buttons[e];
+        c.render = A.render != 0;
+        c.frame();
+    }
+    c.store(A.sc, e);
+    A.bad[e] += c.bad_ops;
+    A.instr[e] += c.instructions;
+}
+
+// 240x256 gray images (env-major) -> 84x84.
+__global__ void k_resize_images(const uint8_t* src, uint8_t* dst, int n, const AreaTables* T) {
+    const int i = blockIdx.y;
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n || o >= OBS_PIX) return;
+    dst[(size_t)i * OBS_PIX + o] = area_pixel(src + (size_t)i * GRAY_PIX, nullptr, 1, o, T);
+}
+
+// ------------------------------------------------------------------ host side
+thread_local std::string g_err;
+
+static bool ok(hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    return false;
+}
+#define CK(expr) do { if (!ok((expr), #expr)) return -1; } while (0)
+#define CKN(expr) do { if (!ok((expr), #expr)) { return nullptr; } } while (0)
+
+static uint32_t pad64(int n) { return (uint32_t)((n + 63) / 64 * 64); }
+
+struct DevBufs {
+    std::vector<void*> ptrs;
+    template <class T> T* alloc(size_t count, bool& good) {
+        void* p = nullptr;
+        if (hipMalloc(&p, count * sizeof(T) + 16) != hipSuccess) { good = false; g_err = "hipMalloc failed"; return nullptr; }
+        if (hipMemset(p, 0, count * sizeof(T) + 16) != hipSuccess) { good = false; g_err = "hipMemset failed"; }
+        ptrs.push_back(p);
+        return (T*)p;
+    }
+    ~DevBufs() { for (void* p : ptrs) (void)hipFree(p); }
+};
+
+// iNES NROM image -> 0x8000 PRG (16 KB mirrored) + 0x2000 CHR and name-table offsets (nes_core.hpp:66-87).
+static bool load_cart(const uint8_t* d, int64_t n, std::vector<uint8_t>& img, uint16_t nt[4]) {
+    if (!d || n < 16 || d[0] != 'N' || d[1] != 'E' || d[2] != 'S' || d[3] != 0x1a) { g_err = "not an iNES image"; return false; }
+    int mapper = ((d[6] >> 4) & 0xf) | (d[7] & 0xf0);
+    if (mapper != 0 || (d[6] & 0x6)) { g_err = "unsupported ROM (mapper / PRG-RAM / trainer)"; return false; }
+    int banks = d[4];
+    if (banks < 1 || banks > 2 || d[5] != 1) { g_err = "unsupported ROM (PRG/CHR size)"; return false; }
+    if (n < 16 + 0x4000LL * banks + 0x2000) { g_err = "truncated ROM"; return false; }
+    img.assign(0xa000, 0);
+    for (int i = 0; i < 0x8000; i++) img[i] = d[16 + (i % (0x4000 * banks))];
+    memcpy(img.data() + 0x8000, d + 16 + 0x4000 * banks, 0x2000);
+    switch (d[6] & 0xB) {
+        case 0: nt[0] = 0; nt[1] = 0; nt[2] = 0x400; nt[3] = 0x400; break;
+        case 1: nt[0] = 0; nt[1] = 0x400; nt[2] = 0; nt[3] = 0x400; break;
+        default: nt[0] = nt[1] = nt[2] = nt[3] = 0; break;
+    }
+    return true;
+}
+
+}  // namespace
+
+struct MhEnv {
+    int n = 0, K = 4, nl = 0, nk = 1, nc = 0, device = 0;
+    uint32_t np = 0, nlp = 0, ncp = 0;
+    Cfg cfg{};
+    DevBufs B;
+    RomArgs R{};
+    AreaTables* T = nullptr;
+    uint8_t *mem = nullptr, *snap_mem = nullptr, *gray = nullptr, *fresh = nullptr;
+    uint32_t *sc = nullptr, *snap_sc = nullptr, *ev = nullptr;
+    uint8_t *boot_mem = nullptr, *boot_gray = nullptr, *boot_obs = nullptr;
+    uint32_t* boot_sc = nullptr;
+    int64_t *x0 = nullptr, *t0 = nullptr;
+    uint8_t *cmem = nullptr, *csnap_mem = nullptr, *cgray = nullptr, *cobs = nullptr, *cboot = nullptr;
+    uint32_t *csc = nullptr, *csnap_sc = nullptr;
+    int64_t *cx = nullptr, *ct = nullptr;
+    int32_t *clives = nullptr, *cdraws = nullptr;
+    uint64_t *cframes = nullptr, *cinstr = nullptr;
+    uint32_t* cbad = nullptr;
+    uint8_t *obs = nullptr, *fin = nullptr, *term = nullptr, *trunc = nullptr;
+    float* rew = nullptr;
+    int32_t *info = nullptr, *ep_len = nullptr;
+    double* ep_ret = nullptr;
+};
+
+struct MhRaw {
+    int n = 0, device = 0;
+    uint32_t np = 0;
+    DevBufs B;
+    RomArgs R{};
+    uint8_t *mem = nullptr, *screen = nullptr, *bk_mem = nullptr;
+    uint32_t *sc = nullptr, *bk_sc = nullptr, *bad = nullptr, *instr = nullptr;
+};
+
+extern "C" {
+
+const char* mh_last_error(void) { return g_err.c_str(); }
+
+MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, const uint8_t* lut,
+                 int skip, int max_steps, double sticky, int noop_max, int maxpool, int frame_stack,
+                 const uint64_t* rng, int device) {
+    g_err.clear();
+    if (n < 1 || skip < 1 || skip > MAX_SKIP || frame_stack < 1 || frame_stack > 16 || noop_max < 0 ||
+        max_steps < 1 || !(sticky >= 0.0 && sticky <= 1.0) || !levels || !lut || !rng) {
+        g_err = "invalid arguments";
+        return nullptr;
+    }
+    std::vector<uint8_t> img;
+    uint16_t nt[4];
+    if (!load_cart(rom, rom_len, img, nt)) return nullptr;
+    CKN(hipSetDevice(device));
+    MhEnv* h = new MhEnv();
+    bool good = true;
+    h->n = n; h->K = frame_stack; h->device = device; h->np = pad64(n);
+    h->cfg = Cfg{skip, max_steps, noop_max, maxpool ? 1 : 0, sticky};
+    // distinct levels in order of first appearance (fastmario.cpp:584-593)
+    std::vector<int> lv, env_level(n);
+    for (int i = 0; i < n; i++) {
+        int li = -1;
+        for (size_t k = 0; k < lv.size() / 3; k++)
+            if (lv[3 * k] == levels[3 * i] && lv[3 * k + 1] == levels[3 * i + 1] && lv[3 * k + 2] == levels[3 * i + 2]) li = (int)k;
+        if (li < 0) { li = (int)lv.size() / 3; lv.insert(lv.end(), levels + 3 * i, levels + 3 * i + 3); }
+        env_level[i] = li;
+    }
+    h->nl = (int)lv.size() / 3; h->nlp = pad64(h->nl);
+    h->nk = noop_max + 1; h->nc = h->nl * h->nk; h->ncp = pad64(h->nc);
+    auto& B = h->B;
+    uint8_t* d_rom = B.alloc<uint8_t>(0xa000, good);
+    uint8_t* d_lut = B.alloc<uint8_t>(256, good);
+    h->T = B.alloc<AreaTables>(1, good);
+    int* d_levels = B.alloc<int>(lv.size(), good);
+    h->mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
+    h->snap_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
+    h->sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
+    h->snap_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
+    h->ev = B.alloc<uint32_t>((size_t)E_COUNT * h->np, good);
+    h->gray = B.alloc<uint8_t>((size_t)2 * GRAY_PIX * h->np, good);
+    h->fresh = B.alloc<uint8_t>((size_t)OBS_PIX * h->np, good);
+    h->boot_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->nlp, good);
+    h->boot_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->nlp, good);
+    h->boot_gray = B.alloc<uint8_t>((size_t)GRAY_PIX * h->nlp, good);
+    h->boot_obs = B.alloc<uint8_t>((size_t)OBS_PIX * h->nl, good);
+    h->x0 = B.alloc<int64_t>(h->nl, good); h->t0 = B.alloc<int64_t>(h->nl, good);
+    h->cmem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->ncp, good);
+    h->csc = B.alloc<uint32_t>((size_t)S_COUNT * h->ncp, good);
+    h->csnap_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->ncp, good);
+    h->csnap_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->ncp, good);
+    h->cgray = B.alloc<uint8_t>((size_t)2 * GRAY_PIX * h->ncp, good);
+    h->cobs = B.alloc<uint8_t>((size_t)OBS_PIX * h->nc, good);
+    h->cboot = B.alloc<uint8_t>(h->nc, good);
+    h->cx = B.alloc<int64_t>(h->nc, good); h->ct = B.alloc<int64_t>(h->nc, good);
+    h->clives = B.alloc<int32_t>(h->nc, good); h->cdraws = B.alloc<int32_t>(h->nc, good);
+    h->cframes = B.alloc<uint64_t>(h->nc, good); h->cinstr = B.alloc<uint64_t>(h->nc, good);
+    h->cbad = B.alloc<uint32_t>(h->nc, good);
+    uint32_t* d_err = B.alloc<uint32_t>(1, good);
+    if (!good) { delete h; return nullptr; }
+    // tables
+    AreaTables T;
+    memset(&T, 0, sizeof(T));
+    area_taps(256, 84, T.xs, T.xw, T.xn);
+    area_taps(240, 84, T.ys, T.yw, T.yn);
+    // per-env words: level, RNG, lives = -1 (reset() installs the real start state)
+    std::vector<uint32_t> ev((size_t)E_COUNT * h->np, 0);
+    for (int i = 0; i < n; i++) {
+        auto w = [&](int k) -> uint32_t& { return ev[(size_t)k * h->np + i]; };
+        w(E_LEVEL) = (uint32_t)env_level[i];
+        const uint64_t* r = rng + 6 * i;
+        w(E_RNG_S3) = (uint32_t)(r[0] >> 32); w(E_RNG_S2) = (uint32_t)r[0];
+        w(E_RNG_S1) = (uint32_t)(r[1] >> 32); w(E_RNG_S0) = (uint32_t)r[1];
+        w(E_RNG_I3) = (uint32_t)(r[2] >> 32); w(E_RNG_I2) = (uint32_t)r[2];
+        w(E_RNG_I1) = (uint32_t)(r[3] >> 32); w(E_RNG_I0) = (uint32_t)r[3];
+        w(E_RNG_HAS32) = (uint32_t)r[4]; w(E_RNG_HALF) = (uint32_t)r[5];
+        w(E_LIVES) = 0xffffffffu; w(E_SHOWS_BOOT) = 1; w(E_RESET_IDX) = 0xffffffffu;
+    }
+    auto fail = [&]() -> MhEnv* { delete h; return nullptr; };
+    if (!ok(hipMemcpy(d_rom, img.data(), 0xa000, hipMemcpyHostToDevice), "upload rom") ||
+        !ok(hipMemcpy(d_lut, lut, 256, hipMemcpyHostToDevice), "upload lut") ||
+        !ok(hipMemcpy(h->T, &T, sizeof(T), hipMemcpyHostToDevice), "upload tables") ||
+        !ok(hipMemcpy(d_levels, lv.data(), lv.size() * sizeof(int), hipMemcpyHostToDevice), "upload levels") ||
+        !ok(hipMemcpy(h->ev, ev.data(), ev.size() * 4, hipMemcpyHostToDevice), "upload env words"))
+        return fail();
+    h->R.rom = d_rom; h->R.lut = d_lut;
+    for (int i = 0; i < 4; i++) h->R.nt[i] = nt[i];
+    // boot every level, build the reset cache
+    BootArgs ba{h->R, h->nl, h->nlp, d_levels, h->boot_mem, h->boot_sc, h->boot_gray, h->x0, h->t0, d_err};
+    hipLaunchKernelGGL(k_boot, dim3((h->nl + 63) / 64), dim3(64), 0, 0, ba);
+    if (!ok(hipGetLastError(), "k_boot launch")) return fail();
+    SmallObsArgs so{h->boot_gray, h->nlp, nullptr, nullptr, 1, h->boot_obs, h->nl, h->T};
+    hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nl), dim3(256), 0, 0, so);
+    CacheArgs ca{h->R, h->cfg, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
+                 h->cmem, h->csc, h->csnap_mem, h->csnap_sc, h->cgray, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
+                 h->cframes, h->cinstr, h->cbad};
+    hipLaunchKernelGGL(k_cache, dim3((h->nc + 63) / 64), dim3(64), 0, 0, ca);
+    if (!ok(hipGetLastError(), "k_cache launch")) return fail();
+    SmallObsArgs co{h->cgray, h->ncp, h->cboot, h->boot_obs, h->nk, h->cobs, h->nc, h->T};
+    hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nc), dim3(256), 0, 0, co);
+    if (!ok(hipDeviceSynchronize(), "boot / reset cache")) return fail();
+    uint32_t err = 0;
+    if (!ok(hipMemcpy(&err, d_err, 4, hipMemcpyDeviceToHost), "boot status")) return fail();
+    if (err) { g_err = "level boot did not finish (the ROM never started a level)"; return fail(); }
+    return h;
+}
+
+int mh_set_buffers(MhEnv* h, uint8_t* obs, uint8_t* fin, float* rew, uint8_t* term, uint8_t* trunc,
+                   int32_t* info, double* ep_ret, int32_t* ep_len) {
+    if (!h || !obs || !fin || !rew || !term || !trunc || !info || !ep_ret || !ep_len) { g_err = "null buffer"; return -1; }
+    h->obs = obs; h->fin = fin; h->rew = rew; h->term = term; h->trunc = trunc; h->info = info;
+    h->ep_ret = ep_ret; h->ep_len = ep_len;
+    return 0;
+}
+
+static int launch_reset_and_stack(MhEnv* h, hipStream_t s, int all) {
+    ResetArgs ra{h->n, h->np, h->cfg, h->nk, h->ncp, h->mem, h->sc, h->ev, h->cmem, h->csc, h->cx, h->ct,
+                 h->clives, h->cdraws, h->cboot, h->cframes, h->cinstr, h->cbad, all};
+    hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, ra);
+    CK(hipGetLastError());
+    StackArgs sa{h->n, h->np, h->K, h->obs, h->fin, h->fresh, h->ev, h->cobs, all};
+    hipLaunchKernelGGL(k_stack, dim3((OBS_PIX / 4 + 63) / 64, h->np / 64), dim3(256), 0, s, sa);
+    CK(hipGetLastError());
+    return 0;
+}
+
+int mh_reset(MhEnv* h, void* stream) {
+    if (!h || !h->obs) { g_err = "buffers not set"; return -1; }
+    CK(hipSetDevice(h->device));
+    return launch_reset_and_stack(h, (hipStream_t)stream, 1);
+}
+
+int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
+    if (!h || !h->obs || !d_actions) { g_err = "buffers or actions not set"; return -1; }
+    CK(hipSetDevice(h->device));
+    hipStream_t s = (hipStream_t)stream;
+    CK(hipMemcpyAsync(h->snap_mem, h->mem, (size_t)MEM_ROWS * h->np, hipMemcpyDeviceToDevice, s));
+    CK(hipMemcpyAsync(h->snap_sc, h->sc, (size_t)S_COUNT * h->np * 4, hipMemcpyDeviceToDevice, s));
+    StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->snap_mem, h->snap_sc, h->ev, h->gray, d_actions,
+                h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len};
+    hipLaunchKernelGGL(k_step, dim3(h->np / 64), dim3(64), 0, s, sa);
+    CK(hipGetLastError());
+    ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
+    hipLaunchKernelGGL(k_obs, dim3(h->np / 64, OBS_PIX / 4), dim3(256), 0, s, oa);
+    CK(hipGetLastError());
+    return launch_reset_and_stack(h, s, 0);
+}
+
+int mh_step_wait(MhEnv* h, void* stream) {
+    if (!h) return -1;
+    CK(hipStreamSynchronize((hipStream_t)stream));
+    return 0;
+}
+
+void mh_destroy(MhEnv* h) {
+    if (!h) return;
+    (void)hipSetDevice(h->device);
+    (void)hipDeviceSynchronize();
+    delete h;
+}
+
+static int64_t sum_words(const MhEnv* h, int lo_word, bool wide) {
+    std::vector<uint32_t> lo(h->np), hi(h->np, 0);
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    if (hipMemcpy(lo.data(), h->ev + (size_t)lo_word * h->np, h->np * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if (wide && hipMemcpy(hi.data(), h->ev + (size_t)(lo_word + 1) * h->np, h->np * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    int64_t s = 0;
+    for (int i = 0; i < h->n; i++) s += (int64_t)(lo[i] | ((uint64_t)hi[i] << 32));
+    return s;
+}
+int64_t mh_frames(MhEnv* h) { return h ? sum_words(h, E_FRAMES_LO, true) : -1; }
+int64_t mh_bad_ops(MhEnv* h) { return h ? sum_words(h, E_BAD, false) : -1; }
+int64_t mh_instructions(MhEnv* h) { return h ? sum_words(h, E_INSTR_LO, true) : -1; }
+
+int mh_env_ram(MhEnv* h, uint8_t* d_out, void* stream) {
+    if (!h || !d_out) return -1;
+    hipLaunchKernelGGL(k_ram_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n, d_out);
+    CK(hipGetLastError());
+    return 0;
+}
+int mh_env_canon(MhEnv* h, uint8_t* d_out, void* stream) {
+    if (!h || !d_out) return -1;
+    hipLaunchKernelGGL(k_canon, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, h->mem, h->sc, h->np, h->n, d_out);
+    CK(hipGetLastError());
+    return 0;
+}
+int mh_level_canon(MhEnv* h, uint8_t* d_out, void* stream) {
+    if (!h || !d_out) return -1;
+    hipLaunchKernelGGL(k_canon, dim3(h->nlp / 64), dim3(64), 0, (hipStream_t)stream, h->boot_mem, h->boot_sc, h->nlp, h->nl, d_out);
+    CK(hipGetLastError());
+    return 0;
+}
+int mh_level_obs(MhEnv* h, uint8_t* d_out, void* stream) {
+    if (!h || !d_out) return -1;
+    CK(hipMemcpyAsync(d_out, h->boot_obs, (size_t)OBS_PIX * h->nl, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return 0;
+}
+int mh_num_levels(MhEnv* h) { return h ? h->nl : -1; }
+
+int64_t mh_state_bytes(void) { return (int64_t)MEM_ROWS + 4LL * S_COUNT; }
+int64_t mh_env_bytes(MhEnv* h) {
+    if (!h) return -1;
+    int64_t per = 2 * (MEM_ROWS + 4LL * S_COUNT) + 4LL * E_COUNT + 2LL * GRAY_PIX + OBS_PIX;
+    return per * h->np / h->n;
+}
+
+MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
+    g_err.clear();
+    if (n < 1) { g_err = "invalid arguments"; return nullptr; }
+    std::vector<uint8_t> img;
+    uint16_t nt[4];
+    if (!load_cart(rom, rom_len, img, nt)) return nullptr;
+    CKN(hipSetDevice(device));
+    MhRaw* h = new MhRaw();
+    bool good = true;
+    h->n = n; h->np = pad64(n); h->device = device;
+    auto& B = h->B;
+    uint8_t* d_rom = B.alloc<uint8_t>(0xa000, good);
+    uint8_t* d_lut = B.alloc<uint8_t>(256, good);
+    h->mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
+    h->bk_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
+    h->sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
+    h->bk_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
+    h->screen = B.alloc<uint8_t>((size_t)GRAY_PIX * h->np, good);
+    h->bad = B.alloc<uint32_t>(h->np, good);
+    h->instr = B.alloc<uint32_t>(h->np, good);
+    if (!good) { delete h; return nullptr; }
+    uint8_t ident[256];
+    for (int i = 0; i < 256; i++) ident[i] = (uint8_t)i;
+    if (!ok(hipMemcpy(d_rom, img.data(), 0xa000, hipMemcpyHostToDevice), "upload rom") ||
+        !ok(hipMemcpy(d_lut, ident, 256, hipMemcpyHostToDevice), "upload lut")) { delete h; return nullptr; }
+    h->R.rom = d_rom; h->R.lut = d_lut;
+    for (int i = 0; i < 4; i++) h->R.nt[i] = nt[i];
+    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, 1};
+    hipLaunchKernelGGL(k_raw, dim3(h->np / 64), dim3(64), 0, 0, ra);
+    if (!ok(hipDeviceSynchronize(), "raw power-on")) { delete h; return nullptr; }
+    return h;
+}
+int mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream) {
+    if (!h || !d_buttons) return -1;
+    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, d_buttons, render, h->bad, h->instr, 0};
+    hipLaunchKernelGGL(k_raw, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, ra);
+    CK(hipGetLastError());
+    return 0;
+}
+int mh_raw_ram(MhRaw* h, uint8_t* d_out, void* stream) {
+    if (!h || !d_out) return -1;
+    hipLaunchKernelGGL(k_ram_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n, d_out);
+    CK(hipGetLastError());
+    return 0;
+}
+// screen rows are lane-interleaved; reuse the RAM transpose row by row block
+__global__ void k_screen_out(const uint8_t* scr, uint32_t np, int n, uint8_t* out) {
+    const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
+    const uint32_t p = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (e >= (uint32_t)n || p >= (uint32_t)GRAY_PIX) return;
+    out[(size_t)e * GRAY_PIX + p] = scr[(size_t)p * np + e];
+}
+int mh_raw_screen(MhRaw* h, uint8_t* d_out, void* stream) {
+    if (!h || !d_out) return -1;
+    hipLaunchKernelGGL(k_screen_out, dim3(h->np / 64, GRAY_PIX / 4), dim3(256), 0, (hipStream_t)stream, h->screen, h->np, h->n, d_out);
+    CK(hipGetLastError());
+    return 0;
+}
+int mh_raw_canon(MhRaw* h, uint8_t* d_out, void* stream) {
+    if (!h || !d_out) return -1;
+    hipLaunchKernelGGL(k_canon, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, h->mem, h->sc, h->np, h->n, d_out);
+    CK(hipGetLastError());
+    return 0;
+}
+int mh_raw_backup(MhRaw* h, void* stream) {
+    if (!h) return -1;
+    CK(hipMemcpyAsync(h->bk_mem, h->mem, (size_t)MEM_ROWS * h->np, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    CK(hipMemcpyAsync(h->bk_sc, h->sc, (size_t)S_COUNT * h->np * 4, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return 0;
+}
+int mh_raw_restore(MhRaw* h, void* stream) {
+    if (!h) return -1;
+    CK(hipMemcpyAsync(h->mem, h->bk_mem, (size_t)MEM_ROWS * h->np, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    CK(hipMemcpyAsync(h->sc, h->bk_sc, (size_t)S_COUNT * h->np * 4, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return 0;
+}
+static int64_t raw_sum(MhRaw* h, uint32_t* d) {
+    std::vector<uint32_t> v(h->np);
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    if (hipMemcpy(v.data(), d, h->np * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    int64_t s = 0;
+    for (int i = 0; i < h->n; i++) s += v[i];
+    return s;
+}
+int64_t mh_raw_bad_ops(MhRaw* h) { return h ? raw_sum(h, h->bad) : -1; }
+int64_t mh_raw_instructions(MhRaw* h) { return h ? raw_sum(h, h->instr) : -1; }
+void mh_raw_destroy(MhRaw* h) {
+    if (!h) return;
+    (void)hipSetDevice(h->device);
+    (void)hipDeviceSynchronize();
+    delete h;
+}
+
+int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
+    if (!d_src || !d_dst || n < 1) { g_err = "invalid arguments"; return -1; }
+    static AreaTables* d_T = nullptr;
+    if (!d_T) {
+        AreaTables T;
+        memset(&T, 0, sizeof(T));
+        area_taps(256, 84, T.xs, T.xw, T.xn);
+        area_taps(240, 84, T.ys, T.yw, T.yn);
+        CK(hipMalloc(&d_T, sizeof(T)));
+        CK(hipMemcpy(d_T, &T, sizeof(T), hipMemcpyHostToDevice));
+    }
+    hipLaunchKernelGGL(k_resize_images, dim3((OBS_PIX + 255) / 256, n), dim3(256), 0, (hipStream_t)stream, d_src, d_dst, n, d_T);
+    CK(hipGetLastError());
+    return 0;
+}
+
+}  // extern "C"

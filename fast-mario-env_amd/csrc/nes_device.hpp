@@ -1,0 +1,663 @@
+// Device-side NES console for gfx950: one env per lane.
+//
+// Layout in HBM (all lane-interleaved, NP = env count rounded up to a multiple of 64):
+//   MEM[row * NP + e]  one byte per row: RAM 0..2047, VRAM 2048..4095, OAM 4096..4351, PAL 4352..4383.
+//                      Lanes that touch the same emulated address touch one contiguous 64-byte run.
+//   SC[word * NP + e]  32-bit scalar registers of the CPU / PPU / joypads (enum Scalar).
+// PRG (32 KB) and CHR (8 KB) are read-only and shared by every env: each workgroup stages them in LDS.
+//
+// The machine follows the reference's nes-py-exact model (csrc/nes_core.hpp): instruction-atomic CPU
+// with skip cycles, catch-up PPU advanced only at PPU register accesses / the NMI point / frame end,
+// exact sprite-0 hit, nes-py's flag layout and bus quirks. Counters are kept relative to the current
+// frame start (32-bit) instead of the reference's absolute int64 values; the 64-bit iteration count at
+// the frame start is only needed for the OAM-DMA odd/even cycle (nes_core.hpp:194).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mh {
+
+constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
+constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
+constexpr int LINE_END = 341;
+constexpr int GRAY_PIX = 256 * 240;
+enum : uint8_t { FN = 0x01, FV = 0x02, FONE = 0x04, FB = 0x08, FD = 0x10, FI = 0x20, FZ = 0x40, FC = 0x80 };
+enum : uint8_t { ST_PRE = 0, ST_RENDER = 1, ST_POST = 2, ST_VBLANK = 3 };
+
+// Scalar words of one console, interleaved as SC[w * NP + e].
+enum Scalar : int {
+    S_ITER_LO = 0, S_ITER_HI, S_EXEC_REL, S_PC, S_SP, S_A, S_X, S_Y, S_P, S_ZERO_SKIP,
+    S_JOY_STROBE0, S_JOY_STROBE1, S_JOY_BUTTONS0, S_JOY_BUTTONS1, S_JOY_BITS0, S_JOY_BITS1,
+    S_PSTATE, S_EVEN, S_VBLANK, S_S0HIT, S_FIRST_WRITE, S_DATA_BUFFER, S_OAM_ADDR, S_FINE_X,
+    S_SHOW_BG, S_SHOW_SPR, S_HIDE_EDGE_BG, S_HIDE_EDGE_SPR, S_LONG_SPR, S_NMI_EN, S_BG_PAGE, S_SPR_PAGE,
+    S_NSL, S_SL_LO, S_SL_HI, S_PCYC, S_SCANLINE, S_V, S_T, S_INC, S_COUNT
+};
+
+// Base cycles per opcode (data table of nes_core.hpp:42-51; 0 = not an official opcode).
+__device__ __constant__ static const uint8_t kCycles[256] = {
+    7, 6, 0, 0, 0, 3, 5, 0, 3, 2, 2, 0, 0, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
+    6, 6, 0, 0, 3, 3, 5, 0, 4, 2, 2, 0, 4, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
+    6, 6, 0, 0, 0, 3, 5, 0, 3, 2, 2, 0, 3, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
+    6, 6, 0, 0, 0, 3, 5, 0, 4, 2, 2, 0, 5, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
+    0, 6, 0, 0, 3, 3, 3, 0, 2, 0, 2, 0, 4, 4, 4, 0, 2, 6, 0, 0, 4, 4, 4, 0, 2, 5, 2, 0, 0, 5, 0, 0,
+    2, 6, 2, 0, 3, 3, 3, 0, 2, 2, 2, 0, 4, 4, 4, 0, 2, 5, 0, 0, 4, 4, 4, 0, 2, 4, 2, 0, 4, 4, 4, 0,
+    2, 6, 0, 0, 3, 3, 5, 0, 2, 2, 2, 0, 4, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
+    2, 6, 0, 0, 3, 3, 5, 0, 2, 2, 2, 2, 4, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
+};
+
+// Read-only cartridge view: PRG/CHR in LDS, name-table offsets in registers (uniform).
+struct Cart {
+    const uint8_t* prg;      // 0x8000 bytes (16 KB images mirrored)
+    const uint8_t* chr;      // 0x2000 bytes
+    uint16_t nt[4];
+};
+
+struct Console {
+    // ---- memory views
+    uint8_t* mem;            // MEM + e (row stride np)
+    uint32_t np;
+    Cart cart;
+    uint8_t* gray;           // GRAY slot + e (row stride np), written when render is on
+    const uint8_t* lut;      // palette value -> gray (LDS, 256 entries)
+    bool render;
+    // ---- CPU
+    uint16_t pc;
+    uint8_t sp, a, x, y, p, zero_skip;
+    int32_t exec_at, ppu_calls, nmi_thresh;  // relative to the current frame start
+    uint32_t iter_lo;                        // low word of the iteration count at the frame start
+    uint32_t iter_hi;
+    int32_t cur, skip;
+    // ---- joypads
+    uint8_t joy_strobe[2], joy_buttons[2], joy_bits[2];
+    // ---- PPU
+    uint8_t pstate, even, vblank, s0hit, first_write, data_buffer, oam_addr, fine_x;
+    uint8_t show_bg, show_spr, hide_edge_bg, hide_edge_spr, long_spr, nmi_en, bg_page, spr_page;
+    uint8_t nsl;
+    uint32_t sl_lo, sl_hi;                   // sprite list: 8 indices packed in two words
+    int32_t pcyc, scanline;
+    uint16_t v, t, inc;
+    // ---- counters
+    uint32_t bad_ops, instructions;
+
+    // ------------------------------------------------------------ interleaved memory
+    __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mem[(size_t)__umul24(row, np)]; }
+    __device__ __forceinline__ void st(uint32_t row, uint8_t val) { mem[(size_t)__umul24(row, np)] = val; }
+    __device__ __forceinline__ uint8_t ram(uint32_t a) const { return ld(ROW_RAM + (a & 0x7ff)); }
+    __device__ __forceinline__ uint8_t oam(uint32_t i) const { return ld(ROW_OAM + (i & 0xff)); }
+    __device__ __forceinline__ uint8_t pal(uint32_t i) const { return ld(ROW_PAL + (i & 0x1f)); }
+    __device__ __forceinline__ uint8_t vram(uint32_t i) const { return ld(ROW_VRAM + (i & 0x7ff)); }
+    __device__ __forceinline__ uint8_t sl(int k) const {
+        return (uint8_t)((k < 4 ? sl_lo >> (8 * k) : sl_hi >> (8 * (k - 4))) & 0xff);
+    }
+    __device__ __forceinline__ void set_sl(int k, uint8_t i) {
+        if (k < 4) sl_lo = (sl_lo & ~(0xffu << (8 * k))) | ((uint32_t)i << (8 * k));
+        else sl_hi = (sl_hi & ~(0xffu << (8 * (k - 4)))) | ((uint32_t)i << (8 * (k - 4)));
+    }
+    __device__ __forceinline__ uint8_t prg(uint16_t a) const { return cart.prg[a & 0x7fff]; }
+
+    // ------------------------------------------------------------ state in / out
+    __device__ void load(const uint32_t* sc, uint32_t e) {
+        auto w = [&](int k) { return sc[(size_t)k * np + e]; };
+        iter_lo = w(S_ITER_LO); iter_hi = w(S_ITER_HI);
+        exec_at = (int32_t)w(S_EXEC_REL);
+        ppu_calls = 0;
+        pc = (uint16_t)w(S_PC); sp = (uint8_t)w(S_SP); a = (uint8_t)w(S_A); x = (uint8_t)w(S_X);
+        y = (uint8_t)w(S_Y); p = (uint8_t)w(S_P); zero_skip = (uint8_t)w(S_ZERO_SKIP);
+        joy_strobe[0] = (uint8_t)w(S_JOY_STROBE0); joy_strobe[1] = (uint8_t)w(S_JOY_STROBE1);
+        joy_buttons[0] = (uint8_t)w(S_JOY_BUTTONS0); joy_buttons[1] = (uint8_t)w(S_JOY_BUTTONS1);
+        joy_bits[0] = (uint8_t)w(S_JOY_BITS0); joy_bits[1] = (uint8_t)w(S_JOY_BITS1);
+        pstate = (uint8_t)w(S_PSTATE); even = (uint8_t)w(S_EVEN); vblank = (uint8_t)w(S_VBLANK);
+        s0hit = (uint8_t)w(S_S0HIT); first_write = (uint8_t)w(S_FIRST_WRITE);
+        data_buffer = (uint8_t)w(S_DATA_BUFFER); oam_addr = (uint8_t)w(S_OAM_ADDR); fine_x = (uint8_t)w(S_FINE_X);
+        show_bg = (uint8_t)w(S_SHOW_BG); show_spr = (uint8_t)w(S_SHOW_SPR);
+        hide_edge_bg = (uint8_t)w(S_HIDE_EDGE_BG); hide_edge_spr = (uint8_t)w(S_HIDE_EDGE_SPR);
+        long_spr = (uint8_t)w(S_LONG_SPR); nmi_en = (uint8_t)w(S_NMI_EN);
+        bg_page = (uint8_t)w(S_BG_PAGE); spr_page = (uint8_t)w(S_SPR_PAGE);
+        nsl = (uint8_t)w(S_NSL); sl_lo = w(S_SL_LO); sl_hi = w(S_SL_HI);
+        pcyc = (int32_t)w(S_PCYC); scanline = (int32_t)w(S_SCANLINE);
+        v = (uint16_t)w(S_V); t = (uint16_t)w(S_T); inc = (uint16_t)w(S_INC);
+        nmi_threshold();
+    }
+    __device__ void store(uint32_t* sc, uint32_t e) const {
+        auto w = [&](int k, uint32_t val) { sc[(size_t)k * np + e] = val; };
+        w(S_ITER_LO, iter_lo); w(S_ITER_HI, iter_hi); w(S_EXEC_REL, (uint32_t)exec_at);
+        w(S_PC, pc); w(S_SP, sp); w(S_A, a); w(S_X, x); w(S_Y, y); w(S_P, p); w(S_ZERO_SKIP, zero_skip);
+        w(S_JOY_STROBE0, joy_strobe[0]); w(S_JOY_STROBE1, joy_strobe[1]);
+        w(S_JOY_BUTTONS0, joy_buttons[0]); w(S_JOY_BUTTONS1, joy_buttons[1]);
+        w(S_JOY_BITS0, joy_bits[0]); w(S_JOY_BITS1, joy_bits[1]);
+        w(S_PSTATE, pstate); w(S_EVEN, even); w(S_VBLANK, vblank); w(S_S0HIT, s0hit);
+        w(S_FIRST_WRITE, first_write); w(S_DATA_BUFFER, data_buffer); w(S_OAM_ADDR, oam_addr);
+        w(S_FINE_X, fine_x); w(S_SHOW_BG, show_bg); w(S_SHOW_SPR, show_spr);
+        w(S_HIDE_EDGE_BG, hide_edge_bg); w(S_HIDE_EDGE_SPR, hide_edge_spr); w(S_LONG_SPR, long_spr);
+        w(S_NMI_EN, nmi_en); w(S_BG_PAGE, bg_page); w(S_SPR_PAGE, spr_page);
+        w(S_NSL, nsl); w(S_SL_LO, sl_lo); w(S_SL_HI, sl_hi); w(S_PCYC, (uint32_t)pcyc);
+        w(S_SCANLINE, (uint32_t)scanline); w(S_V, v); w(S_T, t); w(S_INC, inc);
+    }
+
+    // power-on: zeroed machine, then CPU and PPU reset (nes_core.hpp:123-147)
+    __device__ void power_on() {
+        for (uint32_t r = 0; r < MEM_ROWS; r++) st(r, 0);
+        iter_lo = iter_hi = 0; exec_at = 0; ppu_calls = 0;
+        joy_strobe[0] = joy_strobe[1] = 1; joy_buttons[0] = joy_buttons[1] = 0; joy_bits[0] = joy_bits[1] = 0;
+        zero_skip = 0; a = x = y = 0; p = 0x34;
+        pc = (uint16_t)(prg(0xfffc) | prg(0xfffd) << 8);
+        sp = 0xfd;
+        s0hit = 0; data_buffer = 0; hide_edge_bg = hide_edge_spr = 0;
+        long_spr = 0; nmi_en = 0; vblank = 0; show_bg = 1; show_spr = 1; even = 1;
+        first_write = 1; bg_page = 0; spr_page = 0; v = 0; pcyc = 0; scanline = 0;
+        oam_addr = 0; fine_x = 0; t = 0; inc = 1; pstate = ST_PRE; nsl = 0; sl_lo = sl_hi = 0;
+        nmi_threshold();
+    }
+
+    // ------------------------------------------------------------ CPU bus (nes_core.hpp:150-208)
+    __device__ uint8_t read(uint16_t ad) {
+        if (ad >= 0x8000) return prg(ad);
+        if (ad < 0x2000) return ram(ad);
+        if (ad < 0x4000) {
+            uint16_t r = ad & 0x2007;
+            if (r == 0x2002) { catch_up(); return status_read(); }
+            if (r == 0x2007) { catch_up(); return data_read(); }
+            if (r == 0x2004) return oam(oam_addr);
+            return 0;
+        }
+        if (ad == 0x4016) return pad_read(0);
+        if (ad == 0x4017) return pad_read(1);
+        return 0;
+    }
+    __device__ void write(uint16_t ad, uint8_t val) {
+        if (ad < 0x2000) { st(ROW_RAM + (ad & 0x7ff), val); return; }
+        if (ad < 0x4000) {
+            switch (ad & 0x2007) {
+                case 0x2000: catch_up(); ctrl_write(val); break;
+                case 0x2001: catch_up(); mask_write(val); break;
+                case 0x2003: catch_up(); oam_addr = val; break;
+                case 0x2004: catch_up(); st(ROW_OAM + oam_addr, val); oam_addr++; break;
+                case 0x2005: catch_up(); scroll_write(val); break;
+                case 0x2006: catch_up(); addr_write(val); break;
+                case 0x2007: catch_up(); data_write(val); break;
+                default: break;
+            }
+            return;
+        }
+        if (ad == 0x4014) {  // OAM DMA: 513 cycles, +1 on an odd absolute cycle; copies from RAM pages only
+            catch_up();
+            skip += 513 + (int)((iter_lo + (uint32_t)cur + 1u) & 1u);
+            uint16_t src = (uint16_t)(val << 8);
+            if (src < 0x2000)
+                for (int i = 0; i < 256; i++) st(ROW_OAM + ((oam_addr + i) & 0xff), ram(src + i));
+            return;
+        }
+        if (ad == 0x4016) {
+            for (int i = 0; i < 2; i++) {
+                joy_strobe[i] = val & 1;
+                if (!joy_strobe[i]) joy_bits[i] = joy_buttons[i];
+            }
+        }
+    }
+    __device__ uint8_t pad_read(int i) {
+        uint8_t bit;
+        if (joy_strobe[i]) bit = joy_buttons[i] & 1;
+        else { bit = joy_bits[i] & 1; joy_bits[i] >>= 1; }
+        return bit | 0x40;
+    }
+
+    // ------------------------------------------------------------ PPU registers (nes_core.hpp:211-260)
+    __device__ void ctrl_write(uint8_t c) {
+        nmi_en = (c >> 7) & 1; long_spr = (c >> 5) & 1; bg_page = (c >> 4) & 1; spr_page = (c >> 3) & 1;
+        inc = (c & 4) ? 32 : 1;
+        t = (uint16_t)((t & 0xf3ff) | ((c & 3) << 10));
+    }
+    __device__ void mask_write(uint8_t k) {
+        hide_edge_bg = !(k & 2); hide_edge_spr = !(k & 4); show_bg = (k >> 3) & 1; show_spr = (k >> 4) & 1;
+    }
+    __device__ uint8_t status_read() {
+        uint8_t r = (uint8_t)((s0hit << 6) | (vblank << 7));
+        vblank = 0; first_write = 1;
+        return r;
+    }
+    __device__ void addr_write(uint8_t d) {
+        if (first_write) { t = (uint16_t)((t & 0x00ff) | ((d & 0x3f) << 8)); first_write = 0; }
+        else { t = (uint16_t)((t & 0xff00) | d); v = t; first_write = 1; }
+    }
+    __device__ uint8_t data_read() {
+        uint8_t d = vbus_read(v);
+        v = (uint16_t)(v + inc);
+        if (v < 0x3f00) { uint8_t b = data_buffer; data_buffer = d; d = b; }
+        return d;
+    }
+    __device__ void data_write(uint8_t d) { vbus_write(v, d); v = (uint16_t)(v + inc); }
+    __device__ void scroll_write(uint8_t d) {
+        if (first_write) { t = (uint16_t)((t & ~0x1f) | (d >> 3)); fine_x = d & 7; first_write = 0; }
+        else { t = (uint16_t)((t & ~0x73e0) | ((d & 7) << 12) | ((d & 0xf8) << 2)); first_write = 1; }
+    }
+
+    // ------------------------------------------------------------ picture bus (nes_core.hpp:263-285)
+    __device__ __forceinline__ uint32_t nt_row(uint16_t ad) const {
+        int k = ad < 0x2400 ? 0 : ad < 0x2800 ? 1 : ad < 0x2c00 ? 2 : 3;
+        return cart.nt[k] + (ad & 0x3ff);
+    }
+    __device__ uint8_t vbus_read(uint16_t ad) const {
+        if (ad < 0x2000) return cart.chr[ad];
+        if (ad < 0x3eff) return vram(nt_row(ad));
+        if (ad < 0x3fff) return pal(ad);
+        return 0;
+    }
+    __device__ void vbus_write(uint16_t ad, uint8_t d) {
+        if (ad < 0x2000) return;
+        if (ad < 0x3eff) st(ROW_VRAM + nt_row(ad), d);
+        else if (ad < 0x3fff) st(ROW_PAL + (ad == 0x3f10 ? 0 : (ad & 0x1f)), d);
+    }
+    __device__ __forceinline__ uint8_t nametable(uint16_t ad) const { return vram(cart.nt[(ad >> 10) & 3] + (ad & 0x3ff)); }
+
+    // ------------------------------------------------------------ PPU timing (nes_core.hpp:289-308)
+    __device__ void nmi_threshold() {
+        int line = pstate == ST_PRE ? -1 : pstate == ST_POST ? 240 : scanline;
+        int32_t pos = (line + 1) * 341 + (pcyc - 1);
+        const int32_t vbl = 242 * 341;
+        int32_t d = pos <= vbl ? vbl - pos + 1 : (262 * 341 - pos) + vbl + 1;
+        nmi_thresh = ppu_calls + d - 8;
+    }
+    __device__ void advance_to(int32_t target) {
+        if (target > ppu_calls) { ppu_run(target - ppu_calls); nmi_threshold(); }
+    }
+    __device__ void catch_up() { advance_to(3 * (cur + 1)); }
+
+    __device__ void coarse_x_add(int n) {
+        int tot = (v & 0x1f) + n;
+        v = (uint16_t)((v & ~0x1f) | (tot & 31));
+        if ((tot >> 5) & 1) v ^= 0x400;
+    }
+    __device__ void fine_y_step() {
+        if ((v & 0x7000) != 0x7000) { v += 0x1000; return; }
+        v &= ~0x7000;
+        int yy = (v >> 5) & 31;
+        if (yy == 29) { yy = 0; v ^= 0x800; }
+        else if (yy == 31) yy = 0;
+        else yy++;
+        v = (uint16_t)((v & ~0x3e0) | (yy << 5));
+    }
+    __device__ void copy_h() { v = (uint16_t)((v & ~0x41f) | (t & 0x41f)); }
+    __device__ void copy_v() { v = (uint16_t)((v & ~0x7be0) | (t & 0x7be0)); }
+
+    // per-line sprite list from oam_addr/4 (nes_core.hpp:336-349)
+    __device__ void eval_sprites() {
+        nsl = 0;
+        int h = long_spr ? 16 : 8;
+        for (int i = oam_addr / 4; i < 64 && nsl < 8; i++) {
+            int d = scanline - (int)oam(i * 4);
+            if (d >= 0 && d < h) { set_sl(nsl, (uint8_t)i); nsl++; }
+        }
+    }
+    __device__ uint8_t bg_colour(int px, uint8_t* pattern) const {
+        int xf = (fine_x + px) % 8;
+        uint8_t tile = nametable((uint16_t)(0x2000 | (v & 0x0fff)));
+        uint16_t pa = (uint16_t)(((tile * 16) + ((v >> 12) & 7)) | (bg_page << 12));
+        uint8_t c = (uint8_t)(((cart.chr[pa] >> (7 ^ xf)) & 1) | (((cart.chr[pa + 8] >> (7 ^ xf)) & 1) << 1));
+        *pattern = c;
+        uint16_t aa = (uint16_t)(0x23c0 | (v & 0x0c00) | ((v >> 4) & 0x38) | ((v >> 2) & 7));
+        int sh = ((v >> 4) & 4) | (v & 2);
+        return (uint8_t)(c | (((nametable(aa) >> sh) & 3) << 2));
+    }
+    // sprite i's 2-bit pattern at (px, py), with C++ int semantics for stale lists (nes_core.hpp:369-391)
+    __device__ uint8_t sprite_pattern(int i, int px, int py) const {
+        uint8_t sx = oam(i * 4 + 3);
+        uint8_t sy = (uint8_t)(oam(i * 4) + 1), tile = oam(i * 4 + 1), attr = oam(i * 4 + 2);
+        int h = long_spr ? 16 : 8;
+        int xs = (px - sx) % 8, yo = (py - sy) % h;
+        if (!(attr & 0x40)) xs ^= 7;
+        if (attr & 0x80) yo ^= (h - 1);
+        uint16_t ad;
+        if (!long_spr) {
+            ad = (uint16_t)(tile * 16 + yo);
+            if (spr_page) ad += 0x1000;
+        } else {
+            yo = (yo & 7) | ((yo & 8) << 1);
+            ad = (uint16_t)((tile >> 1) * 32 + yo);
+            ad |= (tile & 1) << 12;
+        }
+        return (uint8_t)(((vbus_read(ad) >> xs) & 1) | (((vbus_read((uint16_t)(ad + 8)) >> xs) & 1) << 1));
+    }
+
+    // visible dots [x0, x1) without pixel output (nes_core.hpp:394-413)
+    __device__ void dots_quiet(int x0, int x1) {
+        if (!show_bg) return;
+        if (!s0hit && show_spr && nsl > 0 && sl(0) == 0) {
+            int sx = oam(3);
+            int lo = x0 > sx ? x0 : sx;
+            int hi = x1 < sx + 8 ? x1 : sx + 8;
+            if (hide_edge_spr && lo < 8) lo = 8;
+            if (lo < hi) {
+                coarse_x_add(inc_count(x0, lo));
+                for (int px = lo; px < hi; px++) {
+                    if (!s0hit && (!hide_edge_bg || px >= 8)) {
+                        uint8_t pat;
+                        bg_colour(px, &pat);
+                        if (pat && sprite_pattern(0, px, scanline)) s0hit = 1;
+                    }
+                    if ((fine_x + px) % 8 == 7) coarse_x_add(1);
+                }
+                coarse_x_add(inc_count(hi, x1));
+                return;
+            }
+        }
+        coarse_x_add(inc_count(x0, x1));
+    }
+    __device__ __forceinline__ int inc_count(int lo, int hi) const {   // x in [lo, hi) with (fine_x + x) % 8 == 7
+        int r = (7 - fine_x) & 7;
+        return (hi - r + 7) / 8 - (lo - r + 7) / 8;
+    }
+
+    // visible dots [x0, x1) with pixel output: gray values into the frame buffer (nes_core.hpp:467-513)
+    __device__ void dots_drawn(int x0, int x1) {
+        const int py = scanline;
+        for (int px = x0; px < x1; px++) {
+            uint8_t pa = 0, bg_op = 0;
+            if (show_bg) {
+                uint8_t pat;
+                uint8_t c = bg_colour(px, &pat);
+                if (!(hide_edge_bg && px < 8) && pat) { pa = c; bg_op = pat; }
+                if ((fine_x + px) % 8 == 7) coarse_x_add(1);
+            }
+            if (show_spr && nsl && !(hide_edge_spr && px < 8)) {
+                for (int k = 0; k < nsl; k++) {
+                    int i = sl(k);
+                    int sx = oam(i * 4 + 3);
+                    if (px < sx || px >= sx + 8) continue;
+                    uint8_t c = sprite_pattern(i, px, py);
+                    if (!c) continue;
+                    uint8_t attr = oam(i * 4 + 2);
+                    if (i == 0 && bg_op && !s0hit && show_bg) s0hit = 1;
+                    if (!bg_op || !(attr & 0x20)) pa = (uint8_t)(c | 0x10 | ((attr & 3) << 2));
+                    break;
+                }
+            }
+            gray[(size_t)__umul24((uint32_t)(py * 256 + px), np)] = lut[pal(pa)];
+        }
+    }
+
+    // NMI raised by PPU call `call` (1-based, frame-relative); nes_core.hpp:520-531
+    __device__ void nmi(int32_t call) {
+        int32_t it = (call - 1) / 3;
+        push((uint8_t)(pc >> 8)); push((uint8_t)pc); push((uint8_t)(p | 0x20));
+        p |= FI;
+        pc = (uint16_t)(prg(0xfffa) | prg(0xfffb) << 8);
+        int32_t d = (zero_skip && it == exec_at) ? 0 : (exec_at - it + 1);
+        exec_at = it + d + 6;
+        zero_skip = 0;
+    }
+
+    // advance the PPU by n calls (nes_core.hpp:539-616)
+    __device__ void ppu_run(int32_t n) {
+        while (n > 0) {
+            int c = pcyc;
+            if (pstate == ST_PRE) {
+                bool on = show_bg && show_spr;
+                int end = LINE_END - (!even && on);
+                int k = c >= end ? 1 : (n < end - c ? n : end - c);
+                int lo = c, hi = c + k;
+                if (lo <= 1 && 1 < hi) vblank = s0hit = 0;
+                if (on) {
+                    if (lo <= 258 && 258 < hi) copy_h();
+                    if (lo <= 304 && 281 < hi) copy_v();
+                }
+                ppu_calls += k; n -= k;
+                if (hi - 1 >= end) { pstate = ST_RENDER; scanline = 0; pcyc = 1; }
+                else pcyc = hi;
+            } else if (pstate == ST_RENDER) {
+                if (c >= 1 && c <= 256) {
+                    int k = n < 257 - c ? n : 257 - c;
+                    if (render) dots_drawn(c - 1, c - 1 + k);
+                    else dots_quiet(c - 1, c - 1 + k);
+                    pcyc += k; ppu_calls += k; n -= k;
+                } else if (c == 257) {
+                    if (show_bg) fine_y_step();
+                    pcyc++; ppu_calls++; n--;
+                } else if (c == 258) {
+                    if (show_bg && show_spr) copy_h();
+                    pcyc++; ppu_calls++; n--;
+                } else if (c > 258 && c < LINE_END) {
+                    int k = n < LINE_END - c ? n : LINE_END - c;
+                    pcyc += k; ppu_calls += k; n -= k;
+                } else if (c >= LINE_END) {
+                    eval_sprites();
+                    scanline++;
+                    pcyc = 1; ppu_calls++; n--;
+                    if (scanline >= 240) pstate = ST_POST;
+                } else {
+                    pcyc++; ppu_calls++; n--;
+                }
+            } else if (pstate == ST_POST) {
+                if (c >= LINE_END) { scanline++; pcyc = 1; pstate = ST_VBLANK; ppu_calls++; n--; }
+                else { int k = n < LINE_END - c ? n : LINE_END - c; pcyc += k; ppu_calls += k; n -= k; }
+            } else {
+                if (c >= LINE_END) {
+                    scanline++; pcyc = 1;
+                    if (scanline >= 261) { pstate = ST_PRE; scanline = 0; even = !even; }
+                    ppu_calls++; n--;
+                } else if (c == 1 && scanline == 241) {
+                    vblank = 1; ppu_calls++; n--; pcyc = 2;
+                    if (nmi_en) nmi(ppu_calls);
+                } else {
+                    int lim = LINE_END - c;
+                    if (scanline == 241 && c < 1) lim = 1 - c;
+                    int k = n < lim ? n : lim;
+                    pcyc += k; ppu_calls += k; n -= k;
+                }
+            }
+        }
+    }
+
+    // ------------------------------------------------------------ CPU (nes_core.hpp:619-899)
+    __device__ __forceinline__ void set_nz(uint8_t r) { p = (uint8_t)((p & ~(FZ | FN)) | (r ? 0 : FZ) | (r & 0x80 ? FN : 0)); }
+    __device__ __forceinline__ void flag(uint8_t f, bool on) { p = on ? (uint8_t)(p | f) : (uint8_t)(p & ~f); }
+    __device__ __forceinline__ bool has(uint8_t f) const { return (p & f) != 0; }
+    __device__ uint16_t read16(uint16_t ad) { uint8_t lo = read(ad); uint8_t hi = read((uint16_t)(ad + 1)); return (uint16_t)(lo | hi << 8); }
+    __device__ __forceinline__ void push(uint8_t d) { st(ROW_RAM + ((0x100 | sp) & 0x7ff), d); sp--; }
+    __device__ __forceinline__ uint8_t pull() { sp++; return ram(0x100 | sp); }
+    __device__ __forceinline__ void cross_penalty(uint16_t u, uint16_t w, int k) { if ((u & 0xff00) != (w & 0xff00)) skip += k; }
+
+    __device__ bool op_implied(uint8_t op) {
+        switch (op) {
+            case 0x00:
+                pc++;
+                push((uint8_t)(pc >> 8)); push((uint8_t)pc); push((uint8_t)(p | 0x30));
+                p |= FI; pc = read16(0xfffe); skip += 7;
+                return true;
+            case 0x08: push(p); return true;
+            case 0x18: flag(FC, false); return true;
+            case 0x20: { uint16_t ret = (uint16_t)(pc + 1); push((uint8_t)(ret >> 8)); push((uint8_t)ret); pc = read16(pc); return true; }
+            case 0x28: p = pull(); return true;
+            case 0x38: flag(FC, true); return true;
+            case 0x40: { p = pull(); uint8_t lo = pull(); uint8_t hi = pull(); pc = (uint16_t)(lo | hi << 8); return true; }
+            case 0x48: push(a); return true;
+            case 0x4c: pc = read16(pc); return true;
+            case 0x58: flag(FI, false); return true;
+            case 0x60: { uint8_t lo = pull(); uint8_t hi = pull(); pc = (uint16_t)((lo | hi << 8) + 1); return true; }
+            case 0x68: a = pull(); set_nz(a); return true;
+            case 0x6c: {
+                uint16_t ptr = read16(pc);
+                uint8_t lo = read(ptr);
+                uint8_t hi = read((uint16_t)((ptr & 0xff00) | ((ptr + 1) & 0xff)));
+                pc = (uint16_t)(lo | hi << 8);
+                return true;
+            }
+            case 0x78: flag(FI, true); return true;
+            case 0x88: y--; set_nz(y); return true;
+            case 0x8a: a = x; set_nz(a); return true;
+            case 0x98: a = y; set_nz(a); return true;
+            case 0x9a: sp = x; return true;
+            case 0xa8: y = a; set_nz(y); return true;
+            case 0xaa: x = a; set_nz(x); return true;
+            case 0xb8: flag(FV, false); return true;
+            case 0xba: x = sp; set_nz(x); return true;
+            case 0xc8: y++; set_nz(y); return true;
+            case 0xca: x--; set_nz(x); return true;
+            case 0xd8: flag(FD, false); return true;
+            case 0xe8: x++; set_nz(x); return true;
+            case 0xea: return true;
+            case 0xf8: flag(FD, true); return true;
+            default: return false;
+        }
+    }
+    __device__ bool op_branch(uint8_t op) {
+        if ((op & 0x1f) != 0x10) return false;
+        const uint8_t which = (op >> 6) == 0 ? FN : (op >> 6) == 1 ? FV : (op >> 6) == 2 ? FC : FZ;
+        bool take = has(which) == ((op & 0x20) != 0);
+        if (take) {
+            int8_t off = (int8_t)read(pc++);
+            skip += 1;
+            uint16_t to = (uint16_t)(pc + off);
+            cross_penalty(pc, to, 2);
+            pc = to;
+        } else {
+            pc++;
+        }
+        return true;
+    }
+    __device__ bool op_group0(uint8_t op) {
+        if ((op & 3) != 0) return false;
+        uint16_t ea;
+        switch ((op >> 2) & 7) {
+            case 0: ea = pc++; break;
+            case 1: ea = read(pc++); break;
+            case 3: ea = read16(pc); pc += 2; break;
+            case 5: ea = (uint8_t)(read(pc++) + x); break;
+            case 7: ea = read16(pc); pc += 2; cross_penalty(ea, (uint16_t)(ea + x), 1); ea = (uint16_t)(ea + x); break;
+            default: return false;
+        }
+        switch (op >> 5) {
+            case 1: { uint8_t d = read(ea); flag(FZ, !(a & d)); flag(FV, d & 0x40); flag(FN, d & 0x80); return true; }
+            case 4: write(ea, y); return true;
+            case 5: y = read(ea); set_nz(y); return true;
+            case 6: { uint16_t r = (uint16_t)(y - read(ea)); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); return true; }
+            case 7: { uint16_t r = (uint16_t)(x - read(ea)); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); return true; }
+            default: return false;
+        }
+    }
+    __device__ bool op_group1(uint8_t op) {
+        if ((op & 3) != 1) return false;
+        int fn = op >> 5;
+        bool store = fn == 4;
+        uint16_t ea;
+        switch ((op >> 2) & 7) {
+            case 0: { uint8_t z = (uint8_t)(x + read(pc++)); uint8_t lo = read(z); uint8_t hi = read((uint8_t)(z + 1)); ea = (uint16_t)(lo | hi << 8); break; }
+            case 1: ea = read(pc++); break;
+            case 2: ea = pc++; break;
+            case 3: ea = read16(pc); pc += 2; break;
+            case 4: {
+                uint8_t z = read(pc++); uint8_t lo = read(z); uint8_t hi = read((uint8_t)(z + 1));
+                ea = (uint16_t)(lo | hi << 8);
+                if (!store) cross_penalty(ea, (uint16_t)(ea + y), 1);
+                ea = (uint16_t)(ea + y);
+                break;
+            }
+            case 5: ea = (uint8_t)(read(pc++) + x); break;
+            case 6: ea = read16(pc); pc += 2; if (!store) cross_penalty(ea, (uint16_t)(ea + y), 1); ea = (uint16_t)(ea + y); break;
+            default: ea = read16(pc); pc += 2; if (!store) cross_penalty(ea, (uint16_t)(ea + x), 1); ea = (uint16_t)(ea + x); break;
+        }
+        switch (fn) {
+            case 0: a |= read(ea); set_nz(a); break;
+            case 1: a &= read(ea); set_nz(a); break;
+            case 2: a ^= read(ea); set_nz(a); break;
+            case 3: {
+                uint8_t d = read(ea);
+                uint16_t s = (uint16_t)(a + d + (has(FC) ? 1 : 0));
+                flag(FC, s & 0x100); flag(FV, (a ^ s) & (d ^ s) & 0x80);
+                a = (uint8_t)s; set_nz(a);
+                break;
+            }
+            case 4: write(ea, a); break;
+            case 5: a = read(ea); set_nz(a); break;
+            case 6: { uint16_t r = (uint16_t)(a - read(ea)); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
+            default: {
+                uint16_t d = read(ea);
+                uint16_t r = (uint16_t)(a - d - (has(FC) ? 0 : 1));
+                flag(FC, !(r & 0x100)); flag(FV, (a ^ r) & (~d ^ r) & 0x80);
+                a = (uint8_t)r; set_nz((uint8_t)r);
+                break;
+            }
+        }
+        return true;
+    }
+    __device__ bool op_group2(uint8_t op) {
+        if ((op & 3) != 2) return false;
+        int fn = op >> 5, mode = (op >> 2) & 7;
+        bool xy = fn == 4 || fn == 5;
+        uint16_t ea = 0;
+        switch (mode) {
+            case 0: ea = pc++; break;
+            case 1: ea = read(pc++); break;
+            case 2: break;
+            case 3: ea = read16(pc); pc += 2; break;
+            case 5: ea = (uint8_t)(read(pc++) + (xy ? y : x)); break;
+            case 7: { ea = read16(pc); pc += 2; uint8_t ix = xy ? y : x; cross_penalty(ea, (uint16_t)(ea + ix), 1); ea = (uint16_t)(ea + ix); break; }
+            default: return false;
+        }
+        switch (fn) {
+            case 0: case 1: {
+                bool cin = has(FC) && fn == 1;
+                if (mode == 2) { flag(FC, a & 0x80); a = (uint8_t)((a << 1) | cin); set_nz(a); }
+                else { uint8_t d = read(ea); flag(FC, d & 0x80); d = (uint8_t)((d << 1) | cin); set_nz(d); write(ea, d); }
+                break;
+            }
+            case 2: case 3: {
+                bool cin = has(FC) && fn == 3;
+                if (mode == 2) { flag(FC, a & 1); a = (uint8_t)((a >> 1) | (cin << 7)); set_nz(a); }
+                else { uint8_t d = read(ea); flag(FC, d & 1); d = (uint8_t)((d >> 1) | (cin << 7)); set_nz(d); write(ea, d); }
+                break;
+            }
+            case 4: write(ea, x); break;
+            case 5: x = read(ea); set_nz(x); break;
+            case 6: { uint8_t d = (uint8_t)(read(ea) - 1); set_nz(d); write(ea, d); break; }
+            default: { uint8_t d = (uint8_t)(read(ea) + 1); set_nz(d); write(ea, d); break; }
+        }
+        return true;
+    }
+    __device__ int step_instruction() {
+        skip = 0;
+        uint8_t op = read(pc++);
+        instructions++;
+        if (op_implied(op) || op_branch(op) || op_group1(op) || op_group2(op) || op_group0(op)) skip += kCycles[op];
+        else bad_ops++;
+        return skip;
+    }
+
+    // one nes-py Emulator::step (nes_core.hpp:1166-1204) with the exact `JMP *` idle fast-forward
+    __device__ void frame() {
+        const int32_t end = FRAME_ITERS;
+        while (exec_at < end) {
+            const int32_t j = exec_at;
+            if (3 * (j + 1) >= nmi_thresh) {
+                cur = j;
+                advance_to(3 * (j + 1));
+                if (exec_at != j) continue;
+            }
+            uint16_t here = pc;
+            if (here >= 0x8000 && prg(here) == 0x4c) {
+                uint16_t p1 = (uint16_t)(here + 1), p2 = (uint16_t)(here + 2);
+                uint8_t lo = p1 >= 0x8000 ? prg(p1) : 0xff, hi = p2 >= 0x8000 ? prg(p2) : 0xff;
+                if ((uint16_t)(lo | hi << 8) == here) {
+                    int32_t lim_end = end - j, lim_nmi = nmi_thresh - 3 * (j + 1);
+                    int32_t k1 = lim_end > 0 ? (lim_end + 2) / 3 : 0;
+                    int32_t k2 = lim_nmi > 0 ? (lim_nmi + 8) / 9 : 0;
+                    int32_t k = k1 < k2 ? k1 : k2;
+                    if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; continue; }
+                }
+            }
+            cur = j;
+            int s = step_instruction();
+            exec_at = j + (s >= 1 ? s : 1);
+            zero_skip = s <= 0;
+        }
+        advance_to(3 * end);
+        // rebase the frame-relative counters on the new frame start
+        exec_at -= FRAME_ITERS;
+        ppu_calls -= 3 * FRAME_ITERS;
+        nmi_thresh -= 3 * FRAME_ITERS;
+        uint32_t lo = iter_lo + FRAME_ITERS;
+        iter_hi += lo < iter_lo;
+        iter_lo = lo;
+    }
+};
+
+}  // namespace mh

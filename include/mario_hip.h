@@ -1,0 +1,109 @@
+/* mario_hip: batched Super Mario Bros env stepping on one AMD MI355X (gfx950) — C ABI.
+ *
+ * This is the drop-in boundary for the hot path. It replaces the reference's CPU C-ABI
+ * (csrc/fastmario.cpp:562-674, bound by ctypes in src/fast_mario_env/_native.py:30-60) and its GPU
+ * launch path (src/fast_mario_env/cuda/vec_env.py:350-393 + cuda/cujit.py:157-178) with one library:
+ * the same create / set_buffers / reset / step_async / step_wait / destroy life cycle, but every
+ * per-env buffer lives in HBM and every call is queued on the caller's HIP stream.
+ *
+ * Conventions
+ *   - Plain C types only. `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Output buffers are device pointers owned by the caller (e.g. torch tensors); the library
+ *     writes them in place. Internal state (consoles, snapshots, reset cache) is owned by the library.
+ *   - Functions returning int return 0 on success and -1 on failure; creators return NULL on
+ *     failure. mh_last_error() then returns a message (thread-local, valid until the next call).
+ *   - One host thread drives one handle. Calls on one stream are ordered; no call blocks except
+ *     mh_step_wait and the query functions that copy results to the host.
+ */
+#ifndef MARIO_HIP_H
+#define MARIO_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct MhEnv MhEnv;
+typedef struct MhRaw MhRaw;
+
+#define MH_OBS_HW 84
+#define MH_INFO_FIELDS 10   /* x_pos flag_get life score time world stage coins y_pos status */
+#define MH_CANON_BYTES 4464 /* canonical console-state dump, layout shared with the CPU checker */
+
+/* Last error message of this thread ("" if none). */
+const char* mh_last_error(void);
+
+/* Creates N envs and boots every distinct level on the GPU (power-on + title sequence), then
+ * builds the no-op reset cache (one console per (level, k), k = 0..noop_max).
+ * Replaces fm_create (fastmario.cpp:566-601) and CudaVecEnv.__init__ (vec_env.py:247-347).
+ *   rom/rom_len   iNES image (NROM only), host memory
+ *   levels        3*n ints (world, stage, area) per env, host memory
+ *   lut           256 bytes, palette value -> gray, host memory
+ *   rng           6*n u64 per env: numpy PCG64 (state_hi, state_lo, inc_hi, inc_lo, has_uint32, uinteger)
+ *   skip 1..16, frame_stack 1..16, maxpool 0/1, sticky in [0, 1], noop_max >= 0, max_steps >= 1.
+ * Blocks until construction is finished. */
+MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, const uint8_t* lut,
+                 int skip, int max_steps, double sticky, int noop_max, int maxpool, int frame_stack,
+                 const uint64_t* rng, int device);
+
+/* Output buffers (device pointers, caller-owned). Replaces fm_set_buffers (fastmario.cpp:603-609).
+ *   obs, fin  n * frame_stack * 84 * 84 u8 (stacked observations; final stack of finished episodes)
+ *   rew       n f32;  term, trunc  n u8 (0/1);  info  n * 10 i32
+ *   ep_ret    n f64;  ep_len  n i32 (written only for envs whose episode ended this step) */
+int mh_set_buffers(MhEnv* h, uint8_t* obs, uint8_t* fin, float* rew, uint8_t* term, uint8_t* trunc,
+                   int32_t* info, double* ep_ret, int32_t* ep_len);
+
+/* Reset every env (no-op starts drawn from each env's PCG64 stream). Replaces fm_reset. */
+int mh_reset(MhEnv* h, void* stream);
+
+/* Queue one agent step of every env; d_actions: n i64 device pointer (values 0..6).
+ * Replaces fm_step_async (fastmario.cpp:611-616) / CudaVecEnv.step (vec_env.py:367-373). */
+int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream);
+
+/* Wait for queued work on `stream`. Replaces fm_step_wait (fastmario.cpp:617). */
+int mh_step_wait(MhEnv* h, void* stream);
+
+void mh_destroy(MhEnv* h);
+
+/* Counters summed over envs (synchronizing). Replace fm_frames / fm_bad_ops (fastmario.cpp:619-628).
+ * frames counts every emulated NES frame the reference CPU path emulates (hack frames and
+ * early-termination re-renders included); instructions counts retired 6502 instructions. */
+int64_t mh_frames(MhEnv* h);
+int64_t mh_bad_ops(MhEnv* h);
+int64_t mh_instructions(MhEnv* h);
+
+/* RAM of every env into d_out (n * 2048 u8, device). Replaces fm_env_ram (fastmario.cpp:630). */
+int mh_env_ram(MhEnv* h, uint8_t* d_out, void* stream);
+/* Canonical console state of every env (n * MH_CANON_BYTES u8, device); level boot states
+ * (n_levels * MH_CANON_BYTES) and boot observations (n_levels * 84 * 84). */
+int mh_env_canon(MhEnv* h, uint8_t* d_out, void* stream);
+int mh_level_canon(MhEnv* h, uint8_t* d_out, void* stream);
+int mh_level_obs(MhEnv* h, uint8_t* d_out, void* stream);
+int mh_num_levels(MhEnv* h);
+
+/* Bytes of console state per env (replaces fm_state_bytes) and device bytes per env. */
+int64_t mh_state_bytes(void);
+int64_t mh_env_bytes(MhEnv* h);
+
+/* ---- raw consoles: frame stepping without the env layer (replaces fm_raw_*, fastmario.cpp:651-673) */
+MhRaw*  mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device);
+/* one frame of every console; d_buttons: n u8 device pointer; render != 0 draws the screen */
+int     mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream);
+int     mh_raw_ram(MhRaw* h, uint8_t* d_out, void* stream);        /* n * 2048 */
+int     mh_raw_screen(MhRaw* h, uint8_t* d_out, void* stream);     /* n * 240 * 256 palette values */
+int     mh_raw_canon(MhRaw* h, uint8_t* d_out, void* stream);      /* n * MH_CANON_BYTES */
+int     mh_raw_backup(MhRaw* h, void* stream);
+int     mh_raw_restore(MhRaw* h, void* stream);
+int64_t mh_raw_bad_ops(MhRaw* h);
+int64_t mh_raw_instructions(MhRaw* h);
+void    mh_raw_destroy(MhRaw* h);
+
+/* ---- helpers */
+/* 240x256 gray images -> 84x84 INTER_AREA on the device (n images, device pointers).
+ * Replaces fm_resize_fast (fastmario.cpp:641-649). */
+int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,132 @@
+"""GPU parity: the HIP path (libmario_hip.so through the C ABI) against the CPU oracle, bit for bit.
+
+Raw consoles: RAM, rendered screen and the full canonical machine state after every frame, on the
+synthetic workload ROM and on generated fuzz ROMs. Env level: stacked obs, rewards, terminated,
+truncated, info, RAM, final_obs, episode return/length and frame counts every step, across the
+wrapper configurations of the reference's fidelity tests (tests/test_fidelity_env.py:17-22) plus
+max-pool.
+"""
+import numpy as np
+import pytest
+from conftest import scaled
+
+import fuzz
+from build_roms import rom_path
+from cpu_libs import OracleRaw, OracleVec
+
+pytestmark = pytest.mark.gpu
+
+MINI = open(rom_path("vanilla"), "rb").read()
+
+
+def _first_diff(a, b):
+    d = np.flatnonzero(np.asarray(a).reshape(-1) != np.asarray(b).reshape(-1))
+    return d[:8].tolist()
+
+
+def _raw_run(rom, n, frames, seed, render_p=0.5, backup_p=0.0):
+    import torch
+
+    from fast_mario_env_amd import HipRawNES
+    gpu = HipRawNES(rom, n)
+    cpu = [OracleRaw(rom) for _ in range(n)]
+    rng = np.random.default_rng(seed)
+    buttons = np.zeros(n, np.uint8)
+    have = False
+    for f in range(frames):
+        ch = rng.random(n) < 0.15
+        buttons[ch] = rng.integers(0, 256, int(ch.sum()))
+        render = bool(rng.random() < render_p)
+        u = rng.random()
+        if u < backup_p:
+            gpu.backup(); [c.backup() for c in cpu]; have = True
+        elif u < 2 * backup_p and have:
+            gpu.restore(); [c.restore() for c in cpu]
+        gpu.frame(torch.from_numpy(buttons), render)
+        for i, c in enumerate(cpu):
+            c.frame(int(buttons[i]), render)
+        ram = gpu.ram.cpu().numpy()
+        canon = gpu.canon().cpu().numpy()
+        scr = gpu.screen.cpu().numpy() if render else None
+        for i, c in enumerate(cpu):
+            assert np.array_equal(ram[i], c.ram), (f, i, "ram", _first_diff(ram[i], c.ram))
+            assert np.array_equal(canon[i], c.canon()), (f, i, "canon", _first_diff(canon[i], c.canon()))
+            if render:
+                assert np.array_equal(scr[i], c.screen), (f, i, "screen", _first_diff(scr[i], c.screen))
+    assert gpu.bad_ops() == sum(c.bad_ops() for c in cpu)
+    assert gpu.instructions() == sum(c.instructions() for c in cpu)
+
+
+def test_raw_mini_smb():
+    _raw_run(MINI, 8, scaled(120), seed=1)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_raw_program_fuzz(seed):
+    _raw_run(fuzz.program_rom(seed), 4, scaled(80), seed=seed, backup_p=0.05)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_raw_random_fuzz(seed):
+    _raw_run(fuzz.random_rom(seed), 4, scaled(40), seed=seed, render_p=0.5, backup_p=0.05)
+
+
+CONFIGS = {
+    "default": dict(),
+    "sticky_noop": dict(sticky=0.25, noop_max=30),
+    "maxpool_sticky": dict(maxpool=True, sticky=0.25),
+    "short_timelimit": dict(max_steps=60, noop_max=5),
+    "headline": dict(sticky=0.25, noop_max=30, maxpool=True),
+}
+ACTION_P = [.05, .2, .25, .15, .25, .05, .05]
+
+
+def _levels(names):
+    from fast_mario_env_amd import decode_level
+    return [decode_level(x) for x in names]
+
+
+@pytest.mark.parametrize("config", list(CONFIGS))
+def test_env_vs_oracle(config):
+    import torch
+
+    from fast_mario_env_amd import HipVecEnv
+    kw = CONFIGS[config]
+    names = ["1-1", "1-1", "4-1", "8-4", "2-3", "1-2", "1-1", "5-2"]
+    n = len(names)
+    cpu = OracleVec(MINI, _levels(names), n, seed=7, **kw)
+    gpu = HipVecEnv(names, n, seed=7, rom=MINI, **kw)
+    o1 = cpu.reset().copy()
+    o2 = gpu.reset().cpu().numpy()
+    assert np.array_equal(o1, o2), "reset obs"
+    assert np.array_equal(gpu.canon().cpu().numpy(), np.stack([cpu.canon(i) for i in range(n)])), "reset state"
+    rng = np.random.default_rng(130)
+    eps = 0
+    for t in range(scaled(150)):
+        a = rng.choice(7, n, p=ACTION_P)
+        o1, r1, te1, tr1, i1 = cpu.step(a)
+        o2, r2, te2, tr2, i2 = gpu.step(torch.from_numpy(a).cuda())
+        o2, r2, te2, tr2, i2 = (x.cpu().numpy() for x in (o2, r2, te2, tr2, gpu.info_t))
+        assert np.array_equal(r1, r2), (t, "reward", r1, r2)
+        assert np.array_equal(te1, te2) and np.array_equal(tr1, tr2), (t, "done", te1, te2, tr1, tr2)
+        assert np.array_equal(i1, i2), (t, "info", i1, i2)
+        ram = gpu.ram().cpu().numpy()
+        for i in range(n):
+            assert np.array_equal(cpu.ram(i), ram[i]), (t, i, "ram", _first_diff(cpu.ram(i), ram[i]))
+        assert np.array_equal(o1, o2), (t, "obs", np.argwhere(o1 != o2)[:5].tolist())
+        done = te1 | tr1
+        if done.any():
+            fo = gpu.final_obs.cpu().numpy()
+            epr, epl = gpu.ep_ret.cpu().numpy(), gpu.ep_len.cpu().numpy()
+            for i in np.flatnonzero(done):
+                eps += 1
+                assert np.array_equal(cpu.fin[i], fo[i]), (t, i, "final_obs")
+                assert cpu.ep_ret[i] == epr[i] and cpu.ep_len[i] == epl[i], (t, i, "episode")
+    canon = gpu.canon().cpu().numpy()
+    for i in range(n):
+        assert np.array_equal(canon[i], cpu.canon(i)), (i, "final state", _first_diff(canon[i], cpu.canon(i)))
+    assert gpu.frames == cpu.frames()
+    assert gpu.bad_ops() == 0 and cpu.bad_ops() == 0
+    assert gpu.instructions() == cpu.instructions()
+    if config == "short_timelimit":
+        assert eps > 0
