@@ -1079,6 +1079,20 @@ void or_level_canon(void* h, int level, uint8_t* out) { canon(((Vec*)h)->levels[
 void or_level_obs(void* h, int level, uint8_t* out) { memcpy(out, ((Vec*)h)->levels[level]->obs0, kObs); }
 void or_destroy(void* h) { delete (Vec*)h; }
 
+void or_pcg_run(const uint64_t* st, const int64_t* ops, int n, uint64_t* out, uint64_t* state_out) {
+    Pcg g;
+    g.state = ((unsigned __int128)st[0] << 64) | st[1];
+    g.inc = ((unsigned __int128)st[2] << 64) | st[3];
+    g.has32 = (int)st[4];
+    g.half = (uint32_t)st[5];
+    for (int i = 0; i < n; i++) {
+        if (ops[i] == 0) { double d = g.random(); memcpy(&out[i], &d, 8); }
+        else out[i] = (uint64_t)g.integers(ops[i]);
+    }
+    state_out[0] = (uint64_t)(g.state >> 64); state_out[1] = (uint64_t)g.state;
+    state_out[2] = (uint64_t)(g.inc >> 64); state_out[3] = (uint64_t)g.inc;
+    state_out[4] = (uint64_t)g.has32; state_out[5] = g.half;
+}
 void or_palette(uint32_t* out) { memcpy(out, kPalette, sizeof(kPalette)); }
 void or_resize(const uint8_t* src, uint8_t* dst) { area_resize(src, dst); }
 int or_area_tab(int ssize, int dsize, int* di, int* si, float* alpha) {

@@ -65,6 +65,9 @@ void    or_level_obs(void* h, int level, uint8_t* out);   /* 84*84 boot observat
 void    or_destroy(void* h);
 
 /* ---- helpers ---- */
+/* PCG64 stream from the 6 state words; ops[i] = 0 -> out[i] = random() as double bits,
+ * ops[i] = h > 0 -> out[i] = integers(0, h). Lets tests compare the interleaved sequence with numpy. */
+void    or_pcg_run(const uint64_t* state6, const int64_t* ops, int n, uint64_t* out, uint64_t* state_out);
 void    or_palette(uint32_t* out);                       /* 64 x 0xRRGGBB */
 void    or_resize(const uint8_t* src, uint8_t* dst);     /* 240x256 -> 84x84 INTER_AREA */
 int     or_area_tab(int ssize, int dsize, int* di, int* si, float* alpha); /* returns entry count */

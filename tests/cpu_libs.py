@@ -53,6 +53,7 @@ def oracle() -> ctypes.CDLL:
         for f in ("or_env_ram", "or_env_canon", "or_env_gray", "or_level_canon", "or_level_obs"):
             getattr(L, f).argtypes = [_P, _i32, _P]
         L.or_palette.argtypes = [_P]
+        L.or_pcg_run.argtypes = [_P, _P, _i32, _P, _P]
         L.or_resize.argtypes = [_P, _P]
         L.or_area_tab.restype = _i32
         L.or_area_tab.argtypes = [_i32, _i32, _P, _P, _P]

@@ -1,0 +1,120 @@
+"""Host-side API and boundary checks that need no GPU (mirrors the reference's tests/test_api.py)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+from conftest import HAVE_GPU, ROOT
+
+import fast_mario_env_amd as fme
+from fast_mario_env_amd import _native, rom
+from build_roms import MODES, rom_path
+
+HEADER = os.path.join(ROOT, "include", "mario_hip.h")
+
+
+def test_decode_level():
+    """Known answers of the reference's test_api.py:10-18."""
+    assert fme.decode_level("1-1") == (1, 1, 1)
+    assert fme.decode_level("1-2") == (1, 2, 3)
+    assert fme.decode_level((4, 4)) == (4, 4, 5)
+    assert fme.decode_level("3-2") == (3, 2, 2)
+    assert fme.decode_level("8-4") == (8, 4, 4)
+    for bad in ("0-1", "9-1", "1-5", "x"):
+        with pytest.raises(ValueError):
+            fme.decode_level(bad)
+    assert len(fme.ALL_LEVELS) == 32 and fme.ALL_LEVELS[0] == "1-1" and fme.ALL_LEVELS[-1] == "8-4"
+
+
+def test_missing_rom_message(tmp_path, monkeypatch):
+    monkeypatch.setenv(fme.ROM_ENV_VAR, str(tmp_path / "nope.nes"))
+    with pytest.raises(fme.RomNotFoundError, match="does not ship a ROM"):
+        fme.find_rom()
+
+
+def test_rom_lookup_order(tmp_path, monkeypatch):
+    a, b = tmp_path / "a.nes", tmp_path / "b.nes"
+    data = open(rom_path("vanilla"), "rb").read()
+    a.write_bytes(data)
+    b.write_bytes(data)
+    monkeypatch.setenv(fme.ROM_ENV_VAR, str(b))
+    assert fme.find_rom(a) == str(a)            # rom_path wins over the environment variable
+    assert fme.find_rom() == str(b)
+    assert fme.load_rom() == data
+    with pytest.raises(ValueError):
+        fme.find_rom(a, rom_mode="nope")
+
+
+def test_bad_rom_rejected(tmp_path):
+    p = tmp_path / "bad.nes"
+    p.write_bytes(b"not a rom" * 100)
+    with pytest.raises(ValueError, match="iNES"):
+        fme.load_rom(p)
+    good = bytearray(open(rom_path("vanilla"), "rb").read())
+    good[6] |= 0x10                               # mapper 1
+    with pytest.raises(ValueError, match="unsupported"):
+        fme.check_rom(bytes(good))
+    with pytest.raises(ValueError, match="truncated"):
+        fme.check_rom(bytes(open(rom_path("vanilla"), "rb").read()[:30000]))
+
+
+def test_rom_file_table():
+    assert rom.ROM_FILES["vanilla"] == "super-mario-bros.nes"
+    assert set(rom.ROM_FILES) == set(MODES)
+
+
+def test_rng_state_words():
+    st = np.random.default_rng(5).bit_generator.state
+    w = fme.rng_state(5)
+    assert (w[0] << 64 | w[1]) == st["state"]["state"] and (w[2] << 64 | w[3]) == st["state"]["inc"]
+
+
+def _declared_symbols():
+    return sorted(set(re.findall(r"\b(mh_\w+)\s*\(", open(HEADER).read())))
+
+
+def test_library_exports_header():
+    """libmario_hip.so loads without a GPU and exports every entry point include/mario_hip.h declares."""
+    L = ctypes.CDLL(_native.lib_path())
+    syms = _declared_symbols()
+    assert len(syms) >= 25
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    L.mh_state_bytes.restype = ctypes.c_int64
+    assert L.mh_state_bytes() > 4384
+
+
+def test_bindings_cover_header():
+    src = open(os.path.join(ROOT, "fast-mario-env_amd", "fast_mario_env_amd", "_native.py")).read()
+    for s in _declared_symbols():
+        assert s in src, f"{s} has no ctypes binding"
+
+
+@pytest.mark.skipif(HAVE_GPU, reason="checks the no-GPU error path")
+def test_no_cpu_fallback():
+    """Without a GPU the product raises; there is no silent CPU path."""
+    with pytest.raises(RuntimeError, match="GPU"):
+        fme.HipVecEnv("1-1", 2, rom=open(rom_path("vanilla"), "rb").read())
+
+
+def test_resize_kernel_has_no_fma(tmp_path):
+    """The INTER_AREA float sums must not be contracted into FMAs (bit-exactness with the reference's
+    -ffp-contract=off build): compile the device code to gfx950 assembly and inspect the obs kernels."""
+    src = os.path.join(ROOT, "fast-mario-env_amd", "csrc", "mario_hip.hip")
+    out = tmp_path / "dev.s"
+    cmd = ["hipcc", "--offload-arch=gfx950", "--cuda-device-only", "-S", "-O3", "-std=c++17", "-ffp-contract=off",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", src, "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    asm = out.read_text()
+    checked = 0
+    for name in ("k_obs", "k_small_obs", "k_resize_images"):
+        m = re.search(rf"^(_Z\w*{name}\w*):[^\n]*$(.*?)^\s*s_endpgm", asm, re.S | re.M)
+        assert m, name
+        body = m.group(2)
+        assert "v_mul_f32" in body and "v_add_f32" in body
+        assert not re.search(r"\bv_(fma|fmac|mac|mad|pk_fma)\w*_f32", body), name
+        checked += 1
+    assert checked == 3
