@@ -1,0 +1,216 @@
+#!/usr/bin/env python
+"""Headline benchmark: batched Super Mario Bros agent steps on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--envs N] [--gpus 1]
+
+Workload: N = 32768 envs on level 1-1, sticky 0.25, no-op starts up to 30, skip 4, 2-frame max-pool,
+gray + INTER_AREA 84x84, frame stack 4, time limit 2000, auto-reset, seed 0 (env i: PCG64 stream i);
+actions uniform in {0..6}, pre-generated on the device from torch.Generator seed 0. The ROM is the
+real one when the reference's lookup finds it, else this repository's synthetic NROM stand-in
+(tests/golden/roms/mini_smb_vanilla.nes); the JSON line names which.
+
+One step = mh_step_async (snapshot copy, k_step, k_obs, k_reset, k_stack) on torch's current stream;
+inputs are resident in HBM. K steps are timed between two device synchronizations after W warm-up
+steps. Stage times come from HIP events recorded on the same stream. The reference C++ FastVecEnv
+(oracle/_ref, the checker build of the reference) is timed on the host cores on a bounded sample of
+the same workload and reported beside the GPU number.
+"""
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "fast-mario-env_amd"), os.path.join(ROOT, "tests"),
+           os.path.join(ROOT, "tests", "golden", "roms")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "agent env-steps/sec (skip=4) at 32768 envs on 1 MI355X; % HBM/VALU roofline"
+HBM_PEAK_GBS = 8000.0
+# bytes the kernels must move per env and agent step: console state read + write,
+# env words read + write, action, reward / term / trunc / info out; ep stats on episode end.
+STATE_BYTES = 4384 + 4 * 41
+ENV_WORD_BYTES = 4 * 30
+K_STEP_BYTES = 2 * STATE_BYTES + 2 * ENV_WORD_BYTES + 8 + 4 + 1 + 1 + 40
+K_STEP_DONE_BYTES = 12
+OBS = 84 * 84
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def pick_rom():
+    from fast_mario_env_amd import RomNotFoundError, load_rom
+    try:
+        data = load_rom()
+        return data, "super-mario-bros.nes (real ROM)"
+    except (RomNotFoundError, ValueError):
+        from build_roms import rom_path
+        path = rom_path("vanilla")
+        return open(path, "rb").read(), "mini_smb_vanilla.nes (synthetic NROM stand-in; no SMB ROM on this machine)"
+
+
+def traffic_from_profiles(workload_key):
+    """HBM bytes per k_step launch from the committed rocprofv3 --pmc summary, if one exists for this workload."""
+    path = os.path.join(ROOT, "profiles", "k_step_pmc_traffic.md")
+    if not os.path.isfile(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if ":" in line and line.strip().startswith("-"):
+            k, v = line.strip("- \n").split(":", 1)
+            vals[k.strip()] = v.strip()
+    if vals.get("workload") != workload_key:
+        return None
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(rom, seconds):
+    """The reference C++ thread pool (oracle/_ref) on the host cores, config-3 settings, bounded sample."""
+    import numpy as np
+
+    from cpu_libs import OracleVec, RefVec, have_ref
+    from fast_mario_env_amd import decode_level
+    cores = os.cpu_count() or 1
+    n = max(256, 32 * cores)
+    kw = dict(seed=0, sticky=0.25, noop_max=30, skip=4, maxpool=True, frame_stack=4, max_steps=2000)
+    lv = [decode_level("1-1")] * n
+    if have_ref():
+        env, kind, threads = RefVec(rom, lv, n, n_threads=cores, **kw), "reference", cores
+    else:
+        n = 64
+        env, kind, threads = OracleVec(rom, [decode_level("1-1")] * n, n, **kw), "port", 1
+    env.reset()
+    rng = np.random.default_rng(0)
+    for _ in range(3):
+        env.step(rng.integers(0, 7, n))
+    steps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        env.step(rng.integers(0, 7, n))
+        steps += 1
+    dt = time.perf_counter() - t0
+    env.close()
+    try:
+        load1 = os.getloadavg()[0]
+    except OSError:
+        load1 = None
+    model = ""
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"value": round(n * steps / dt, 1), "unit": "agent-steps/s", "cores": threads, "kind": kind,
+            "sample": f"{n} envs x {steps} timed steps after 3 warm-up steps ({dt:.1f} s), level 1-1, config-3 "
+                      f"wrapper settings; {model}; load1 {load1}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--envs", type=int, default=32768)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: every GPU box in this build has one GPU and the env step "
+              f"needs no collectives (envs shard by env_offset with zero exchange). Got --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from fast_mario_env_amd import HipVecEnv
+    rom, rom_name = pick_rom()
+    rom_sha = hashlib.sha1(rom).hexdigest()[:12]
+    n = args.envs
+    log(f"creating {n} envs on {torch.cuda.get_device_name(0)} ({rom_name})")
+    t0 = time.perf_counter()
+    env = HipVecEnv("1-1", n, seed=0, sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4,
+                    maxpool=True, rom=rom, device="cuda:0")
+    env.reset()
+    torch.cuda.synchronize()
+    log(f"boot + reset cache + reset: {time.perf_counter() - t0:.1f} s")
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(0)
+    acts = torch.randint(0, 7, (args.warmup + args.steps, n), generator=gen, device="cuda:0", dtype=torch.int64)
+    done_count = torch.zeros((), dtype=torch.int64, device="cuda:0")
+    for i in range(args.warmup):
+        env.step(acts[i])
+    torch.cuda.synchronize()
+    log(f"{args.warmup} warm-up steps done")
+    f0, i0 = env.frames, env.instructions()
+    env.timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        _, _, term, trunc, _ = env.step(acts[args.warmup + i])
+        done_count += (term | trunc).sum()
+        if (i + 1) % max(1, args.steps // 4) == 0:
+            torch.cuda.synchronize()
+            log(f"step {i + 1}/{args.steps}")
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    stages, timed = env.timing_read()
+    env.timing(False)
+    frames = env.frames - f0
+    instr = env.instructions() - i0
+    bad = env.bad_ops()
+    p_done = float(done_count.item()) / (n * args.steps)
+    value = n * args.steps / dt
+    k_step_ms = stages["k_step"] / max(1, timed)
+    workload = f"config3/{n}envs/1-1/rom:{rom_sha}"
+    k_bytes = n * (K_STEP_BYTES + K_STEP_DONE_BYTES * p_done)
+    achieved = k_bytes / (k_step_ms * 1e-3) / 1e9
+    traffic = traffic_from_profiles(workload)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "agent-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 3 (headline): full wrapper stack", "envs": n, "level": "1-1",
+                   "rom": rom_name, "rom_sha1": rom_sha, "sticky": 0.25, "noop_max": 30, "skip": 4, "maxpool": True,
+                   "frame_stack": 4, "max_steps": 2000, "seed": 0, "actions": "uniform {0..6}, torch.Generator seed 0"},
+        "roofline": {"bound": "hbm", "kernel": "k_step", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
+                     "traffic": traffic,
+                     "algorithmic_bytes_per_launch": round(k_bytes),
+                     "note": "k_step is bound by dependent VALU/LDS/memory latency per lane, not by HBM; "
+                             "VALU-issue utilization is in profiles/ (rocprofv3 SQ counters)"},
+        "stages_ms_per_step": {k: round(v / max(1, timed), 3) for k, v in stages.items()},
+        "p_done": round(p_done, 5),
+        "frames_per_step": round(frames / (n * args.steps), 3),
+        "instructions_per_step": round(instr / (n * args.steps), 1),
+        "emulated_instructions_per_s": round(instr / dt, 1),
+        "bad_ops": bad,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        out["cpu_baseline"] = cpu_baseline(rom, args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    env.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,346 @@
+// Per-lane bodies of the env kernels (one env / level / cache entry per lane). The __global__ wrappers
+// in mario_hip.hip stage the cartridge in LDS and call these.
+#pragma once
+#include <cmath>
+
+#include "env_device.hpp"
+
+namespace mh {
+
+constexpr int OBS_PIX = 84 * 84;
+constexpr int TAPS = 6;   // max area-filter taps per output row / column
+
+// ------------------------------------------------------------------ INTER_AREA tables
+// OpenCV computeResizeAreaTab in double precision (fastmario.cpp:83-100): per output index the source
+// indices and float weights, in the order the float sums are taken.
+struct AreaTables {
+    int32_t xs[84 * TAPS], ys[84 * TAPS];
+    float xw[84 * TAPS], yw[84 * TAPS];
+    int32_t xn[84], yn[84];
+};
+
+inline void area_taps(int ssize, int dsize, int32_t* idx, float* w, int32_t* cnt) {
+    double scale = 1.0 / ((double)dsize / ssize);
+    for (int d = 0; d < dsize; d++) cnt[d] = 0;
+    auto add = [&](int d, int s, float a) { idx[d * TAPS + cnt[d]] = s; w[d * TAPS + cnt[d]] = a; cnt[d]++; };
+    for (int d = 0; d < dsize; d++) {
+        double f1 = d * scale, f2 = f1 + scale;
+        double cell = scale < ssize - f1 ? scale : ssize - f1;
+        int s1 = (int)std::ceil(f1), s2 = (int)std::floor(f2);
+        if (s2 > ssize - 1) s2 = ssize - 1;
+        if (s1 > s2) s1 = s2;
+        if (s1 - f1 > 1e-3) add(d, s1 - 1, (float)((s1 - f1) / cell));
+        for (int s = s1; s < s2; s++) add(d, s, (float)(1.0 / cell));
+        if (f2 - s2 > 1e-3) {
+            double ww = f2 - s2 < 1.0 ? f2 - s2 : 1.0;
+            if (cell < ww) ww = cell;
+            add(d, s2, (float)(ww / cell));
+        }
+    }
+}
+
+inline void area_tables(AreaTables* T) {
+    memset(T, 0, sizeof(*T));
+    area_taps(256, 84, T->xs, T->xw, T->xn);
+    area_taps(240, 84, T->ys, T->yw, T->yn);
+}
+
+__device__ __forceinline__ uint8_t round_sat(float v) {
+    float r = __builtin_rintf(v);           // round half to even, like lrintf
+    int iv = (int)r;
+    return (uint8_t)(iv < 0 ? 0 : iv > 255 ? 255 : iv);
+}
+
+// INTER_AREA output pixel o of one image. g0/g1: pixel p at g[p * stride]; g1 == nullptr: no max-pool.
+__device__ __forceinline__ uint8_t area_pixel(const uint8_t* g0, const uint8_t* g1, uint32_t stride, int o,
+                                              const AreaTables* T) {
+    const int dy = o / 84, dx = o - dy * 84;
+    const int ny = T->yn[dy], nx = T->xn[dx];
+    float acc = 0.f;
+    for (int j = 0; j < ny; j++) {
+        const int sy = T->ys[dy * TAPS + j];
+        float row = 0.f;
+        for (int k = 0; k < nx; k++) {
+            const uint32_t p = (uint32_t)(sy * 256 + T->xs[dx * TAPS + k]);
+            uint8_t s = g0[(size_t)p * stride];
+            if (g1) { uint8_t s1 = g1[(size_t)p * stride]; s = s1 > s ? s1 : s; }
+            row += (float)s * T->xw[dx * TAPS + k];
+        }
+        const float term = T->yw[dy * TAPS + j] * row;
+        acc = j == 0 ? term : acc + term;
+    }
+    return round_sat(acc);
+}
+
+// ------------------------------------------------------------------ arguments
+struct RomArgs {
+    const uint8_t* rom;      // 0x8000 PRG (mirrored) + 0x2000 CHR
+    const uint8_t* lut;      // 256
+    uint16_t nt[4];
+};
+
+__device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom) {
+    Cart c;
+    c.prg = s_rom;
+    c.chr = s_rom + 0x8000;
+    for (int i = 0; i < 4; i++) c.nt[i] = R.nt[i];
+    return c;
+}
+
+struct BootArgs {
+    RomArgs R;
+    int nl;
+    uint32_t nlp;
+    const int* levels;           // 3 * nl
+    uint8_t* mem; uint32_t* sc;  // boot consoles [row * nlp + l]
+    uint8_t* gray;               // [pix * nlp + l]
+    int64_t* x0; int64_t* t0;
+    uint32_t* err;
+};
+
+struct CacheArgs {
+    RomArgs R;
+    Cfg cfg;
+    int nl, nk, nc;
+    uint32_t nlp, ncp;
+    const uint8_t* boot_mem; const uint32_t* boot_sc; const int64_t* x0; const int64_t* t0;
+    uint8_t* mem; uint32_t* sc;          // cache consoles [row * ncp + c]
+    uint8_t* snap_mem; uint32_t* snap_sc;
+    uint8_t* gray;                       // [(slot * GRAY_PIX + pix) * ncp + c]
+    int64_t* cx; int64_t* ct; int32_t* clives; int32_t* cdraws; uint8_t* cboot;
+    uint64_t* cframes; uint64_t* cinstr; uint32_t* cbad;
+};
+
+struct StepArgs {
+    RomArgs R;
+    Cfg cfg;
+    int n;
+    uint32_t np;
+    uint8_t* mem; uint32_t* sc;
+    uint8_t* snap_mem; uint32_t* snap_sc;
+    uint32_t* ev;                 // env words [w * np + e]
+    uint8_t* gray;                // [(slot * GRAY_PIX + pix) * np + e]
+    const int64_t* actions;
+    float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
+};
+
+struct ResetArgs {
+    int n; uint32_t np;
+    Cfg cfg;
+    int nk; uint32_t ncp;
+    uint8_t* mem; uint32_t* sc; uint32_t* ev;
+    const uint8_t* cmem; const uint32_t* csc;
+    const int64_t* cx; const int64_t* ct; const int32_t* clives; const int32_t* cdraws; const uint8_t* cboot;
+    const uint64_t* cframes; const uint64_t* cinstr; const uint32_t* cbad;
+    int all;
+};
+
+struct RawArgs {
+    RomArgs R;
+    int n; uint32_t np;
+    uint8_t* mem; uint32_t* sc;
+    uint8_t* screen;             // [pix * np + e], palette values
+    const uint8_t* buttons;      // n
+    int render;
+    uint32_t* bad; uint32_t* instr;
+    int power_on;
+};
+
+// ------------------------------------------------------------------ env words
+__device__ __forceinline__ void load_env(EnvRegs& ev, const uint32_t* E, uint32_t np, uint32_t e) {
+    auto w = [&](int k) { return E[(size_t)k * np + e]; };
+    ev.x_last = (int64_t)((uint64_t)w(E_XLAST_LO) | ((uint64_t)w(E_XLAST_HI) << 32));
+    ev.time_last = (int64_t)((uint64_t)w(E_TLAST_LO) | ((uint64_t)w(E_TLAST_HI) << 32));
+    ev.prev = (int)w(E_PREV); ev.lives = (int)w(E_LIVES); ev.t = (int)w(E_T); ev.ep_len = (int)w(E_EP_LEN);
+    uint64_t r = (uint64_t)w(E_EPRET_LO) | ((uint64_t)w(E_EPRET_HI) << 32);
+    ev.ep_ret = __longlong_as_double((long long)r);
+    ev.shows_boot = w(E_SHOWS_BOOT) != 0; ev.pooled = w(E_POOLED) != 0;
+    ev.frames = 0; ev.draws = 0;
+}
+__device__ __forceinline__ void store_env(const EnvRegs& ev, uint32_t* E, uint32_t np, uint32_t e) {
+    auto w = [&](int k, uint32_t v) { E[(size_t)k * np + e] = v; };
+    w(E_XLAST_LO, (uint32_t)ev.x_last); w(E_XLAST_HI, (uint32_t)((uint64_t)ev.x_last >> 32));
+    w(E_TLAST_LO, (uint32_t)ev.time_last); w(E_TLAST_HI, (uint32_t)((uint64_t)ev.time_last >> 32));
+    w(E_PREV, (uint32_t)ev.prev); w(E_LIVES, (uint32_t)ev.lives); w(E_T, (uint32_t)ev.t);
+    w(E_EP_LEN, (uint32_t)ev.ep_len);
+    uint64_t r = (uint64_t)__double_as_longlong(ev.ep_ret);
+    w(E_EPRET_LO, (uint32_t)r); w(E_EPRET_HI, (uint32_t)(r >> 32));
+    w(E_SHOWS_BOOT, ev.shows_boot); w(E_POOLED, ev.pooled);
+}
+__device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e, int lo_word, uint64_t add) {
+    uint64_t v = (uint64_t)E[(size_t)lo_word * np + e] | ((uint64_t)E[(size_t)(lo_word + 1) * np + e] << 32);
+    v += add;
+    E[(size_t)lo_word * np + e] = (uint32_t)v;
+    E[(size_t)(lo_word + 1) * np + e] = (uint32_t)(v >> 32);
+}
+
+// ------------------------------------------------------------------ lane bodies
+// Power-on and title sequence with the target level written into RAM (fastmario.cpp:414-445).
+__device__ inline void boot_lane(const BootArgs& A, const Cart& cart, const uint8_t* lut, int l) {
+    Console c;
+    c.mem = A.mem + l; c.np = A.nlp; c.cart = cart; c.lut = lut;
+    c.gray = A.gray + l; c.render = true; c.bad_ops = 0; c.instructions = 0;
+    c.power_on();
+    auto fr = [&](uint8_t b) { c.joy_buttons[0] = b; c.frame(); };
+    const int w = A.levels[3 * l], s = A.levels[3 * l + 1], ar = A.levels[3 * l + 2];
+    fr(8); fr(0);
+    int guard = 0;
+    while (smb_time(c) == 0) {
+        if (++guard > HACK_FRAME_LIMIT) { atomicOr(A.err, 1u); break; }
+        fr(8);
+        c.st(ROW_RAM + 0x75f, (uint8_t)(w - 1)); c.st(ROW_RAM + 0x75c, (uint8_t)(s - 1));
+        c.st(ROW_RAM + 0x760, (uint8_t)(ar - 1));
+        fr(0);
+        c.st(ROW_RAM + 0x7a0, 0);
+    }
+    int64_t tl = smb_time(c);
+    guard = 0;
+    while (smb_time(c) >= tl) {
+        if (++guard > HACK_FRAME_LIMIT) { atomicOr(A.err, 2u); break; }
+        tl = smb_time(c); fr(8); fr(0);
+    }
+    c.store(A.sc, l);
+    A.x0[l] = smb_x(c);
+    A.t0[l] = smb_time(c);
+}
+
+// Reset cache: the state after k no-op agent steps from the boot state of a level, k in 0..noop_max
+// (fastmario.cpp:389-401), restarting on termination like the reference. The sticky draws only choose
+// between action 0 and prev == 0, so their count is recorded, not their values.
+__device__ inline void cache_lane(const CacheArgs& A, const Cart& cart, const uint8_t* lut, int ci) {
+    const int lvl = ci / A.nk, k = ci - lvl * A.nk;
+    Region boot{(uint8_t*)A.boot_mem, (uint32_t*)A.boot_sc, A.nlp, (uint32_t)lvl};
+    Region live{A.mem, A.sc, A.ncp, (uint32_t)ci};
+    Region snap{A.snap_mem, A.snap_sc, A.ncp, (uint32_t)ci};
+    copy_console(live, boot);
+    Console c;
+    c.mem = A.mem + ci; c.np = A.ncp; c.cart = cart; c.lut = lut;
+    c.bad_ops = 0; c.instructions = 0;
+    c.load(A.sc, ci);
+    EnvRegs ev{};
+    ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
+    ev.prev = 0; ev.lives = -1; ev.shows_boot = true; ev.frames = 0; ev.draws = 0;
+    Stepper stp{c, ev, A.cfg, nullptr, A.gray + ci, A.gray + (size_t)GRAY_PIX * A.ncp + ci, live, snap, false};
+    for (int j = 0; j < k; j++) {
+        const bool want = j == k - 1;
+        if (want) { c.store(A.sc, ci); copy_console(snap, live); }
+        bool term;
+        stp.agent_step(0, want, &term);
+        if (term) {
+            copy_console(live, boot);
+            c.load(A.sc, ci);
+            ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
+            ev.prev = 0; ev.lives = -1; ev.shows_boot = true;
+        }
+    }
+    c.store(A.sc, ci);
+    A.cx[ci] = ev.x_last; A.ct[ci] = ev.time_last; A.clives[ci] = ev.lives;
+    A.cdraws[ci] = (int32_t)ev.draws; A.cboot[ci] = ev.shows_boot;
+    A.cframes[ci] = ev.frames; A.cinstr[ci] = c.instructions; A.cbad[ci] = c.bad_ops;
+}
+
+// One agent step of env e (fastmario.cpp:403-411 + 336-374).
+__device__ inline void step_lane(const StepArgs& A, const Cart& cart, const uint8_t* lut, uint32_t e) {
+    Console c;
+    c.mem = A.mem + e; c.np = A.np; c.cart = cart; c.lut = lut;
+    c.bad_ops = 0; c.instructions = 0;
+    c.load(A.sc, e);
+    EnvRegs ev;
+    load_env(ev, A.ev, A.np, e);
+    Pcg rng;
+    rng.load(A.ev, A.np, e);
+    int64_t a64 = A.actions[e];
+    const int act = (a64 >= 0 && a64 < 7) ? (int)a64 : 0;
+    Region live{A.mem, A.sc, A.np, e}, snap{A.snap_mem, A.snap_sc, A.np, e};
+    Stepper stp{c, ev, A.cfg, &rng, A.gray + e, A.gray + (size_t)GRAY_PIX * A.np + e, live, snap, true};
+    bool tm;
+    double r = stp.agent_step(act, true, &tm);
+    ev.t++;
+    const bool tr = ev.t >= A.cfg.max_steps;
+    ev.ep_ret += r; ev.ep_len++;
+    A.rew[e] = (float)r;
+    A.term[e] = tm;
+    A.trunc[e] = tr;
+    for (int k = 0; k < 10; k++) A.info[(size_t)e * 10 + k] = (int32_t)ev.info.v[k];
+    const bool done = tm || tr;
+    if (done) { A.ep_ret_out[e] = ev.ep_ret; A.ep_len_out[e] = ev.ep_len; }
+    c.store(A.sc, e);
+    store_env(ev, A.ev, A.np, e);
+    rng.store(A.ev, A.np, e);
+    A.ev[(size_t)E_DONE * A.np + e] = done;
+    add_counter(A.ev, A.np, e, E_FRAMES_LO, ev.frames);
+    add_counter(A.ev, A.np, e, E_INSTR_LO, c.instructions);
+    A.ev[(size_t)E_BAD * A.np + e] += c.bad_ops;
+}
+
+// Auto-reset (fastmario.cpp:389-401): k = integers(noop_max + 1) from the env's stream, the draws of
+// the k no-op steps are skipped, and the cached state of (level, k) is installed.
+__device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
+    uint32_t* E = A.ev;
+    const size_t np = A.np;
+    if (!A.all && !E[E_DONE * np + e]) { E[E_RESET_IDX * np + e] = 0xffffffffu; return; }
+    Pcg rng;
+    rng.load(E, A.np, e);
+    int k = 0;
+    if (A.cfg.noop_max) k = (int)rng.integers(A.cfg.noop_max + 1);
+    const int lvl = (int)E[E_LEVEL * np + e];
+    const int ci = lvl * A.nk + k;
+    if (A.cfg.sticky != 0.0)
+        for (int d = 0; d < A.cdraws[ci]; d++) rng.next64();
+    rng.store(E, A.np, e);
+    Region dst{A.mem, A.sc, A.np, e}, src{(uint8_t*)A.cmem, (uint32_t*)A.csc, A.ncp, (uint32_t)ci};
+    copy_console(dst, src);
+    EnvRegs ev{};
+    ev.x_last = A.cx[ci]; ev.time_last = A.ct[ci]; ev.lives = A.clives[ci]; ev.prev = 0;
+    ev.t = 0; ev.ep_len = 0; ev.ep_ret = 0.0; ev.shows_boot = A.cboot[ci] != 0; ev.pooled = false;
+    store_env(ev, E, A.np, e);
+    E[E_RESET_IDX * np + e] = (uint32_t)ci;
+    // the no-op steps count as emulated work, as on the reference CPU path
+    add_counter(E, A.np, e, E_FRAMES_LO, A.cframes[ci]);
+    add_counter(E, A.np, e, E_INSTR_LO, A.cinstr[ci]);
+    E[E_BAD * np + e] += A.cbad[ci];
+}
+
+// One nes-py frame of raw console e (fastmario.cpp:656-661); power_on != 0 boots it instead.
+__device__ inline void raw_lane(const RawArgs& A, const Cart& cart, const uint8_t* lut, uint32_t e) {
+    Console c;
+    c.mem = A.mem + e; c.np = A.np; c.cart = cart; c.lut = lut;
+    c.gray = A.screen + e; c.bad_ops = 0; c.instructions = 0;
+    if (A.power_on) {
+        c.power_on();
+    } else {
+        c.load(A.sc, e);
+        c.joy_buttons[0] = A.buttons[e];
+        c.render = A.render != 0;
+        c.frame();
+    }
+    c.store(A.sc, e);
+    A.bad[e] += c.bad_ops;
+    A.instr[e] += c.instructions;
+}
+
+// Canonical state dump of console e (layout in include/mario_hip.h).
+__device__ inline void canon_lane(const uint8_t* mem, const uint32_t* sc, uint32_t np, uint32_t e, uint8_t* o) {
+    auto w = [&](int k) { return sc[(size_t)k * np + e]; };
+    auto put = [&](int off, uint64_t v, int bytes) { for (int b = 0; b < bytes; b++) o[off + b] = (uint8_t)(v >> (8 * b)); };
+    for (int i = 0; i < 80; i++) o[i] = 0;
+    const uint64_t iter = (uint64_t)w(S_ITER_LO) | ((uint64_t)w(S_ITER_HI) << 32);
+    put(0, iter, 8);
+    put(8, iter + (int64_t)(int32_t)w(S_EXEC_REL), 8);
+    put(16, 3 * iter, 8);
+    put(24, w(S_PCYC), 4); put(28, w(S_SCANLINE), 4);
+    put(32, w(S_PC), 2); put(34, w(S_V), 2); put(36, w(S_T), 2); put(38, w(S_INC), 2);
+    const int order[] = {S_SP, S_A, S_X, S_Y, S_P, S_ZERO_SKIP, S_JOY_STROBE0, S_JOY_STROBE1, S_JOY_BUTTONS0,
+                         S_JOY_BUTTONS1, S_JOY_BITS0, S_JOY_BITS1, S_PSTATE, S_EVEN, S_VBLANK, S_S0HIT,
+                         S_FIRST_WRITE, S_DATA_BUFFER, S_OAM_ADDR, S_FINE_X, S_SHOW_BG, S_SHOW_SPR,
+                         S_HIDE_EDGE_BG, S_HIDE_EDGE_SPR, S_LONG_SPR, S_NMI_EN, S_BG_PAGE, S_SPR_PAGE, S_NSL};
+    for (int i = 0; i < 29; i++) o[40 + i] = (uint8_t)w(order[i]);
+    const uint32_t nsl = w(S_NSL);
+    const uint64_t sl = (uint64_t)w(S_SL_LO) | ((uint64_t)w(S_SL_HI) << 32);
+    for (uint32_t i = 0; i < 8; i++) o[69 + i] = i < nsl ? (uint8_t)(sl >> (8 * i)) : 0;
+    const uint32_t rows[4][3] = {{80, ROW_OAM, 256}, {336, ROW_PAL, 32}, {368, ROW_VRAM, 2048}, {2416, ROW_RAM, 2048}};
+    for (int k = 0; k < 4; k++)
+        for (uint32_t i = 0; i < rows[k][2]; i++) o[rows[k][0] + i] = mem[(size_t)(rows[k][1] + i) * np + e];
+}
+
+}  // namespace mh

@@ -1,6 +1,6 @@
 // mario_hip: batched Super Mario Bros env stepping on gfx950 — kernels and the C-ABI (include/mario_hip.h).
 //
-// One agent step of N envs is four launches on the caller's stream:
+// One agent step of N envs is five stages on the caller's stream:
 //   hipMemcpyAsync  MEM/SC -> SNAP         step-start snapshot (early termination re-renders from it)
 //   k_step          one lane per env: sticky draw, K frames of 6502 + catch-up PPU, reward/done/info,
 //                   hack frames, gray rendering of the observed frame(s) into GRAY (lane-interleaved)
@@ -9,57 +9,17 @@
 //   k_stack         LDS-transposed frame-stack shift, final_obs, reset observation
 #include <hip/hip_runtime.h>
 
-#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
 #include <vector>
 
 #include "../../include/mario_hip.h"
-#include "env_device.hpp"
+#include "lane_kernels.hpp"
 
 using namespace mh;
 
 namespace {
-
-constexpr int OBS_PIX = 84 * 84;
-constexpr int TAPS = 6;                  // max area-filter taps per output row / column
-
-// ------------------------------------------------------------------ INTER_AREA tables (host)
-// OpenCV computeResizeAreaTab in double precision (fastmario.cpp:83-100): per output index the
-// source indices and float weights in the order the float sums are taken.
-struct AreaTables {
-    int32_t xs[84 * TAPS], ys[84 * TAPS];
-    float xw[84 * TAPS], yw[84 * TAPS];
-    int32_t xn[84], yn[84];
-};
-
-static void area_taps(int ssize, int dsize, int32_t* idx, float* w, int32_t* cnt) {
-    double scale = 1.0 / ((double)dsize / ssize);
-    for (int d = 0; d < dsize; d++) cnt[d] = 0;
-    auto add = [&](int d, int s, float a) { idx[d * TAPS + cnt[d]] = s; w[d * TAPS + cnt[d]] = a; cnt[d]++; };
-    for (int d = 0; d < dsize; d++) {
-        double f1 = d * scale, f2 = f1 + scale;
-        double cell = scale < ssize - f1 ? scale : ssize - f1;
-        int s1 = (int)std::ceil(f1), s2 = (int)std::floor(f2);
-        if (s2 > ssize - 1) s2 = ssize - 1;
-        if (s1 > s2) s1 = s2;
-        if (s1 - f1 > 1e-3) add(d, s1 - 1, (float)((s1 - f1) / cell));
-        for (int s = s1; s < s2; s++) add(d, s, (float)(1.0 / cell));
-        if (f2 - s2 > 1e-3) {
-            double ww = f2 - s2 < 1.0 ? f2 - s2 : 1.0;
-            if (cell < ww) ww = cell;
-            add(d, s2, (float)(ww / cell));
-        }
-    }
-}
-
-// ------------------------------------------------------------------ device helpers
-struct RomArgs {
-    const uint8_t* rom;      // 0x8000 PRG (mirrored) + 0x2000 CHR, device
-    const uint8_t* lut;      // 256, device
-    uint16_t nt[4];
-};
 
 // Stage PRG + CHR (40 KB) and the gray LUT in LDS; every thread of the block must call this.
 __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint8_t* s_lut) {
@@ -70,138 +30,41 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
     __syncthreads();
 }
 
-__device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom) {
-    Cart c;
-    c.prg = s_rom;
-    c.chr = s_rom + 0x8000;
-    for (int i = 0; i < 4; i++) c.nt[i] = R.nt[i];
-    return c;
-}
-
-__device__ __forceinline__ uint8_t round_sat(float v) {
-    float r = __builtin_rintf(v);           // round half to even, like lrintf
-    int iv = (int)r;
-    return (uint8_t)(iv < 0 ? 0 : iv > 255 ? 255 : iv);
-}
-
-// INTER_AREA output pixel o of one image. g0/g1: pixel p at g[p * stride]; g1 == nullptr: no max-pool.
-__device__ __forceinline__ uint8_t area_pixel(const uint8_t* g0, const uint8_t* g1, uint32_t stride, int o,
-                                              const AreaTables* T) {
-    const int dy = o / 84, dx = o - dy * 84;
-    const int ny = T->yn[dy], nx = T->xn[dx];
-    float acc = 0.f;
-    for (int j = 0; j < ny; j++) {
-        const int sy = T->ys[dy * TAPS + j];
-        float row = 0.f;
-        for (int k = 0; k < nx; k++) {
-            const uint32_t p = (uint32_t)(sy * 256 + T->xs[dx * TAPS + k]);
-            uint8_t s = g0[(size_t)p * stride];
-            if (g1) { uint8_t s1 = g1[(size_t)p * stride]; s = s1 > s ? s1 : s; }
-            row += (float)s * T->xw[dx * TAPS + k];
-        }
-        const float term = T->yw[dy * TAPS + j] * row;
-        acc = j == 0 ? term : acc + term;
-    }
-    return round_sat(acc);
-}
-
-// ------------------------------------------------------------------ kernels
-struct BootArgs {
-    RomArgs R;
-    int nl;
-    uint32_t nlp;
-    const int* levels;       // 3 * nl
-    uint8_t* mem; uint32_t* sc;  // boot consoles [row * nlp + l]
-    uint8_t* gray;           // [pix * nlp + l]
-    int64_t* x0; int64_t* t0;
-    uint32_t* err;
-};
-
-// Power-on and title sequence with the target level written into RAM (fastmario.cpp:414-445).
-__global__ void __launch_bounds__(64) k_boot(BootArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
+#define ROM_LDS                                                     \
+    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000]; \
     __shared__ uint8_t s_lut[256];
+
+__global__ void __launch_bounds__(64) k_boot(BootArgs A) {
+    ROM_LDS
     stage_rom(A.R, s_rom, s_lut);
     const int l = blockIdx.x * blockDim.x + threadIdx.x;
-    if (l >= A.nl) return;
-    Console c;
-    c.mem = A.mem + l; c.np = A.nlp; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
-    c.gray = A.gray + l; c.render = true; c.bad_ops = 0; c.instructions = 0;
-    c.power_on();
-    auto fr = [&](uint8_t b) { c.joy_buttons[0] = b; c.frame(); };
-    const int w = A.levels[3 * l], s = A.levels[3 * l + 1], ar = A.levels[3 * l + 2];
-    fr(8); fr(0);
-    int guard = 0;
-    while (smb_time(c) == 0) {
-        if (++guard > HACK_FRAME_LIMIT) { atomicOr(A.err, 1u); break; }
-        fr(8);
-        c.st(ROW_RAM + 0x75f, (uint8_t)(w - 1)); c.st(ROW_RAM + 0x75c, (uint8_t)(s - 1));
-        c.st(ROW_RAM + 0x760, (uint8_t)(ar - 1));
-        fr(0);
-        c.st(ROW_RAM + 0x7a0, 0);
-    }
-    int64_t tl = smb_time(c);
-    guard = 0;
-    while (smb_time(c) >= tl) {
-        if (++guard > HACK_FRAME_LIMIT) { atomicOr(A.err, 2u); break; }
-        tl = smb_time(c); fr(8); fr(0);
-    }
-    c.store(A.sc, l);
-    A.x0[l] = smb_x(c);
-    A.t0[l] = smb_time(c);
+    if (l < A.nl) boot_lane(A, make_cart(A.R, s_rom), s_lut, l);
 }
 
-struct CacheArgs {
-    RomArgs R;
-    Cfg cfg;
-    int nl, nk, nc;
-    uint32_t nlp, ncp;
-    const uint8_t* boot_mem; const uint32_t* boot_sc; const int64_t* x0; const int64_t* t0;
-    uint8_t* mem; uint32_t* sc;          // cache consoles [row * ncp + c]
-    uint8_t* snap_mem; uint32_t* snap_sc;
-    uint8_t* gray;                       // [(slot * GRAY_PIX + pix) * ncp + c]
-    int64_t* cx; int64_t* ct; int32_t* clives; int32_t* cdraws; uint8_t* cboot;
-    uint64_t* cframes; uint64_t* cinstr; uint32_t* cbad;
-};
-
-// Reset cache: the state after k no-op agent steps from the boot state of a level, for k in
-// 0..noop_max (fastmario.cpp:389-401). Restarts on termination exactly like the reference; the
-// sticky draws only decide between action 0 and prev == 0, so their count is recorded, not their values.
 __global__ void __launch_bounds__(64) k_cache(CacheArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
-    __shared__ uint8_t s_lut[256];
+    ROM_LDS
     stage_rom(A.R, s_rom, s_lut);
     const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci >= A.nc) return;
-    const int lvl = ci / A.nk, k = ci - lvl * A.nk;
-    Region boot{(uint8_t*)A.boot_mem, (uint32_t*)A.boot_sc, A.nlp, (uint32_t)lvl};
-    Region live{A.mem, A.sc, A.ncp, (uint32_t)ci};
-    Region snap{A.snap_mem, A.snap_sc, A.ncp, (uint32_t)ci};
-    copy_console(live, boot);
-    Console c;
-    c.mem = A.mem + ci; c.np = A.ncp; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
-    c.bad_ops = 0; c.instructions = 0;
-    c.load(A.sc, ci);
-    EnvRegs ev{};
-    ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
-    ev.prev = 0; ev.lives = -1; ev.shows_boot = true; ev.frames = 0; ev.draws = 0;
-    Stepper stp{c, ev, A.cfg, nullptr, A.gray + ci, A.gray + (size_t)GRAY_PIX * A.ncp + ci, live, snap, false};
-    for (int j = 0; j < k; j++) {
-        const bool want = j == k - 1;
-        if (want) { c.store(A.sc, ci); copy_console(snap, live); }
-        bool term;
-        stp.agent_step(0, want, &term);
-        if (term) {
-            copy_console(live, boot);
-            c.load(A.sc, ci);
-            ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
-            ev.prev = 0; ev.lives = -1; ev.shows_boot = true;
-        }
-    }
-    c.store(A.sc, ci);
-    A.cx[ci] = ev.x_last; A.ct[ci] = ev.time_last; A.clives[ci] = ev.lives;
-    A.cdraws[ci] = (int32_t)ev.draws; A.cboot[ci] = ev.shows_boot;
-    A.cframes[ci] = ev.frames; A.cinstr[ci] = c.instructions; A.cbad[ci] = c.bad_ops;
+    if (ci < A.nc) cache_lane(A, make_cart(A.R, s_rom), s_lut, ci);
+}
+
+__global__ void __launch_bounds__(64) k_step(StepArgs A) {
+    ROM_LDS
+    stage_rom(A.R, s_rom, s_lut);
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < (uint32_t)A.n) step_lane(A, make_cart(A.R, s_rom), s_lut, e);
+}
+
+__global__ void __launch_bounds__(64) k_raw(RawArgs A) {
+    ROM_LDS
+    stage_rom(A.R, s_rom, s_lut);
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < (uint32_t)A.n) raw_lane(A, make_cart(A.R, s_rom), s_lut, e);
+}
+
+__global__ void __launch_bounds__(64) k_reset(ResetArgs A) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < (uint32_t)A.n) reset_lane(A, e);
 }
 
 // Observation of a reset-cache entry or a boot state: the boot observation, or the resized last frame.
@@ -222,85 +85,6 @@ __global__ void k_small_obs(SmallObsArgs A) {
     A.out[(size_t)i * OBS_PIX + o] = v;
 }
 
-struct StepArgs {
-    RomArgs R;
-    Cfg cfg;
-    int n;
-    uint32_t np;
-    uint8_t* mem; uint32_t* sc;
-    uint8_t* snap_mem; uint32_t* snap_sc;
-    uint32_t* ev;                 // env words [w * np + e]
-    uint8_t* gray;                // [(slot * GRAY_PIX + pix) * np + e]
-    const int64_t* actions;
-    float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
-};
-
-__device__ __forceinline__ void load_env(EnvRegs& ev, const uint32_t* E, uint32_t np, uint32_t e) {
-    auto w = [&](int k) { return E[(size_t)k * np + e]; };
-    ev.x_last = (int64_t)((uint64_t)w(E_XLAST_LO) | ((uint64_t)w(E_XLAST_HI) << 32));
-    ev.time_last = (int64_t)((uint64_t)w(E_TLAST_LO) | ((uint64_t)w(E_TLAST_HI) << 32));
-    ev.prev = (int)w(E_PREV); ev.lives = (int)w(E_LIVES); ev.t = (int)w(E_T); ev.ep_len = (int)w(E_EP_LEN);
-    uint64_t r = (uint64_t)w(E_EPRET_LO) | ((uint64_t)w(E_EPRET_HI) << 32);
-    ev.ep_ret = __longlong_as_double((long long)r);
-    ev.shows_boot = w(E_SHOWS_BOOT) != 0; ev.pooled = w(E_POOLED) != 0;
-    ev.frames = 0; ev.draws = 0;
-}
-__device__ __forceinline__ void store_env(const EnvRegs& ev, uint32_t* E, uint32_t np, uint32_t e) {
-    auto w = [&](int k, uint32_t v) { E[(size_t)k * np + e] = v; };
-    w(E_XLAST_LO, (uint32_t)ev.x_last); w(E_XLAST_HI, (uint32_t)((uint64_t)ev.x_last >> 32));
-    w(E_TLAST_LO, (uint32_t)ev.time_last); w(E_TLAST_HI, (uint32_t)((uint64_t)ev.time_last >> 32));
-    w(E_PREV, (uint32_t)ev.prev); w(E_LIVES, (uint32_t)ev.lives); w(E_T, (uint32_t)ev.t);
-    w(E_EP_LEN, (uint32_t)ev.ep_len);
-    uint64_t r = (uint64_t)__double_as_longlong(ev.ep_ret);
-    w(E_EPRET_LO, (uint32_t)r); w(E_EPRET_HI, (uint32_t)(r >> 32));
-    w(E_SHOWS_BOOT, ev.shows_boot); w(E_POOLED, ev.pooled);
-}
-__device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e, int lo_word, uint64_t add) {
-    uint64_t v = (uint64_t)E[(size_t)lo_word * np + e] | ((uint64_t)E[(size_t)(lo_word + 1) * np + e] << 32);
-    v += add;
-    E[(size_t)lo_word * np + e] = (uint32_t)v;
-    E[(size_t)(lo_word + 1) * np + e] = (uint32_t)(v >> 32);
-}
-
-// One agent step of every env (fastmario.cpp:403-411 + 336-374).
-__global__ void __launch_bounds__(64) k_step(StepArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
-    __shared__ uint8_t s_lut[256];
-    stage_rom(A.R, s_rom, s_lut);
-    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (uint32_t)A.n) return;
-    Console c;
-    c.mem = A.mem + e; c.np = A.np; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
-    c.bad_ops = 0; c.instructions = 0;
-    c.load(A.sc, e);
-    EnvRegs ev;
-    load_env(ev, A.ev, A.np, e);
-    Pcg rng;
-    rng.load(A.ev, A.np, e);
-    int64_t a64 = A.actions[e];
-    const int act = (a64 >= 0 && a64 < 7) ? (int)a64 : 0;
-    Region live{A.mem, A.sc, A.np, e}, snap{A.snap_mem, A.snap_sc, A.np, e};
-    Stepper stp{c, ev, A.cfg, &rng, A.gray + e, A.gray + (size_t)GRAY_PIX * A.np + e, live, snap, true};
-    bool tm;
-    double r = stp.agent_step(act, true, &tm);
-    ev.t++;
-    const bool tr = ev.t >= A.cfg.max_steps;
-    ev.ep_ret += r; ev.ep_len++;
-    A.rew[e] = (float)r;
-    A.term[e] = tm;
-    A.trunc[e] = tr;
-    for (int k = 0; k < 10; k++) A.info[(size_t)e * 10 + k] = (int32_t)ev.info.v[k];
-    const bool done = tm || tr;
-    if (done) { A.ep_ret_out[e] = ev.ep_ret; A.ep_len_out[e] = ev.ep_len; }
-    c.store(A.sc, e);
-    store_env(ev, A.ev, A.np, e);
-    rng.store(A.ev, A.np, e);
-    A.ev[(size_t)E_DONE * A.np + e] = done;
-    add_counter(A.ev, A.np, e, E_FRAMES_LO, ev.frames);
-    add_counter(A.ev, A.np, e, E_INSTR_LO, c.instructions);
-    A.ev[(size_t)E_BAD * A.np + e] += c.bad_ops;
-}
-
 struct ObsArgs {
     int n; uint32_t np;
     const uint32_t* ev;
@@ -309,7 +93,7 @@ struct ObsArgs {
     uint8_t* out;                 // [o * np + e]
     const AreaTables* T;
 };
-// New observation of every env: boot observation right after a reset, else INTER_AREA of the last
+// New observation of every env: the boot observation right after a reset, else INTER_AREA of the last
 // frame, max-pooled with its partner frame (fastmario.cpp:377-386). Threads: x = env, y = pixel.
 __global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
     const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
@@ -325,46 +109,6 @@ __global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
     A.out[(size_t)o * A.np + e] = v;
 }
 
-struct ResetArgs {
-    int n; uint32_t np;
-    Cfg cfg;
-    int nk; uint32_t ncp;
-    uint8_t* mem; uint32_t* sc; uint32_t* ev;
-    const uint8_t* cmem; const uint32_t* csc;
-    const int64_t* cx; const int64_t* ct; const int32_t* clives; const int32_t* cdraws; const uint8_t* cboot;
-    const uint64_t* cframes; const uint64_t* cinstr; const uint32_t* cbad;
-    int all;
-};
-// Auto-reset (fastmario.cpp:389-401): k = integers(noop_max + 1) from the env's stream, the draws the
-// k no-op steps would take are skipped, and the cached state of (level, k) is installed.
-__global__ void __launch_bounds__(64) k_reset(ResetArgs A) {
-    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (uint32_t)A.n) return;
-    uint32_t* E = A.ev;
-    const size_t np = A.np;
-    if (!A.all && !E[E_DONE * np + e]) { E[E_RESET_IDX * np + e] = 0xffffffffu; return; }
-    Pcg rng;
-    rng.load(E, A.np, e);
-    int k = 0;
-    if (A.cfg.noop_max) k = (int)rng.integers(A.cfg.noop_max + 1);
-    const int lvl = (int)E[E_LEVEL * np + e];
-    const int ci = lvl * A.nk + k;
-    if (A.cfg.sticky != 0.0)
-        for (int d = 0; d < A.cdraws[ci]; d++) rng.next64();
-    rng.store(E, A.np, e);
-    Region dst{A.mem, A.sc, A.np, e}, src{(uint8_t*)A.cmem, (uint32_t*)A.csc, A.ncp, (uint32_t)ci};
-    copy_console(dst, src);
-    EnvRegs ev{};
-    ev.x_last = A.cx[ci]; ev.time_last = A.ct[ci]; ev.lives = A.clives[ci]; ev.prev = 0;
-    ev.t = 0; ev.ep_len = 0; ev.ep_ret = 0.0; ev.shows_boot = A.cboot[ci] != 0; ev.pooled = false;
-    store_env(ev, E, A.np, e);
-    E[E_RESET_IDX * np + e] = (uint32_t)ci;
-    // the no-op steps count as emulated work, as on the reference CPU path
-    add_counter(E, A.np, e, E_FRAMES_LO, A.cframes[ci]);
-    add_counter(E, A.np, e, E_INSTR_LO, A.cinstr[ci]);
-    E[E_BAD * np + e] += A.cbad[ci];
-}
-
 struct StackArgs {
     int n; uint32_t np; int K;
     uint8_t* obs; uint8_t* fin;   // [e][K][OBS_PIX]
@@ -373,14 +117,13 @@ struct StackArgs {
     const uint8_t* cobs;          // [ci * OBS_PIX + o]
     int mode;                     // 0 step, 1 reset
 };
-// Frame stack, final_obs, reset observation (fastmario.cpp:477-504). Block: 64 envs x 64 words of
-// one frame; the fresh frame is read lane-interleaved and transposed through LDS.
+// Frame stack, final_obs, reset observation (fastmario.cpp:477-504). Block: 64 envs x 64 words of one
+// frame; the fresh frame is read lane-interleaved and transposed through LDS.
 __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
     __shared__ uint32_t tile[64][65];
     const uint32_t e0 = blockIdx.y * 64;
     const int w0 = blockIdx.x * 64;             // word index within a frame (OBS_PIX / 4 = 1764 words)
     const int nw = OBS_PIX / 4;
-    // fresh bytes: 256 byte rows (4 per word) x 64 envs
     if (A.mode == 0) {
         for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
             const int wl = idx >> 6, j = idx & 63;
@@ -393,7 +136,7 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
         }
     }
     __syncthreads();
-    const size_t fw = (size_t)OBS_PIX / 4 * A.K;   // words per env stack
+    const size_t fw = (size_t)nw * A.K;   // words per env stack
     for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
         const int j = idx >> 6, wl = idx & 63;
         const uint32_t e = e0 + j;
@@ -419,72 +162,17 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
     }
 }
 
-// Canonical state dump (layout in include/mario_hip.h): one thread per console.
 __global__ void k_canon(const uint8_t* mem, const uint32_t* sc, uint32_t np, int n, uint8_t* out) {
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (uint32_t)n) return;
-    uint8_t* o = out + (size_t)e * MH_CANON_BYTES;
-    auto w = [&](int k) { return sc[(size_t)k * np + e]; };
-    auto put = [&](int off, uint64_t v, int bytes) { for (int b = 0; b < bytes; b++) o[off + b] = (uint8_t)(v >> (8 * b)); };
-    for (int i = 0; i < 80; i++) o[i] = 0;
-    const uint64_t iter = (uint64_t)w(S_ITER_LO) | ((uint64_t)w(S_ITER_HI) << 32);
-    put(0, iter, 8);
-    put(8, iter + (int64_t)(int32_t)w(S_EXEC_REL), 8);
-    put(16, 3 * iter, 8);
-    put(24, w(S_PCYC), 4); put(28, w(S_SCANLINE), 4);
-    put(32, w(S_PC), 2); put(34, w(S_V), 2); put(36, w(S_T), 2); put(38, w(S_INC), 2);
-    const int order[] = {S_SP, S_A, S_X, S_Y, S_P, S_ZERO_SKIP, S_JOY_STROBE0, S_JOY_STROBE1, S_JOY_BUTTONS0,
-                         S_JOY_BUTTONS1, S_JOY_BITS0, S_JOY_BITS1, S_PSTATE, S_EVEN, S_VBLANK, S_S0HIT,
-                         S_FIRST_WRITE, S_DATA_BUFFER, S_OAM_ADDR, S_FINE_X, S_SHOW_BG, S_SHOW_SPR,
-                         S_HIDE_EDGE_BG, S_HIDE_EDGE_SPR, S_LONG_SPR, S_NMI_EN, S_BG_PAGE, S_SPR_PAGE, S_NSL};
-    for (int i = 0; i < 29; i++) o[40 + i] = (uint8_t)w(order[i]);
-    const uint32_t nsl = w(S_NSL);
-    const uint64_t sl = (uint64_t)w(S_SL_LO) | ((uint64_t)w(S_SL_HI) << 32);
-    for (uint32_t i = 0; i < 8; i++) o[69 + i] = i < nsl ? (uint8_t)(sl >> (8 * i)) : 0;
-    const uint32_t rows[4][3] = {{80, ROW_OAM, 256}, {336, ROW_PAL, 32}, {368, ROW_VRAM, 2048}, {2416, ROW_RAM, 2048}};
-    for (int k = 0; k < 4; k++)
-        for (uint32_t i = 0; i < rows[k][2]; i++) o[rows[k][0] + i] = mem[(size_t)(rows[k][1] + i) * np + e];
+    if (e < (uint32_t)n) canon_lane(mem, sc, np, e, out + (size_t)e * MH_CANON_BYTES);
 }
 
-// RAM of every console, env-major (n x 2048). Threads: x = env, y = address.
-__global__ void k_ram_out(const uint8_t* mem, uint32_t np, int n, uint8_t* out) {
+// Lane-interleaved rows -> env-major (n x rows). Threads: x = env, y = row.
+__global__ void k_rows_out(const uint8_t* src, uint32_t np, int n, uint32_t rows, uint8_t* out) {
     const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
-    const uint32_t ad = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (e >= (uint32_t)n || ad >= 2048) return;
-    out[(size_t)e * 2048 + ad] = mem[(size_t)(ROW_RAM + ad) * np + e];
-}
-
-struct RawArgs {
-    RomArgs R;
-    int n; uint32_t np;
-    uint8_t* mem; uint32_t* sc;
-    uint8_t* screen;             // [pix * np + e], palette values
-    const uint8_t* buttons;      // n
-    int render;
-    uint32_t* bad; uint32_t* instr;   // per env accumulators
-    int power_on;
-};
-// One nes-py frame of every raw console (fastmario.cpp:656-661); power_on != 0 boots them instead.
-__global__ void __launch_bounds__(64) k_raw(RawArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000];
-    __shared__ uint8_t s_lut[256];
-    stage_rom(A.R, s_rom, s_lut);
-    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (uint32_t)A.n) return;
-    Console c;
-    c.mem = A.mem + e; c.np = A.np; c.cart = make_cart(A.R, s_rom); c.lut = s_lut;
-    c.gray = A.screen + e; c.bad_ops = 0; c.instructions = 0;
-    if (A.power_on) {
-        c.power_on();
-    } else {
-        c.load(A.sc, e);
-        c.joy_buttons[0] = A.buttons[e];
-        c.render = A.render != 0;
-        c.frame();
-    }
-    c.store(A.sc, e);
-    A.bad[e] += c.bad_ops;
-    A.instr[e] += c.instructions;
+    const uint32_t r = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (e >= (uint32_t)n || r >= rows) return;
+    out[(size_t)e * rows + r] = src[(size_t)r * np + e];
 }
 
 // 240x256 gray images (env-major) -> 84x84.
@@ -563,6 +251,17 @@ struct MhEnv {
     float* rew = nullptr;
     int32_t *info = nullptr, *ep_len = nullptr;
     double* ep_ret = nullptr;
+    // per-stage HIP event timing of mh_step_async (mh_timing / mh_timing_read)
+    bool timing = false;
+    std::vector<hipEvent_t> events;    // MH_STAGES + 1 events per timed step
+    size_t timed_steps = 0;
+    ~MhEnv() { for (hipEvent_t e : events) (void)hipEventDestroy(e); }
+
+    ResetArgs reset_args(int all) const {
+        return ResetArgs{n, np, cfg, nk, ncp, mem, sc, ev, cmem, csc, cx, ct, clives, cdraws, cboot,
+                         cframes, cinstr, cbad, all};
+    }
+    StackArgs stack_args(int mode) const { return StackArgs{n, np, K, obs, fin, fresh, ev, cobs, mode}; }
 };
 
 struct MhRaw {
@@ -592,6 +291,7 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
     if (!load_cart(rom, rom_len, img, nt)) return nullptr;
     CKN(hipSetDevice(device));
     MhEnv* h = new MhEnv();
+    auto fail = [&]() -> MhEnv* { delete h; return nullptr; };
     bool good = true;
     h->n = n; h->K = frame_stack; h->device = device; h->np = pad64(n);
     h->cfg = Cfg{skip, max_steps, noop_max, maxpool ? 1 : 0, sticky};
@@ -635,12 +335,9 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
     h->cframes = B.alloc<uint64_t>(h->nc, good); h->cinstr = B.alloc<uint64_t>(h->nc, good);
     h->cbad = B.alloc<uint32_t>(h->nc, good);
     uint32_t* d_err = B.alloc<uint32_t>(1, good);
-    if (!good) { delete h; return nullptr; }
-    // tables
+    if (!good) return fail();
     AreaTables T;
-    memset(&T, 0, sizeof(T));
-    area_taps(256, 84, T.xs, T.xw, T.xn);
-    area_taps(240, 84, T.ys, T.yw, T.yn);
+    area_tables(&T);
     // per-env words: level, RNG, lives = -1 (reset() installs the real start state)
     std::vector<uint32_t> ev((size_t)E_COUNT * h->np, 0);
     for (int i = 0; i < n; i++) {
@@ -654,7 +351,6 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
         w(E_RNG_HAS32) = (uint32_t)r[4]; w(E_RNG_HALF) = (uint32_t)r[5];
         w(E_LIVES) = 0xffffffffu; w(E_SHOWS_BOOT) = 1; w(E_RESET_IDX) = 0xffffffffu;
     }
-    auto fail = [&]() -> MhEnv* { delete h; return nullptr; };
     if (!ok(hipMemcpy(d_rom, img.data(), 0xa000, hipMemcpyHostToDevice), "upload rom") ||
         !ok(hipMemcpy(d_lut, lut, 256, hipMemcpyHostToDevice), "upload lut") ||
         !ok(hipMemcpy(h->T, &T, sizeof(T), hipMemcpyHostToDevice), "upload tables") ||
@@ -691,37 +387,76 @@ int mh_set_buffers(MhEnv* h, uint8_t* obs, uint8_t* fin, float* rew, uint8_t* te
     return 0;
 }
 
-static int launch_reset_and_stack(MhEnv* h, hipStream_t s, int all) {
-    ResetArgs ra{h->n, h->np, h->cfg, h->nk, h->ncp, h->mem, h->sc, h->ev, h->cmem, h->csc, h->cx, h->ct,
-                 h->clives, h->cdraws, h->cboot, h->cframes, h->cinstr, h->cbad, all};
-    hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, ra);
+int mh_reset(MhEnv* h, void* stream) {
+    if (!h || !h->obs) { g_err = "buffers not set"; return -1; }
+    CK(hipSetDevice(h->device));
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(1));
     CK(hipGetLastError());
-    StackArgs sa{h->n, h->np, h->K, h->obs, h->fin, h->fresh, h->ev, h->cobs, all};
-    hipLaunchKernelGGL(k_stack, dim3((OBS_PIX / 4 + 63) / 64, h->np / 64), dim3(256), 0, s, sa);
+    hipLaunchKernelGGL(k_stack, dim3((OBS_PIX / 4 + 63) / 64, h->np / 64), dim3(256), 0, s, h->stack_args(1));
     CK(hipGetLastError());
     return 0;
 }
 
-int mh_reset(MhEnv* h, void* stream) {
-    if (!h || !h->obs) { g_err = "buffers not set"; return -1; }
-    CK(hipSetDevice(h->device));
-    return launch_reset_and_stack(h, (hipStream_t)stream, 1);
+// Records event k of the current timed step (k = 0 .. MH_STAGES).
+static int mark(MhEnv* h, hipStream_t s, int k) {
+    if (!h->timing) return 0;
+    size_t idx = h->timed_steps * (MH_STAGES + 1) + k;
+    while (h->events.size() <= idx) {
+        hipEvent_t e;
+        CK(hipEventCreate(&e));
+        h->events.push_back(e);
+    }
+    CK(hipEventRecord(h->events[idx], s));
+    return 0;
 }
 
 int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     if (!h || !h->obs || !d_actions) { g_err = "buffers or actions not set"; return -1; }
     CK(hipSetDevice(h->device));
     hipStream_t s = (hipStream_t)stream;
+    if (mark(h, s, 0)) return -1;
     CK(hipMemcpyAsync(h->snap_mem, h->mem, (size_t)MEM_ROWS * h->np, hipMemcpyDeviceToDevice, s));
     CK(hipMemcpyAsync(h->snap_sc, h->sc, (size_t)S_COUNT * h->np * 4, hipMemcpyDeviceToDevice, s));
+    if (mark(h, s, 1)) return -1;
     StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->snap_mem, h->snap_sc, h->ev, h->gray, d_actions,
                 h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len};
     hipLaunchKernelGGL(k_step, dim3(h->np / 64), dim3(64), 0, s, sa);
     CK(hipGetLastError());
+    if (mark(h, s, 2)) return -1;
     ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
     hipLaunchKernelGGL(k_obs, dim3(h->np / 64, OBS_PIX / 4), dim3(256), 0, s, oa);
     CK(hipGetLastError());
-    return launch_reset_and_stack(h, s, 0);
+    if (mark(h, s, 3)) return -1;
+    hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(0));
+    CK(hipGetLastError());
+    if (mark(h, s, 4)) return -1;
+    hipLaunchKernelGGL(k_stack, dim3((OBS_PIX / 4 + 63) / 64, h->np / 64), dim3(256), 0, s, h->stack_args(0));
+    CK(hipGetLastError());
+    if (mark(h, s, 5)) return -1;
+    if (h->timing) h->timed_steps++;
+    return 0;
+}
+
+int mh_timing(MhEnv* h, int enable) {
+    if (!h) return -1;
+    h->timing = enable != 0;
+    h->timed_steps = 0;
+    return 0;
+}
+
+int mh_timing_read(MhEnv* h, double* ms, int64_t* steps) {
+    if (!h || !ms) return -1;
+    CK(hipDeviceSynchronize());
+    for (int k = 0; k < MH_STAGES; k++) ms[k] = 0.0;
+    for (size_t t = 0; t < h->timed_steps; t++)
+        for (int k = 0; k < MH_STAGES; k++) {
+            float f = 0.f;
+            CK(hipEventElapsedTime(&f, h->events[t * (MH_STAGES + 1) + k], h->events[t * (MH_STAGES + 1) + k + 1]));
+            ms[k] += f;
+        }
+    if (steps) *steps = (int64_t)h->timed_steps;
+    return 0;
 }
 
 int mh_step_wait(MhEnv* h, void* stream) {
@@ -752,7 +487,8 @@ int64_t mh_instructions(MhEnv* h) { return h ? sum_words(h, E_INSTR_LO, true) : 
 
 int mh_env_ram(MhEnv* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
-    hipLaunchKernelGGL(k_ram_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n, d_out);
+    hipLaunchKernelGGL(k_rows_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n,
+                       2048u, d_out);
     CK(hipGetLastError());
     return 0;
 }
@@ -823,20 +559,15 @@ int mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream) {
 }
 int mh_raw_ram(MhRaw* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
-    hipLaunchKernelGGL(k_ram_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n, d_out);
+    hipLaunchKernelGGL(k_rows_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n,
+                       2048u, d_out);
     CK(hipGetLastError());
     return 0;
 }
-// screen rows are lane-interleaved; reuse the RAM transpose row by row block
-__global__ void k_screen_out(const uint8_t* scr, uint32_t np, int n, uint8_t* out) {
-    const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
-    const uint32_t p = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (e >= (uint32_t)n || p >= (uint32_t)GRAY_PIX) return;
-    out[(size_t)e * GRAY_PIX + p] = scr[(size_t)p * np + e];
-}
 int mh_raw_screen(MhRaw* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
-    hipLaunchKernelGGL(k_screen_out, dim3(h->np / 64, GRAY_PIX / 4), dim3(256), 0, (hipStream_t)stream, h->screen, h->np, h->n, d_out);
+    hipLaunchKernelGGL(k_rows_out, dim3(h->np / 64, GRAY_PIX / 4), dim3(256), 0, (hipStream_t)stream, h->screen, h->np,
+                       h->n, (uint32_t)GRAY_PIX, d_out);
     CK(hipGetLastError());
     return 0;
 }
@@ -880,9 +611,7 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
     static AreaTables* d_T = nullptr;
     if (!d_T) {
         AreaTables T;
-        memset(&T, 0, sizeof(T));
-        area_taps(256, 84, T.xs, T.xw, T.xn);
-        area_taps(240, 84, T.ys, T.yw, T.yn);
+        area_tables(&T);
         CK(hipMalloc(&d_T, sizeof(T)));
         CK(hipMemcpy(d_T, &T, sizeof(T), hipMemcpyHostToDevice));
     }

@@ -64,6 +64,8 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).argtypes = [_P]
     L.mh_raw_destroy.argtypes = [_P]
     L.mh_resize.argtypes = [_P, _P, _i32, _P]
+    L.mh_timing.argtypes = [_P, _i32]
+    L.mh_timing_read.argtypes = [_P, _P, _P]
     _lib = L
     return L
 

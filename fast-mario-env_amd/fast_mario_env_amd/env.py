@@ -225,6 +225,19 @@ class HipVecEnv:
     def bytes_per_env(self) -> int:
         return int(lib().mh_env_bytes(self.h))
 
+    STAGES = ("snapshot", "k_step", "k_obs", "k_reset", "k_stack")
+
+    def timing(self, enable: bool = True):
+        """Start (or stop) per-stage HIP-event timing of step(); read it with timing_read()."""
+        check(lib().mh_timing(self.h, int(bool(enable))), "mh_timing")
+
+    def timing_read(self) -> tuple[dict, int]:
+        """-> ({stage: summed ms}, timed steps); synchronizes."""
+        ms = np.zeros(len(self.STAGES), np.float64)
+        n = np.zeros(1, np.int64)
+        check(lib().mh_timing_read(self.h, ms.ctypes.data, n.ctypes.data), "mh_timing_read")
+        return dict(zip(self.STAGES, ms.tolist())), int(n[0])
+
     def synchronize(self):
         check(lib().mh_step_wait(self.h, _stream(self._torch, self.dev)), "mh_step_wait")
 

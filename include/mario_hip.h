@@ -65,6 +65,15 @@ int mh_step_wait(MhEnv* h, void* stream);
 
 void mh_destroy(MhEnv* h);
 
+/* Per-stage timing of mh_step_async with HIP events recorded on the step's own stream (no counterpart
+ * in the reference; used by the benchmark). Stages: 0 step-start snapshot copy, 1 k_step (emulation +
+ * render), 2 k_obs (max-pool + INTER_AREA), 3 k_reset, 4 k_stack. mh_timing(h, 1) clears and starts
+ * recording; mh_timing_read synchronizes and returns the summed milliseconds per stage and the number
+ * of timed steps. */
+#define MH_STAGES 5
+int mh_timing(MhEnv* h, int enable);
+int mh_timing_read(MhEnv* h, double* ms, int64_t* steps);
+
 /* Counters summed over envs (synchronizing). Replace fm_frames / fm_bad_ops (fastmario.cpp:619-628).
  * frames counts every emulated NES frame the reference CPU path emulates (hack frames and
  * early-termination re-renders included); instructions counts retired 6502 instructions. */

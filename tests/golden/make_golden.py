@@ -106,7 +106,7 @@ def run_env(venv, actions):
         done = term | trunc
         if done.any():
             idx = np.flatnonzero(done)
-            parts += [venv.fin[idx], venv.ep_ret[idx], venv.ep_len[idx]]
+            parts += [venv.fin[idx], np.asarray(venv.ep_ret[idx], np.float64), np.asarray(venv.ep_len[idx], np.int64)]
         trace.append(digest(*parts))
     return trace
 
