@@ -87,6 +87,20 @@ __device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom
     return c;
 }
 
+// What a lane needs from its block: the staged cartridge, the gray LUT and its LDS render buffers.
+struct LaneCtx {
+    Cart cart;
+    const uint8_t* lut;
+    uint32_t* sp;     // this lane's sprite line buffer (stride LDS_LANES words)
+    uint32_t* gp;     // this lane's gray palette (stride LDS_LANES words)
+};
+
+__device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* mem, uint32_t np) {
+    c.mem = mem; c.np = np; c.cart = x.cart; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
+    c.bad_ops = 0; c.instructions = 0;
+    c.pend_line = -1; c.sp_line = -1; c.pal_dirty = true;
+}
+
 struct BootArgs {
     RomArgs R;
     int nl;
@@ -176,10 +190,10 @@ __device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e
 
 // ------------------------------------------------------------------ lane bodies
 // Power-on and title sequence with the target level written into RAM (fastmario.cpp:414-445).
-__device__ inline void boot_lane(const BootArgs& A, const Cart& cart, const uint8_t* lut, int l) {
+__device__ inline void boot_lane(const BootArgs& A, const LaneCtx& x, int l) {
     Console c;
-    c.mem = A.mem + l; c.np = A.nlp; c.cart = cart; c.lut = lut;
-    c.gray = A.gray + l; c.render = true; c.bad_ops = 0; c.instructions = 0;
+    attach(c, x, A.mem + l, A.nlp);
+    c.gray = A.gray + l; c.render = true;
     c.power_on();
     auto fr = [&](uint8_t b) { c.joy_buttons[0] = b; c.frame(); };
     const int w = A.levels[3 * l], s = A.levels[3 * l + 1], ar = A.levels[3 * l + 2];
@@ -207,15 +221,14 @@ __device__ inline void boot_lane(const BootArgs& A, const Cart& cart, const uint
 // Reset cache: the state after k no-op agent steps from the boot state of a level, k in 0..noop_max
 // (fastmario.cpp:389-401), restarting on termination like the reference. The sticky draws only choose
 // between action 0 and prev == 0, so their count is recorded, not their values.
-__device__ inline void cache_lane(const CacheArgs& A, const Cart& cart, const uint8_t* lut, int ci) {
+__device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) {
     const int lvl = ci / A.nk, k = ci - lvl * A.nk;
     Region boot{(uint8_t*)A.boot_mem, (uint32_t*)A.boot_sc, A.nlp, (uint32_t)lvl};
     Region live{A.mem, A.sc, A.ncp, (uint32_t)ci};
     Region snap{A.snap_mem, A.snap_sc, A.ncp, (uint32_t)ci};
     copy_console(live, boot);
     Console c;
-    c.mem = A.mem + ci; c.np = A.ncp; c.cart = cart; c.lut = lut;
-    c.bad_ops = 0; c.instructions = 0;
+    attach(c, x, A.mem + ci, A.ncp);
     c.load(A.sc, ci);
     EnvRegs ev{};
     ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
@@ -240,10 +253,9 @@ __device__ inline void cache_lane(const CacheArgs& A, const Cart& cart, const ui
 }
 
 // One agent step of env e (fastmario.cpp:403-411 + 336-374).
-__device__ inline void step_lane(const StepArgs& A, const Cart& cart, const uint8_t* lut, uint32_t e) {
+__device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e) {
     Console c;
-    c.mem = A.mem + e; c.np = A.np; c.cart = cart; c.lut = lut;
-    c.bad_ops = 0; c.instructions = 0;
+    attach(c, x, A.mem + e, A.np);
     c.load(A.sc, e);
     EnvRegs ev;
     load_env(ev, A.ev, A.np, e);
@@ -302,10 +314,10 @@ __device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
 }
 
 // One nes-py frame of raw console e (fastmario.cpp:656-661); power_on != 0 boots it instead.
-__device__ inline void raw_lane(const RawArgs& A, const Cart& cart, const uint8_t* lut, uint32_t e) {
+__device__ inline void raw_lane(const RawArgs& A, const LaneCtx& x, uint32_t e) {
     Console c;
-    c.mem = A.mem + e; c.np = A.np; c.cart = cart; c.lut = lut;
-    c.gray = A.screen + e; c.bad_ops = 0; c.instructions = 0;
+    attach(c, x, A.mem + e, A.np);
+    c.gray = A.screen + e;
     if (A.power_on) {
         c.power_on();
     } else {

@@ -30,36 +30,44 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
     __syncthreads();
 }
 
+// Block-shared LDS of the emulator kernels: the cartridge, the gray LUT and per-lane render buffers.
 #define ROM_LDS                                                     \
     __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000]; \
-    __shared__ uint8_t s_lut[256];
+    __shared__ uint8_t s_lut[256];                                  \
+    __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
+    __shared__ uint32_t s_gp[LDS_GP_WORDS * LDS_LANES];
+
+__device__ __forceinline__ LaneCtx lane_ctx(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_lut,
+                                            uint32_t* s_sp, uint32_t* s_gp) {
+    return LaneCtx{make_cart(R, s_rom), s_lut, s_sp + threadIdx.x, s_gp + threadIdx.x};
+}
 
 __global__ void __launch_bounds__(64) k_boot(BootArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut);
     const int l = blockIdx.x * blockDim.x + threadIdx.x;
-    if (l < A.nl) boot_lane(A, make_cart(A.R, s_rom), s_lut, l);
+    if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), l);
 }
 
 __global__ void __launch_bounds__(64) k_cache(CacheArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut);
     const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci < A.nc) cache_lane(A, make_cart(A.R, s_rom), s_lut, ci);
+    if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), ci);
 }
 
 __global__ void __launch_bounds__(64) k_step(StepArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut);
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) step_lane(A, make_cart(A.R, s_rom), s_lut, e);
+    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), e);
 }
 
 __global__ void __launch_bounds__(64) k_raw(RawArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut);
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) raw_lane(A, make_cart(A.R, s_rom), s_lut, e);
+    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), e);
 }
 
 __global__ void __launch_bounds__(64) k_reset(ResetArgs A) {

@@ -18,6 +18,8 @@
 namespace mh {
 
 constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
+constexpr int LDS_LANES = 64;                      // lanes sharing one block's per-lane LDS buffers
+constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
 constexpr int LINE_END = 341;
 constexpr int GRAY_PIX = 256 * 240;
@@ -78,6 +80,12 @@ struct Console {
     uint16_t v, t, inc;
     // ---- counters
     uint32_t bad_ops, instructions;
+    // ---- derived state (not part of the machine state)
+    int32_t pend_line;       // scanline of a sprite evaluation not yet materialized (-1: the list is current)
+    int32_t sp_line;         // scanline the LDS sprite line buffer holds (-1: invalid)
+    bool pal_dirty;          // the LDS gray palette must be rebuilt
+    uint32_t* lds_sp;        // per-lane sprite line buffer: word (x / 4) of this lane at lds_sp[(x / 4) * LDS_LANES]
+    uint32_t* lds_gp;        // per-lane gray palette: word (i / 4) at lds_gp[(i / 4) * LDS_LANES]
 
     // ------------------------------------------------------------ interleaved memory
     __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mem[(size_t)__umul24(row, np)]; }
@@ -116,9 +124,11 @@ struct Console {
         nsl = (uint8_t)w(S_NSL); sl_lo = w(S_SL_LO); sl_hi = w(S_SL_HI);
         pcyc = (int32_t)w(S_PCYC); scanline = (int32_t)w(S_SCANLINE);
         v = (uint16_t)w(S_V); t = (uint16_t)w(S_T); inc = (uint16_t)w(S_INC);
+        pend_line = -1; sp_line = -1; pal_dirty = true;
         nmi_threshold();
     }
-    __device__ void store(uint32_t* sc, uint32_t e) const {
+    __device__ void store(uint32_t* sc, uint32_t e) {
+        materialize_sprites();
         auto w = [&](int k, uint32_t val) { sc[(size_t)k * np + e] = val; };
         w(S_ITER_LO, iter_lo); w(S_ITER_HI, iter_hi); w(S_EXEC_REL, (uint32_t)exec_at);
         w(S_PC, pc); w(S_SP, sp); w(S_A, a); w(S_X, x); w(S_Y, y); w(S_P, p); w(S_ZERO_SKIP, zero_skip);
@@ -146,6 +156,7 @@ struct Console {
         long_spr = 0; nmi_en = 0; vblank = 0; show_bg = 1; show_spr = 1; even = 1;
         first_write = 1; bg_page = 0; spr_page = 0; v = 0; pcyc = 0; scanline = 0;
         oam_addr = 0; fine_x = 0; t = 0; inc = 1; pstate = ST_PRE; nsl = 0; sl_lo = sl_hi = 0;
+        pend_line = -1; sp_line = -1; pal_dirty = true;
         nmi_threshold();
     }
 
@@ -167,24 +178,28 @@ struct Console {
     __device__ void write(uint16_t ad, uint8_t val) {
         if (ad < 0x2000) { st(ROW_RAM + (ad & 0x7ff), val); return; }
         if (ad < 0x4000) {
+            // a pending sprite evaluation is materialized before its inputs (OAM, oam_addr, sprite
+            // size) change; the sprite line buffer is rebuilt after any write that can change it
             switch (ad & 0x2007) {
-                case 0x2000: catch_up(); ctrl_write(val); break;
+                case 0x2000: catch_up(); materialize_sprites(); ctrl_write(val); sp_line = -1; break;
                 case 0x2001: catch_up(); mask_write(val); break;
-                case 0x2003: catch_up(); oam_addr = val; break;
-                case 0x2004: catch_up(); st(ROW_OAM + oam_addr, val); oam_addr++; break;
+                case 0x2003: catch_up(); materialize_sprites(); oam_addr = val; break;
+                case 0x2004: catch_up(); materialize_sprites(); st(ROW_OAM + oam_addr, val); oam_addr++; sp_line = -1; break;
                 case 0x2005: catch_up(); scroll_write(val); break;
                 case 0x2006: catch_up(); addr_write(val); break;
-                case 0x2007: catch_up(); data_write(val); break;
+                case 0x2007: catch_up(); data_write(val); sp_line = -1; break;
                 default: break;
             }
             return;
         }
         if (ad == 0x4014) {  // OAM DMA: 513 cycles, +1 on an odd absolute cycle; copies from RAM pages only
             catch_up();
+            materialize_sprites();
             skip += 513 + (int)((iter_lo + (uint32_t)cur + 1u) & 1u);
             uint16_t src = (uint16_t)(val << 8);
             if (src < 0x2000)
                 for (int i = 0; i < 256; i++) st(ROW_OAM + ((oam_addr + i) & 0xff), ram(src + i));
+            sp_line = -1;
             return;
         }
         if (ad == 0x4016) {
@@ -245,7 +260,7 @@ struct Console {
     __device__ void vbus_write(uint16_t ad, uint8_t d) {
         if (ad < 0x2000) return;
         if (ad < 0x3eff) st(ROW_VRAM + nt_row(ad), d);
-        else if (ad < 0x3fff) st(ROW_PAL + (ad == 0x3f10 ? 0 : (ad & 0x1f)), d);
+        else if (ad < 0x3fff) { st(ROW_PAL + (ad == 0x3f10 ? 0 : (ad & 0x1f)), d); pal_dirty = true; }
     }
     __device__ __forceinline__ uint8_t nametable(uint16_t ad) const { return vram(cart.nt[(ad >> 10) & 3] + (ad & 0x3ff)); }
 
@@ -279,14 +294,27 @@ struct Console {
     __device__ void copy_h() { v = (uint16_t)((v & ~0x41f) | (t & 0x41f)); }
     __device__ void copy_v() { v = (uint16_t)((v & ~0x7be0) | (t & 0x7be0)); }
 
-    // per-line sprite list from oam_addr/4 (nes_core.hpp:336-349)
-    __device__ void eval_sprites() {
+    // Per-line sprite list from oam_addr/4 (nes_core.hpp:336-349). The PPU only records the scanline
+    // of an evaluation; the list is computed from OAM when something needs it (rendering, a change
+    // of OAM / oam_addr / sprite size, or the end of the kernel). Until then its inputs are unchanged,
+    // so the late evaluation gives the same list.
+    __device__ void materialize_sprites() {
+        if (pend_line < 0) return;
         nsl = 0;
         int h = long_spr ? 16 : 8;
         for (int i = oam_addr / 4; i < 64 && nsl < 8; i++) {
-            int d = scanline - (int)oam(i * 4);
+            int d = pend_line - (int)oam(i * 4);
             if (d >= 0 && d < h) { set_sl(nsl, (uint8_t)i); nsl++; }
         }
+        pend_line = -1;
+    }
+    // "nsl > 0 && sl[0] == 0" without materializing: sprite 0 heads the list exactly when the
+    // evaluation starts at index 0 and sprite 0 is in range.
+    __device__ __forceinline__ bool sprite0_first() const {
+        if (pend_line < 0) return nsl > 0 && sl(0) == 0;
+        if (oam_addr >= 4) return false;
+        int d = pend_line - (int)oam(0);
+        return d >= 0 && d < (long_spr ? 16 : 8);
     }
     __device__ uint8_t bg_colour(int px, uint8_t* pattern) const {
         int xf = (fine_x + px) % 8;
@@ -321,7 +349,7 @@ struct Console {
     // visible dots [x0, x1) without pixel output (nes_core.hpp:394-413)
     __device__ void dots_quiet(int x0, int x1) {
         if (!show_bg) return;
-        if (!s0hit && show_spr && nsl > 0 && sl(0) == 0) {
+        if (!s0hit && show_spr && sprite0_first()) {
             int sx = oam(3);
             int lo = x0 > sx ? x0 : sx;
             int hi = x1 < sx + 8 ? x1 : sx + 8;
@@ -347,31 +375,94 @@ struct Console {
         return (hi - r + 7) / 8 - (lo - r + 7) / 8;
     }
 
-    // visible dots [x0, x1) with pixel output: gray values into the frame buffer (nes_core.hpp:467-513)
+    // ---- per-lane LDS buffers of the renderer
+    __device__ __forceinline__ uint8_t lds_byte(const uint32_t* base, int i) const {
+        return (uint8_t)(base[(i >> 2) * LDS_LANES] >> (8 * (i & 3)));
+    }
+    // gray value of every palette address, lut[pal[i]]; rebuilt after palette writes
+    __device__ void build_gray_palette() {
+        for (int w = 0; w < LDS_GP_WORDS; w++) {
+            uint32_t word = 0;
+            for (int b = 0; b < 4; b++) word |= (uint32_t)lut[pal(4 * w + b)] << (8 * b);
+            lds_gp[w * LDS_LANES] = word;
+        }
+        pal_dirty = false;
+    }
+    // First opaque listed sprite per x of line py (nes_core.hpp:427-441): bits 0-4 palette address
+    // (0x10 | attr << 2 | pattern), bit 5 in front of the background, bit 6 sprite 0. The pattern row
+    // of each listed sprite is fetched once, with the addressing of sprite_pattern().
+    __device__ void build_sprite_line(int py) {
+        for (int w = 0; w < LDS_SP_WORDS; w++) lds_sp[w * LDS_LANES] = 0;
+        const int h = long_spr ? 16 : 8;
+        for (int k = 0; k < nsl; k++) {
+            const int i = sl(k);
+            const uint8_t sx = oam(i * 4 + 3), sy = (uint8_t)(oam(i * 4) + 1), tile = oam(i * 4 + 1), attr = oam(i * 4 + 2);
+            int yo = (py - sy) % h;
+            if (attr & 0x80) yo ^= (h - 1);
+            uint16_t ad;
+            if (!long_spr) {
+                ad = (uint16_t)(tile * 16 + yo);
+                if (spr_page) ad += 0x1000;
+            } else {
+                yo = (yo & 7) | ((yo & 8) << 1);
+                ad = (uint16_t)((tile >> 1) * 32 + yo);
+                ad |= (tile & 1) << 12;
+            }
+            const uint8_t lo = vbus_read(ad), hi = vbus_read((uint16_t)(ad + 8));
+            const uint32_t tag = 0x10u | ((attr & 3u) << 2) | (attr & 0x20 ? 0u : 0x20u) | (i == 0 ? 0x40u : 0u);
+            const int xe = sx + 8 < 256 ? sx + 8 : 256;
+            for (int px = sx; px < xe; px++) {
+                int xs = px - sx;
+                if (!(attr & 0x40)) xs ^= 7;
+                const uint32_t c = ((lo >> xs) & 1u) | (((hi >> xs) & 1u) << 1);
+                uint32_t* wp = &lds_sp[(px >> 2) * LDS_LANES];
+                const int sh = 8 * (px & 3);
+                if (c && !((*wp >> sh) & 0xffu)) *wp |= (c | tag) << sh;
+            }
+        }
+        sp_line = py;
+    }
+
+    // Visible dots [x0, x1) with pixel output: gray values into the frame buffer (nes_core.hpp:467-513).
+    // Background fetches happen once per 8-dot tile; sprites come from the LDS line buffer.
     __device__ void dots_drawn(int x0, int x1) {
         const int py = scanline;
-        for (int px = x0; px < x1; px++) {
-            uint8_t pa = 0, bg_op = 0;
+        materialize_sprites();
+        if (pal_dirty) build_gray_palette();
+        const bool spr = show_spr && nsl;
+        if (spr && sp_line != py) build_sprite_line(py);
+        int px = x0;
+        while (px < x1) {
+            const int xf = (fine_x + px) & 7;
+            int span = 8 - xf;
+            if (span > x1 - px) span = x1 - px;
+            uint32_t lo = 0, hi = 0, at = 0;
             if (show_bg) {
-                uint8_t pat;
-                uint8_t c = bg_colour(px, &pat);
-                if (!(hide_edge_bg && px < 8) && pat) { pa = c; bg_op = pat; }
-                if ((fine_x + px) % 8 == 7) coarse_x_add(1);
+                const uint8_t tile = nametable((uint16_t)(0x2000 | (v & 0x0fff)));
+                const uint16_t pa = (uint16_t)(((tile * 16) + ((v >> 12) & 7)) | (bg_page << 12));
+                lo = cart.chr[pa];
+                hi = cart.chr[pa + 8];
+                const uint16_t aa = (uint16_t)(0x23c0 | (v & 0x0c00) | ((v >> 4) & 0x38) | ((v >> 2) & 7));
+                const int sh = ((v >> 4) & 4) | (v & 2);
+                at = ((nametable(aa) >> sh) & 3u) << 2;
             }
-            if (show_spr && nsl && !(hide_edge_spr && px < 8)) {
-                for (int k = 0; k < nsl; k++) {
-                    int i = sl(k);
-                    int sx = oam(i * 4 + 3);
-                    if (px < sx || px >= sx + 8) continue;
-                    uint8_t c = sprite_pattern(i, px, py);
-                    if (!c) continue;
-                    uint8_t attr = oam(i * 4 + 2);
-                    if (i == 0 && bg_op && !s0hit && show_bg) s0hit = 1;
-                    if (!bg_op || !(attr & 0x20)) pa = (uint8_t)(c | 0x10 | ((attr & 3) << 2));
-                    break;
+            for (int j = 0; j < span; j++, px++) {
+                const int bit = 7 - (xf + j);
+                uint32_t pa = 0, bgop = 0;
+                if (!(hide_edge_bg && px < 8)) {
+                    bgop = ((lo >> bit) & 1u) | (((hi >> bit) & 1u) << 1);
+                    if (bgop) pa = bgop | at;
                 }
+                if (spr && !(hide_edge_spr && px < 8)) {
+                    const uint32_t c = lds_byte(lds_sp, px);
+                    if (c) {
+                        if ((c & 0x40) && bgop && !s0hit && show_bg) s0hit = 1;
+                        if (!bgop || (c & 0x20)) pa = c & 0x1f;
+                    }
+                }
+                gray[(size_t)__umul24((uint32_t)(py * 256 + px), np)] = lds_byte(lds_gp, pa);
             }
-            gray[(size_t)__umul24((uint32_t)(py * 256 + px), np)] = lut[pal(pa)];
+            if (show_bg && xf + span == 8) coarse_x_add(1);
         }
     }
 
@@ -419,7 +510,8 @@ struct Console {
                     int k = n < LINE_END - c ? n : LINE_END - c;
                     pcyc += k; ppu_calls += k; n -= k;
                 } else if (c >= LINE_END) {
-                    eval_sprites();
+                    pend_line = scanline;   // sprite evaluation for the next line (materialized lazily)
+                    sp_line = -1;
                     scanline++;
                     pcyc = 1; ppu_calls++; n--;
                     if (scanline >= 240) pstate = ST_POST;
@@ -622,6 +714,74 @@ struct Console {
         return skip;
     }
 
+    // PPU calls from the current PPU position to (line, dot) on the frame timeline of
+    // nmi_threshold() (pre-render line = -1, 262 x 341 calls); the one-dot-shorter odd pre-render
+    // line is not modelled, so callers keep a margin. 0 means the very next call processes that dot.
+    __device__ __forceinline__ int32_t calls_until(int line, int dot) const {
+        const int now_line = pstate == ST_PRE ? -1 : pstate == ST_POST ? 240 : scanline;
+        int32_t d = ((line + 1) * 341 + (dot - 1)) - ((now_line + 1) * 341 + (pcyc - 1));
+        if (d < 0) d += 262 * 341;
+        return d;
+    }
+
+    // Exact fast-forward of the sprite-0 wait loops `LDA $2002 / AND #$40 / BEQ|BNE *-5` (BEQ: wait
+    // for the hit, BNE: wait for the clear at the pre-render line). Iterations whose $2002 reads
+    // provably return the same value are not executed: they would only re-read an unchanged s0hit,
+    // clear an already clear vblank flag and set first_write, and the PPU is caught up lazily anyway.
+    // The span ends before the first dot where s0hit could change (sprite 0's first line, or the
+    // pre-render clear), before the NMI sync point and inside the frame. Returns true if it advanced.
+    __device__ bool poll_skip(int32_t j, int32_t end) {
+        if (pc < 0x8000 || pc > 0xfff8) return false;
+        if (prg(pc) != 0xad || prg(pc + 1) != 0x02 || prg(pc + 2) != 0x20 || prg(pc + 3) != 0x29 ||
+            prg(pc + 4) != 0x40 || prg(pc + 6) != 0xf9)
+            return false;
+        const uint8_t br = prg(pc + 5);
+        if (br != 0xf0 && br != 0xd0) return false;
+        cur = j;
+        advance_to(3 * (j + 1));                 // the sync the LDA $2002 at j performs
+        const bool wait_hit = br == 0xf0;
+        if (wait_hit == (s0hit != 0)) return false;   // this read ends the loop: run it normally
+        int32_t limit;                           // first PPU call count at which s0hit may differ
+        if (wait_hit) {
+            // A hit needs sprite 0 at the head of the list of the line being drawn. The list already
+            // evaluated serves the current line (in RENDER) or line 0 of the next frame (elsewhere).
+            // The lists still to come are evaluated at the ends of render lines m (the current one
+            // onwards in RENDER, 0 onwards elsewhere) and serve line m + 1 (240: line 0 of the next
+            // frame); with OAM, oam_addr and sprite size fixed (the loop writes nothing) sprite 0 can
+            // head one only for y0 <= m < y0 + h.
+            if (sprite0_first() && pstate == ST_RENDER) return false;
+            const int y0 = oam(0), h = long_spr ? 16 : 8;
+            const int m = pstate == ST_RENDER && scanline > y0 ? scanline : y0;
+            if (m <= 239 && m < y0 + h) limit = ppu_calls + calls_until(m + 1, 1) - 2;
+            else if (y0 <= 238) limit = ppu_calls + calls_until(y0 + 1, 1) - 2;   // next frame
+            else limit = 0x7fffffff;
+            if (pstate != ST_RENDER && sprite0_first()) {
+                const int32_t l0 = ppu_calls + calls_until(0, 1) - 2;
+                if (l0 < limit) limit = l0;
+            }
+        } else {
+            limit = ppu_calls + calls_until(-1, 1) - 2;
+        }
+        const int32_t c = 9 + ((((pc + 7) ^ pc) & 0xff00) ? 2 : 0);   // LDA 4 + AND 2 + taken branch 3 (+2)
+        // start jl of the last skipped iteration: its three instructions start before the frame end
+        // and below the NMI check, and its read precedes `limit`
+        int32_t jl = end - 7;
+        const int32_t by_nmi = (nmi_thresh - 1) / 3 - 7;
+        const int32_t by_limit = (limit - 1) / 3 - 1;
+        if (by_nmi < jl) jl = by_nmi;
+        if (by_limit < jl) jl = by_limit;
+        if (jl < j) return false;
+        const int32_t k = (jl - j) / c + 1;
+        vblank = 0;
+        first_write = 1;
+        a = s0hit ? 0x40 : 0x00;
+        set_nz(a);
+        exec_at = j + k * c;
+        zero_skip = 0;
+        instructions += 3 * (uint32_t)k;
+        return true;
+    }
+
     // one nes-py Emulator::step (nes_core.hpp:1166-1204) with the exact `JMP *` idle fast-forward
     __device__ void frame() {
         const int32_t end = FRAME_ITERS;
@@ -644,6 +804,7 @@ struct Console {
                     if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; continue; }
                 }
             }
+            if (poll_skip(j, end)) continue;
             cur = j;
             int s = step_instruction();
             exec_at = j + (s >= 1 ? s : 1);
