@@ -71,7 +71,8 @@ struct Pcg {
 };
 
 // ------------------------------------------------------------------ SMB RAM protocol (fastmario.cpp:204-250)
-struct Info { int64_t v[10]; };   // x_pos flag_get life score time world stage coins y_pos status
+// x_pos flag_get life score time world stage coins y_pos status, as the int32 values of the C ABI
+struct Info { int32_t v[10]; };
 
 __device__ __forceinline__ int64_t dec_digits(const Console& c, uint32_t ad, int n) {
     int64_t val = 0;
@@ -92,16 +93,16 @@ __device__ __forceinline__ bool smb_stage_over(const Console& c) {
     }
     return false;
 }
-__device__ Info smb_info(const Console& c) {
+__device__ __forceinline__ Info smb_info(const Console& c) {
     Info i;
-    i.v[0] = smb_x(c);
+    i.v[0] = (int32_t)smb_x(c);
     i.v[1] = smb_world_over(c) || smb_stage_over(c);
     i.v[2] = c.ram(0x75a);
-    i.v[3] = dec_digits(c, 0x7de, 6);
-    i.v[4] = smb_time(c);
+    i.v[3] = (int32_t)dec_digits(c, 0x7de, 6);
+    i.v[4] = (int32_t)smb_time(c);
     i.v[5] = c.ram(0x75f) + 1;
     i.v[6] = c.ram(0x75c) + 1;
-    i.v[7] = dec_digits(c, 0x7ed, 2);
+    i.v[7] = (int32_t)dec_digits(c, 0x7ed, 2);
     uint8_t yp = c.ram(0x3b8);
     i.v[8] = c.ram(0xb5) < 1 ? 255 + (255 - yp) : 255 - yp;
     uint8_t st = c.ram(0x756);
@@ -149,28 +150,14 @@ struct Stepper {
     Region live, snap;    // the console's own region and its step-start snapshot
     bool snapped;
 
-    __device__ void nes_frame(uint8_t buttons, bool render, uint8_t* slot) {
-        c.joy_buttons[0] = buttons;
-        c.render = render;
-        c.gray = slot;
-        c.frame();
-        ev.frames++;
-        if (render) ev.shows_boot = false;
-    }
-    // _skip_change_area / _skip_occupied_states of a not-done env (fastmario.cpp:297-308)
-    __device__ void skip_busy(bool render, uint8_t* slot) {
-        uint8_t cat = c.ram(0x6de);
+    __device__ __forceinline__ bool busy() { return smb_busy(c) || smb_world_over(c); }
+    // _skip_change_area before the _skip_occupied_states loop (fastmario.cpp:297-300)
+    __device__ __forceinline__ void fix_change_area() {
+        const uint8_t cat = c.ram(0x6de);
         if (cat > 1 && cat < 255) c.st(ROW_RAM + 0x6de, 1);
-        int guard = 0;
-        while (smb_busy(c) || smb_world_over(c)) {
-            if (++guard > HACK_FRAME_LIMIT) { c.bad_ops |= ERR_HACK_LIMIT; break; }
-            c.st(ROW_RAM + 0x7a0, 0);
-            nes_frame(0, render, slot);
-        }
     }
-    // reward, done, info, hacks (fastmario.cpp:310-334)
-    __device__ double frame_step(uint8_t buttons, bool render, uint8_t* slot, bool* done) {
-        nes_frame(buttons, render, slot);
+    // reward, done and info after an agent frame (fastmario.cpp:310-334)
+    __device__ __forceinline__ double frame_reward(bool* done) {
         int64_t xx = smb_x(c), dx = xx - ev.x_last;
         ev.x_last = xx;
         if (dx < -5 || dx > 5) dx = 0;
@@ -184,50 +171,101 @@ struct Stepper {
         if (r > 15) r = 15;
         ev.info = smb_info(c);
         *done = die || ev.info.v[1];
-        if (!*done) skip_busy(render, slot);
         return (double)r;
     }
-    // sticky + skip + max-pool + early termination + life loss (fastmario.cpp:336-374). On early
-    // termination the frames that were not rendered are re-emulated from the step-start snapshot.
-    __device__ double agent_step(int act0, bool want_obs, bool* term) {
+
+    // Sticky actions + frame skip + max-pool + early termination + life loss (fastmario.cpp:336-374),
+    // with the hack frames of _skip_change_area / _skip_occupied_states (fastmario.cpp:297-308) after
+    // every agent frame that did not end the episode. On early termination the frames that were not
+    // rendered are re-emulated from the step-start snapshot, as the reference re-emulates them from its
+    // per-frame snapshots (fastmario.cpp:354-365). Written as a state machine around ONE console frame
+    // so that the emulator is inlined once.
+    __device__ __forceinline__ double agent_step(int act0, bool want_obs, bool* term) {
+        enum : uint8_t { PH_MAIN, PH_BUSY, PH_REPLAY, PH_RBUSY, PH_FINAL };
         const int K = cfg.skip;
         const bool mp = cfg.maxpool != 0;
         uint64_t acts = 0;
         double total = 0.0;
         bool done = false;
-        int i;
-        for (i = 0; i < K; i++) {
-            int act = act0;
-            if (cfg.sticky != 0.0) {
-                if (rng) { if (rng->random() < cfg.sticky) act = ev.prev; }
-                else ev.draws++;
+        int i = 0, last = 0, j = 0, guard = 0;
+        uint8_t ph = PH_MAIN;
+        bool hack_render = false, rj = false;
+        uint8_t* hack_slot = gray1;
+        uint64_t f0 = 0;
+        uint32_t i0 = 0, b0 = 0;
+        for (;;) {
+            // ---- the frame to emulate
+            uint8_t buttons = 0;
+            bool render = false;
+            uint8_t* slot = gray1;
+            if (ph == PH_MAIN) {
+                int act = act0;
+                if (cfg.sticky != 0.0) {
+                    if (rng) { if (rng->random() < cfg.sticky) act = ev.prev; }
+                    else ev.draws++;
+                }
+                ev.prev = act;
+                acts |= (uint64_t)act << (3 * i);
+                const bool last_frame = i == K - 1, pool_frame = mp && i == K - 2;
+                render = want_obs && (last_frame || pool_frame);
+                slot = last_frame ? gray0 : gray1;
+                buttons = kButtons[act];
+            } else if (ph == PH_BUSY || ph == PH_RBUSY) {
+                c.st(ROW_RAM + 0x7a0, 0);
+                render = hack_render;
+                slot = hack_slot;
+            } else if (ph == PH_REPLAY) {
+                rj = mp && j == last - 1;
+                f0 = ev.frames; i0 = c.instructions; b0 = c.bad_ops;
+                buttons = kButtons[(acts >> (3 * j)) & 7];
+                render = rj;
+            } else {
+                buttons = kButtons[(acts >> (3 * last)) & 7];
+                render = true;
+                slot = gray0;
             }
-            ev.prev = act;
-            bool last_frame = i == K - 1, pool_frame = mp && i == K - 2;
-            bool render = want_obs && (last_frame || pool_frame);
-            acts |= (uint64_t)act << (3 * i);
-            total += frame_step(kButtons[act], render, last_frame ? gray0 : gray1, &done);
-            if (done) break;
-        }
-        int last = done ? i : K - 1;
-        if (want_obs && done && last < K - 1) {
-            // the reference re-emulates frame last-1 (+ its hack frames) and frame last from per-frame
-            // snapshots (fastmario.cpp:354-365); the same frames are reached here by replaying the step
-            copy_console(live, snap);
-            c.load(snap.sc, snap.idx);
-            for (int j = 0; j < last; j++) {
-                const bool r = mp && j == last - 1;
-                const uint64_t f0 = ev.frames;
-                const uint32_t i0 = c.instructions, b0 = c.bad_ops;
-                nes_frame(kButtons[(acts >> (3 * j)) & 7], r, gray1);
-                skip_busy(r, gray1);
-                if (!r) {   // count only the frames the reference re-emulates
+            c.joy_buttons0 = buttons;
+            c.render = render;
+            c.gray = slot;
+            c.frame();
+            ev.frames++;
+            if (render) ev.shows_boot = false;
+            // ---- what follows it
+            if (ph == PH_FINAL) break;
+            bool hack = false;   // another hack frame follows
+            if (ph == PH_MAIN) {
+                total += frame_reward(&done);
+                if (!done) { fix_change_area(); guard = 0; hack = true; }
+                hack_render = render; hack_slot = slot;
+            } else if (ph == PH_REPLAY) {
+                fix_change_area(); guard = 0; hack = true;
+                hack_render = rj; hack_slot = gray1;
+            } else {
+                hack = true;
+            }
+            if (hack && busy()) {
+                if (++guard <= HACK_FRAME_LIMIT) { ph = ph == PH_MAIN || ph == PH_BUSY ? PH_BUSY : PH_RBUSY; continue; }
+                c.bad_ops |= ERR_HACK_LIMIT;
+            }
+            if (ph == PH_MAIN || ph == PH_BUSY) {
+                // the agent frame i (and its hack frames) is complete
+                if (!done && i < K - 1) { i++; ph = PH_MAIN; continue; }
+                last = done ? i : K - 1;
+                if (!(want_obs && done && last < K - 1)) break;
+                copy_console(live, snap);
+                c.load(snap.sc, snap.idx);
+                j = 0;
+                ph = last > 0 ? PH_REPLAY : PH_FINAL;
+            } else {
+                // replayed frame j complete: count only the frames the reference re-emulates
+                if (!rj) {
                     ev.frames = f0;
                     c.instructions = i0;
                     c.bad_ops = b0 | (c.bad_ops & ERR_HACK_LIMIT);
                 }
+                j++;
+                ph = j < last ? PH_REPLAY : PH_FINAL;
             }
-            nes_frame(kButtons[(acts >> (3 * last)) & 7], true, gray0);
         }
         if (want_obs) ev.pooled = mp && last >= 1;
         bool tm = done;

@@ -76,14 +76,15 @@ __device__ __forceinline__ uint8_t area_pixel(const uint8_t* g0, const uint8_t* 
 struct RomArgs {
     const uint8_t* rom;      // 0x8000 PRG (mirrored) + 0x2000 CHR
     const uint8_t* lut;      // 256
-    uint16_t nt[4];
+    uint32_t nt_bits;        // bit k: name table k maps to VRAM $400
 };
 
-__device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom) {
+__device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_cyc) {
     Cart c;
     c.prg = s_rom;
     c.chr = s_rom + 0x8000;
-    for (int i = 0; i < 4; i++) c.nt[i] = R.nt[i];
+    c.cyc = s_cyc;
+    c.nt_bits = R.nt_bits;
     return c;
 }
 
@@ -195,7 +196,7 @@ __device__ inline void boot_lane(const BootArgs& A, const LaneCtx& x, int l) {
     attach(c, x, A.mem + l, A.nlp);
     c.gray = A.gray + l; c.render = true;
     c.power_on();
-    auto fr = [&](uint8_t b) { c.joy_buttons[0] = b; c.frame(); };
+    auto fr = [&](uint8_t b) { c.joy_buttons0 = b; c.frame(); };
     const int w = A.levels[3 * l], s = A.levels[3 * l + 1], ar = A.levels[3 * l + 2];
     fr(8); fr(0);
     int guard = 0;
@@ -322,7 +323,7 @@ __device__ inline void raw_lane(const RawArgs& A, const LaneCtx& x, uint32_t e) 
         c.power_on();
     } else {
         c.load(A.sc, e);
-        c.joy_buttons[0] = A.buttons[e];
+        c.joy_buttons0 = A.buttons[e];
         c.render = A.render != 0;
         c.frame();
     }

@@ -22,11 +22,11 @@ using namespace mh;
 namespace {
 
 // Stage PRG + CHR (40 KB) and the gray LUT in LDS; every thread of the block must call this.
-__device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint8_t* s_lut) {
+__device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint8_t* s_lut, uint8_t* s_cyc) {
     const uint4* src = (const uint4*)R.rom;
     uint4* dst = (uint4*)s_rom;
     for (int i = threadIdx.x; i < 0xa000 / 16; i += blockDim.x) dst[i] = src[i];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) s_lut[i] = R.lut[i];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) { s_lut[i] = R.lut[i]; s_cyc[i] = kCycles[i]; }
     __syncthreads();
 }
 
@@ -34,40 +34,41 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
 #define ROM_LDS                                                     \
     __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000]; \
     __shared__ uint8_t s_lut[256];                                  \
+    __shared__ uint8_t s_cyc[256];                                  \
     __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
     __shared__ uint32_t s_gp[LDS_GP_WORDS * LDS_LANES];
 
 __device__ __forceinline__ LaneCtx lane_ctx(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_lut,
-                                            uint32_t* s_sp, uint32_t* s_gp) {
-    return LaneCtx{make_cart(R, s_rom), s_lut, s_sp + threadIdx.x, s_gp + threadIdx.x};
+                                            const uint8_t* s_cyc, uint32_t* s_sp, uint32_t* s_gp) {
+    return LaneCtx{make_cart(R, s_rom, s_cyc), s_lut, s_sp + threadIdx.x, s_gp + threadIdx.x};
 }
 
 __global__ void __launch_bounds__(64) k_boot(BootArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut);
+    stage_rom(A.R, s_rom, s_lut, s_cyc);
     const int l = blockIdx.x * blockDim.x + threadIdx.x;
-    if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), l);
+    if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), l);
 }
 
 __global__ void __launch_bounds__(64) k_cache(CacheArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut);
+    stage_rom(A.R, s_rom, s_lut, s_cyc);
     const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), ci);
+    if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), ci);
 }
 
 __global__ void __launch_bounds__(64) k_step(StepArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut);
+    stage_rom(A.R, s_rom, s_lut, s_cyc);
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), e);
+    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), e);
 }
 
 __global__ void __launch_bounds__(64) k_raw(RawArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut);
+    stage_rom(A.R, s_rom, s_lut, s_cyc);
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_sp, s_gp), e);
+    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), e);
 }
 
 __global__ void __launch_bounds__(64) k_reset(ResetArgs A) {
@@ -366,7 +367,8 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
         !ok(hipMemcpy(h->ev, ev.data(), ev.size() * 4, hipMemcpyHostToDevice), "upload env words"))
         return fail();
     h->R.rom = d_rom; h->R.lut = d_lut;
-    for (int i = 0; i < 4; i++) h->R.nt[i] = nt[i];
+    h->R.nt_bits = 0;
+    for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     // boot every level, build the reset cache
     BootArgs ba{h->R, h->nl, h->nlp, d_levels, h->boot_mem, h->boot_sc, h->boot_gray, h->x0, h->t0, d_err};
     hipLaunchKernelGGL(k_boot, dim3((h->nl + 63) / 64), dim3(64), 0, 0, ba);
@@ -552,7 +554,8 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     if (!ok(hipMemcpy(d_rom, img.data(), 0xa000, hipMemcpyHostToDevice), "upload rom") ||
         !ok(hipMemcpy(d_lut, ident, 256, hipMemcpyHostToDevice), "upload lut")) { delete h; return nullptr; }
     h->R.rom = d_rom; h->R.lut = d_lut;
-    for (int i = 0; i < 4; i++) h->R.nt[i] = nt[i];
+    h->R.nt_bits = 0;
+    for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, 1};
     hipLaunchKernelGGL(k_raw, dim3(h->np / 64), dim3(64), 0, 0, ra);
     if (!ok(hipDeviceSynchronize(), "raw power-on")) { delete h; return nullptr; }

@@ -51,7 +51,8 @@ __device__ __constant__ static const uint8_t kCycles[256] = {
 struct Cart {
     const uint8_t* prg;      // 0x8000 bytes (16 KB images mirrored)
     const uint8_t* chr;      // 0x2000 bytes
-    uint16_t nt[4];
+    const uint8_t* cyc;      // kCycles (LDS copy)
+    uint32_t nt_bits;        // bit k set: name table k ($2000 + k * $400) maps to VRAM $400, else to $000
 };
 
 struct Console {
@@ -70,7 +71,8 @@ struct Console {
     uint32_t iter_hi;
     int32_t cur, skip;
     // ---- joypads
-    uint8_t joy_strobe[2], joy_buttons[2], joy_bits[2];
+    // two ports as separate scalars: a dynamically indexed array would put the object in scratch
+    uint8_t joy_strobe0, joy_strobe1, joy_buttons0, joy_buttons1, joy_bits0, joy_bits1;
     // ---- PPU
     uint8_t pstate, even, vblank, s0hit, first_write, data_buffer, oam_addr, fine_x;
     uint8_t show_bg, show_spr, hide_edge_bg, hide_edge_spr, long_spr, nmi_en, bg_page, spr_page;
@@ -111,9 +113,9 @@ struct Console {
         ppu_calls = 0;
         pc = (uint16_t)w(S_PC); sp = (uint8_t)w(S_SP); a = (uint8_t)w(S_A); x = (uint8_t)w(S_X);
         y = (uint8_t)w(S_Y); p = (uint8_t)w(S_P); zero_skip = (uint8_t)w(S_ZERO_SKIP);
-        joy_strobe[0] = (uint8_t)w(S_JOY_STROBE0); joy_strobe[1] = (uint8_t)w(S_JOY_STROBE1);
-        joy_buttons[0] = (uint8_t)w(S_JOY_BUTTONS0); joy_buttons[1] = (uint8_t)w(S_JOY_BUTTONS1);
-        joy_bits[0] = (uint8_t)w(S_JOY_BITS0); joy_bits[1] = (uint8_t)w(S_JOY_BITS1);
+        joy_strobe0 = (uint8_t)w(S_JOY_STROBE0); joy_strobe1 = (uint8_t)w(S_JOY_STROBE1);
+        joy_buttons0 = (uint8_t)w(S_JOY_BUTTONS0); joy_buttons1 = (uint8_t)w(S_JOY_BUTTONS1);
+        joy_bits0 = (uint8_t)w(S_JOY_BITS0); joy_bits1 = (uint8_t)w(S_JOY_BITS1);
         pstate = (uint8_t)w(S_PSTATE); even = (uint8_t)w(S_EVEN); vblank = (uint8_t)w(S_VBLANK);
         s0hit = (uint8_t)w(S_S0HIT); first_write = (uint8_t)w(S_FIRST_WRITE);
         data_buffer = (uint8_t)w(S_DATA_BUFFER); oam_addr = (uint8_t)w(S_OAM_ADDR); fine_x = (uint8_t)w(S_FINE_X);
@@ -132,9 +134,9 @@ struct Console {
         auto w = [&](int k, uint32_t val) { sc[(size_t)k * np + e] = val; };
         w(S_ITER_LO, iter_lo); w(S_ITER_HI, iter_hi); w(S_EXEC_REL, (uint32_t)exec_at);
         w(S_PC, pc); w(S_SP, sp); w(S_A, a); w(S_X, x); w(S_Y, y); w(S_P, p); w(S_ZERO_SKIP, zero_skip);
-        w(S_JOY_STROBE0, joy_strobe[0]); w(S_JOY_STROBE1, joy_strobe[1]);
-        w(S_JOY_BUTTONS0, joy_buttons[0]); w(S_JOY_BUTTONS1, joy_buttons[1]);
-        w(S_JOY_BITS0, joy_bits[0]); w(S_JOY_BITS1, joy_bits[1]);
+        w(S_JOY_STROBE0, joy_strobe0); w(S_JOY_STROBE1, joy_strobe1);
+        w(S_JOY_BUTTONS0, joy_buttons0); w(S_JOY_BUTTONS1, joy_buttons1);
+        w(S_JOY_BITS0, joy_bits0); w(S_JOY_BITS1, joy_bits1);
         w(S_PSTATE, pstate); w(S_EVEN, even); w(S_VBLANK, vblank); w(S_S0HIT, s0hit);
         w(S_FIRST_WRITE, first_write); w(S_DATA_BUFFER, data_buffer); w(S_OAM_ADDR, oam_addr);
         w(S_FINE_X, fine_x); w(S_SHOW_BG, show_bg); w(S_SHOW_SPR, show_spr);
@@ -148,7 +150,7 @@ struct Console {
     __device__ void power_on() {
         for (uint32_t r = 0; r < MEM_ROWS; r++) st(r, 0);
         iter_lo = iter_hi = 0; exec_at = 0; ppu_calls = 0;
-        joy_strobe[0] = joy_strobe[1] = 1; joy_buttons[0] = joy_buttons[1] = 0; joy_bits[0] = joy_bits[1] = 0;
+        joy_strobe0 = joy_strobe1 = 1; joy_buttons0 = joy_buttons1 = 0; joy_bits0 = joy_bits1 = 0;
         zero_skip = 0; a = x = y = 0; p = 0x34;
         pc = (uint16_t)(prg(0xfffc) | prg(0xfffd) << 8);
         sp = 0xfd;
@@ -161,13 +163,19 @@ struct Console {
     }
 
     // ------------------------------------------------------------ CPU bus (nes_core.hpp:150-208)
-    __device__ uint8_t read(uint16_t ad) {
+    // Accesses for which needs_sync() holds see the PPU caught up to 3 * (cur + 1): frame() syncs
+    // before it issues them (the reference catches up inside the access; the target is the same).
+    __device__ __forceinline__ static bool needs_sync(uint16_t ad, bool wr) {
+        if (ad >= 0x2000 && ad < 0x4000) return wr || (ad & 7) == 2 || (ad & 7) == 7;
+        return wr && ad == 0x4014;
+    }
+    __device__ __forceinline__ uint8_t read(uint16_t ad) {
         if (ad >= 0x8000) return prg(ad);
         if (ad < 0x2000) return ram(ad);
         if (ad < 0x4000) {
-            uint16_t r = ad & 0x2007;
-            if (r == 0x2002) { catch_up(); return status_read(); }
-            if (r == 0x2007) { catch_up(); return data_read(); }
+            const uint16_t r = ad & 0x2007;
+            if (r == 0x2002) return status_read();
+            if (r == 0x2007) return data_read();
             if (r == 0x2004) return oam(oam_addr);
             return 0;
         }
@@ -175,44 +183,48 @@ struct Console {
         if (ad == 0x4017) return pad_read(1);
         return 0;
     }
-    __device__ void write(uint16_t ad, uint8_t val) {
+    __device__ __forceinline__ void write(uint16_t ad, uint8_t val) {
         if (ad < 0x2000) { st(ROW_RAM + (ad & 0x7ff), val); return; }
         if (ad < 0x4000) {
             // a pending sprite evaluation is materialized before its inputs (OAM, oam_addr, sprite
             // size) change; the sprite line buffer is rebuilt after any write that can change it
-            switch (ad & 0x2007) {
-                case 0x2000: catch_up(); materialize_sprites(); ctrl_write(val); sp_line = -1; break;
-                case 0x2001: catch_up(); mask_write(val); break;
-                case 0x2003: catch_up(); materialize_sprites(); oam_addr = val; break;
-                case 0x2004: catch_up(); materialize_sprites(); st(ROW_OAM + oam_addr, val); oam_addr++; sp_line = -1; break;
-                case 0x2005: catch_up(); scroll_write(val); break;
-                case 0x2006: catch_up(); addr_write(val); break;
-                case 0x2007: catch_up(); data_write(val); sp_line = -1; break;
+            const uint16_t r = ad & 0x2007;
+            if (r == 0x2000 || r == 0x2003 || r == 0x2004) materialize_sprites();
+            switch (r) {
+                case 0x2000: ctrl_write(val); sp_line = -1; break;
+                case 0x2001: mask_write(val); break;
+                case 0x2003: oam_addr = val; break;
+                case 0x2004: st(ROW_OAM + oam_addr, val); oam_addr++; sp_line = -1; break;
+                case 0x2005: scroll_write(val); break;
+                case 0x2006: addr_write(val); break;
+                case 0x2007: data_write(val); sp_line = -1; break;
                 default: break;
             }
             return;
         }
         if (ad == 0x4014) {  // OAM DMA: 513 cycles, +1 on an odd absolute cycle; copies from RAM pages only
-            catch_up();
             materialize_sprites();
             skip += 513 + (int)((iter_lo + (uint32_t)cur + 1u) & 1u);
-            uint16_t src = (uint16_t)(val << 8);
+            const uint16_t src = (uint16_t)(val << 8);
             if (src < 0x2000)
                 for (int i = 0; i < 256; i++) st(ROW_OAM + ((oam_addr + i) & 0xff), ram(src + i));
             sp_line = -1;
             return;
         }
         if (ad == 0x4016) {
-            for (int i = 0; i < 2; i++) {
-                joy_strobe[i] = val & 1;
-                if (!joy_strobe[i]) joy_bits[i] = joy_buttons[i];
-            }
+            joy_strobe0 = joy_strobe1 = val & 1;
+            if (!(val & 1)) { joy_bits0 = joy_buttons0; joy_bits1 = joy_buttons1; }
         }
     }
-    __device__ uint8_t pad_read(int i) {
+    __device__ __forceinline__ uint8_t pad_read(int i) {
         uint8_t bit;
-        if (joy_strobe[i]) bit = joy_buttons[i] & 1;
-        else { bit = joy_bits[i] & 1; joy_bits[i] >>= 1; }
+        if (i == 0) {
+            if (joy_strobe0) bit = joy_buttons0 & 1;
+            else { bit = joy_bits0 & 1; joy_bits0 >>= 1; }
+        } else {
+            if (joy_strobe1) bit = joy_buttons1 & 1;
+            else { bit = joy_bits1 & 1; joy_bits1 >>= 1; }
+        }
         return bit | 0x40;
     }
 
@@ -248,8 +260,8 @@ struct Console {
 
     // ------------------------------------------------------------ picture bus (nes_core.hpp:263-285)
     __device__ __forceinline__ uint32_t nt_row(uint16_t ad) const {
-        int k = ad < 0x2400 ? 0 : ad < 0x2800 ? 1 : ad < 0x2c00 ? 2 : 3;
-        return cart.nt[k] + (ad & 0x3ff);
+        const uint32_t k = ad < 0x2400 ? 0 : ad < 0x2800 ? 1 : ad < 0x2c00 ? 2 : 3;
+        return (((cart.nt_bits >> k) & 1u) << 10) | (ad & 0x3ffu);
     }
     __device__ uint8_t vbus_read(uint16_t ad) const {
         if (ad < 0x2000) return cart.chr[ad];
@@ -262,7 +274,9 @@ struct Console {
         if (ad < 0x3eff) st(ROW_VRAM + nt_row(ad), d);
         else if (ad < 0x3fff) { st(ROW_PAL + (ad == 0x3f10 ? 0 : (ad & 0x1f)), d); pal_dirty = true; }
     }
-    __device__ __forceinline__ uint8_t nametable(uint16_t ad) const { return vram(cart.nt[(ad >> 10) & 3] + (ad & 0x3ff)); }
+    __device__ __forceinline__ uint8_t nametable(uint16_t ad) const {
+        return vram((((cart.nt_bits >> ((ad >> 10) & 3u)) & 1u) << 10) | (ad & 0x3ffu));
+    }
 
     // ------------------------------------------------------------ PPU timing (nes_core.hpp:289-308)
     __device__ void nmi_threshold() {
@@ -275,7 +289,6 @@ struct Console {
     __device__ void advance_to(int32_t target) {
         if (target > ppu_calls) { ppu_run(target - ppu_calls); nmi_threshold(); }
     }
-    __device__ void catch_up() { advance_to(3 * (cur + 1)); }
 
     __device__ void coarse_x_add(int n) {
         int tot = (v & 0x1f) + n;
@@ -543,175 +556,242 @@ struct Console {
     __device__ __forceinline__ void set_nz(uint8_t r) { p = (uint8_t)((p & ~(FZ | FN)) | (r ? 0 : FZ) | (r & 0x80 ? FN : 0)); }
     __device__ __forceinline__ void flag(uint8_t f, bool on) { p = on ? (uint8_t)(p | f) : (uint8_t)(p & ~f); }
     __device__ __forceinline__ bool has(uint8_t f) const { return (p & f) != 0; }
-    __device__ uint16_t read16(uint16_t ad) { uint8_t lo = read(ad); uint8_t hi = read((uint16_t)(ad + 1)); return (uint16_t)(lo | hi << 8); }
     __device__ __forceinline__ void push(uint8_t d) { st(ROW_RAM + ((0x100 | sp) & 0x7ff), d); sp--; }
     __device__ __forceinline__ uint8_t pull() { sp++; return ram(0x100 | sp); }
     __device__ __forceinline__ void cross_penalty(uint16_t u, uint16_t w, int k) { if ((u & 0xff00) != (w & 0xff00)) skip += k; }
 
-    __device__ bool op_implied(uint8_t op) {
-        switch (op) {
-            case 0x00:
-                pc++;
-                push((uint8_t)(pc >> 8)); push((uint8_t)pc); push((uint8_t)(p | 0x30));
-                p |= FI; pc = read16(0xfffe); skip += 7;
-                return true;
-            case 0x08: push(p); return true;
-            case 0x18: flag(FC, false); return true;
-            case 0x20: { uint16_t ret = (uint16_t)(pc + 1); push((uint8_t)(ret >> 8)); push((uint8_t)ret); pc = read16(pc); return true; }
-            case 0x28: p = pull(); return true;
-            case 0x38: flag(FC, true); return true;
-            case 0x40: { p = pull(); uint8_t lo = pull(); uint8_t hi = pull(); pc = (uint16_t)(lo | hi << 8); return true; }
-            case 0x48: push(a); return true;
-            case 0x4c: pc = read16(pc); return true;
-            case 0x58: flag(FI, false); return true;
-            case 0x60: { uint8_t lo = pull(); uint8_t hi = pull(); pc = (uint16_t)((lo | hi << 8) + 1); return true; }
-            case 0x68: a = pull(); set_nz(a); return true;
-            case 0x6c: {
-                uint16_t ptr = read16(pc);
-                uint8_t lo = read(ptr);
-                uint8_t hi = read((uint16_t)((ptr & 0xff00) | ((ptr + 1) & 0xff)));
-                pc = (uint16_t)(lo | hi << 8);
-                return true;
-            }
-            case 0x78: flag(FI, true); return true;
-            case 0x88: y--; set_nz(y); return true;
-            case 0x8a: a = x; set_nz(a); return true;
-            case 0x98: a = y; set_nz(a); return true;
-            case 0x9a: sp = x; return true;
-            case 0xa8: y = a; set_nz(y); return true;
-            case 0xaa: x = a; set_nz(x); return true;
-            case 0xb8: flag(FV, false); return true;
-            case 0xba: x = sp; set_nz(x); return true;
-            case 0xc8: y++; set_nz(y); return true;
-            case 0xca: x--; set_nz(x); return true;
-            case 0xd8: flag(FD, false); return true;
-            case 0xe8: x++; set_nz(x); return true;
-            case 0xea: return true;
-            case 0xf8: flag(FD, true); return true;
-            default: return false;
-        }
+    // Opcode families in the reference's decode order: implied, branch, type 1, type 2, type 0.
+    enum : uint8_t { F_IMP, F_BR, F_G1, F_G2, F_G0, F_BAD };
+    // addressing of the type 0/1/2 families
+    enum : uint8_t { A_NONE, A_IMM, A_ZP, A_ZPI, A_ABS, A_ABSI, A_INDX, A_INDY };
+    // Bus steps of an instruction. The steps after the current one are queued in Ins::prog, 3 bits
+    // each, lowest first: operand byte (B1), operand word (W1, W2), JMP-indirect pointer (PLO, PHI),
+    // data read (DR), data write (DW).
+    enum : uint8_t { U_END = 0, U_B1, U_W1, U_W2, U_PLO, U_PHI, U_DR, U_DW, U_OP, U_START };
+
+    // The instruction in flight.
+    struct Ins {
+        uint32_t prog;
+        uint16_t ea;
+        uint8_t op, fam, fn, am, idx, b1, lo, hi, val, wv, pb1, pb2;
+        bool pen, pf, ok, executed;
+    };
+
+    // the reference's implied-opcode table (nes_core.hpp:640-690)
+    __device__ __forceinline__ static bool is_implied(uint8_t op) {
+        const uint8_t cc = op & 3, bbb = (op >> 2) & 7, aaa = op >> 5;
+        if (cc == 0) return bbb == 2 || bbb == 6 || (bbb == 0 && aaa < 4) || op == 0x4c || op == 0x6c;
+        return cc == 2 && aaa >= 4 && (bbb == 2 || (bbb == 6 && aaa < 6));
     }
-    __device__ bool op_branch(uint8_t op) {
-        if ((op & 0x1f) != 0x10) return false;
-        const uint8_t which = (op >> 6) == 0 ? FN : (op >> 6) == 1 ? FV : (op >> 6) == 2 ? FC : FZ;
-        bool take = has(which) == ((op & 0x20) != 0);
-        if (take) {
-            int8_t off = (int8_t)read(pc++);
-            skip += 1;
-            uint16_t to = (uint16_t)(pc + off);
-            cross_penalty(pc, to, 2);
-            pc = to;
+
+    // Decode the opcode (pc is past it): family, addressing, the queue of bus steps, and the whole
+    // effect of implied instructions without bus steps.
+    __device__ __forceinline__ void decode(Ins& I) {
+        const uint8_t op = I.op, cc = op & 3, bbb = (op >> 2) & 7, fn = op >> 5;
+        I.fn = fn; I.prog = 0; I.am = A_NONE; I.idx = 0; I.pen = false; I.ok = true; I.executed = false;
+        if (is_implied(op)) {
+            I.fam = F_IMP;
+            I.executed = true;
+            switch (op) {
+                case 0x00:
+                    pc++;
+                    push((uint8_t)(pc >> 8)); push((uint8_t)pc); push((uint8_t)(p | 0x30));
+                    p |= FI; pc = (uint16_t)(prg(0xfffe) | prg(0xffff) << 8); skip += 7;
+                    break;
+                case 0x08: push(p); break;
+                case 0x18: flag(FC, false); break;
+                case 0x20: { const uint16_t ret = (uint16_t)(pc + 1); push((uint8_t)(ret >> 8)); push((uint8_t)ret);
+                             I.prog = U_W1 | U_W2 << 3; break; }
+                case 0x28: p = pull(); break;
+                case 0x38: flag(FC, true); break;
+                case 0x40: { p = pull(); const uint8_t lo = pull(); const uint8_t hi = pull(); pc = (uint16_t)(lo | hi << 8); break; }
+                case 0x48: push(a); break;
+                case 0x4c: I.prog = U_W1 | U_W2 << 3; break;
+                case 0x58: flag(FI, false); break;
+                case 0x60: { const uint8_t lo = pull(); const uint8_t hi = pull(); pc = (uint16_t)((lo | hi << 8) + 1); break; }
+                case 0x68: a = pull(); set_nz(a); break;
+                case 0x6c: I.prog = U_W1 | U_W2 << 3 | U_PLO << 6 | U_PHI << 9; break;
+                case 0x78: flag(FI, true); break;
+                case 0x88: y--; set_nz(y); break;
+                case 0x8a: a = x; set_nz(a); break;
+                case 0x98: a = y; set_nz(a); break;
+                case 0x9a: sp = x; break;
+                case 0xa8: y = a; set_nz(y); break;
+                case 0xaa: x = a; set_nz(x); break;
+                case 0xb8: flag(FV, false); break;
+                case 0xba: x = sp; set_nz(x); break;
+                case 0xc8: y++; set_nz(y); break;
+                case 0xca: x--; set_nz(x); break;
+                case 0xd8: flag(FD, false); break;
+                case 0xe8: x++; set_nz(x); break;
+                case 0xf8: flag(FD, true); break;
+                default: break;   // 0xea NOP
+            }
+            return;
+        }
+        if ((op & 0x1f) == 0x10) {
+            I.fam = F_BR;
+            I.executed = true;
+            const uint8_t which = fn >> 1 == 0 ? FN : fn >> 1 == 1 ? FV : fn >> 1 == 2 ? FC : FZ;
+            if (has(which) == ((op & 0x20) != 0)) I.prog = U_B1;
+            else pc++;
+            return;
+        }
+        uint32_t data;   // data steps after the addressing steps
+        if (cc == 1) {
+            I.fam = F_G1;
+            I.am = bbb == 0 ? A_INDX : bbb == 1 ? A_ZP : bbb == 2 ? A_IMM : bbb == 3 ? A_ABS
+                 : bbb == 4 ? A_INDY : bbb == 5 ? A_ZPI : A_ABSI;
+            I.idx = bbb == 6 || bbb == 4 ? y : x;
+            I.pen = fn != 4;
+            data = fn == 4 ? U_DW : U_DR;
+        } else if (cc == 2 && bbb != 4 && bbb != 6) {
+            I.fam = F_G2;
+            I.am = bbb == 0 ? A_IMM : bbb == 1 ? A_ZP : bbb == 2 ? A_NONE : bbb == 3 ? A_ABS : bbb == 5 ? A_ZPI : A_ABSI;
+            I.idx = fn == 4 || fn == 5 ? y : x;
+            I.pen = true;
+            data = fn == 4 ? U_DW : fn == 5 ? U_DR : bbb == 2 ? U_END : (U_DR | U_DW << 3);
+        } else if (cc == 0 && (bbb & 1 || bbb == 0)) {
+            I.fam = F_G0;
+            I.am = bbb == 0 ? A_IMM : bbb == 1 ? A_ZP : bbb == 3 ? A_ABS : bbb == 5 ? A_ZPI : A_ABSI;
+            I.idx = x;
+            I.pen = true;
+            I.ok = fn == 1 || fn >= 4;
+            I.executed = !I.ok;   // an invalid operation still performs its addressing reads
+            data = !I.ok ? U_END : fn == 4 ? U_DW : U_DR;
         } else {
-            pc++;
+            I.fam = F_BAD;
+            I.ok = false;
+            I.executed = true;
+            return;
         }
-        return true;
-    }
-    __device__ bool op_group0(uint8_t op) {
-        if ((op & 3) != 0) return false;
-        uint16_t ea;
-        switch ((op >> 2) & 7) {
-            case 0: ea = pc++; break;
-            case 1: ea = read(pc++); break;
-            case 3: ea = read16(pc); pc += 2; break;
-            case 5: ea = (uint8_t)(read(pc++) + x); break;
-            case 7: ea = read16(pc); pc += 2; cross_penalty(ea, (uint16_t)(ea + x), 1); ea = (uint16_t)(ea + x); break;
-            default: return false;
-        }
-        switch (op >> 5) {
-            case 1: { uint8_t d = read(ea); flag(FZ, !(a & d)); flag(FV, d & 0x40); flag(FN, d & 0x80); return true; }
-            case 4: write(ea, y); return true;
-            case 5: y = read(ea); set_nz(y); return true;
-            case 6: { uint16_t r = (uint16_t)(y - read(ea)); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); return true; }
-            case 7: { uint16_t r = (uint16_t)(x - read(ea)); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); return true; }
-            default: return false;
+        switch (I.am) {
+            case A_IMM: I.ea = pc++; I.prog = data; break;
+            case A_NONE: I.prog = data; break;
+            case A_ABS: case A_ABSI: I.prog = U_W1 | U_W2 << 3 | data << 6; break;
+            default: I.prog = U_B1 | data << 3; break;
         }
     }
-    __device__ bool op_group1(uint8_t op) {
-        if ((op & 3) != 1) return false;
-        int fn = op >> 5;
-        bool store = fn == 4;
-        uint16_t ea;
-        switch ((op >> 2) & 7) {
-            case 0: { uint8_t z = (uint8_t)(x + read(pc++)); uint8_t lo = read(z); uint8_t hi = read((uint8_t)(z + 1)); ea = (uint16_t)(lo | hi << 8); break; }
-            case 1: ea = read(pc++); break;
-            case 2: ea = pc++; break;
-            case 3: ea = read16(pc); pc += 2; break;
-            case 4: {
-                uint8_t z = read(pc++); uint8_t lo = read(z); uint8_t hi = read((uint8_t)(z + 1));
-                ea = (uint16_t)(lo | hi << 8);
-                if (!store) cross_penalty(ea, (uint16_t)(ea + y), 1);
-                ea = (uint16_t)(ea + y);
+    // effective address once the operand bytes are in (type 0/1/2 families)
+    __device__ __forceinline__ void finish_address(Ins& I) {
+        const uint16_t w = (uint16_t)(I.lo | I.hi << 8);
+        switch (I.am) {
+            case A_ZP: I.ea = I.b1; break;
+            case A_ZPI: I.ea = (uint8_t)(I.b1 + I.idx); break;
+            case A_ABS: I.ea = w; break;
+            case A_ABSI: if (I.pen) cross_penalty(w, (uint16_t)(w + I.idx), 1); I.ea = (uint16_t)(w + I.idx); break;
+            case A_INDX: case A_INDY: {
+                const uint8_t z = I.am == A_INDX ? (uint8_t)(I.b1 + x) : I.b1;
+                const uint16_t base = (uint16_t)(ram(z) | ram((uint8_t)(z + 1)) << 8);
+                if (I.am == A_INDX) { I.ea = base; break; }
+                if (I.pen) cross_penalty(base, (uint16_t)(base + I.idx), 1);
+                I.ea = (uint16_t)(base + I.idx);
                 break;
             }
-            case 5: ea = (uint8_t)(read(pc++) + x); break;
-            case 6: ea = read16(pc); pc += 2; if (!store) cross_penalty(ea, (uint16_t)(ea + y), 1); ea = (uint16_t)(ea + y); break;
-            default: ea = read16(pc); pc += 2; if (!store) cross_penalty(ea, (uint16_t)(ea + x), 1); ea = (uint16_t)(ea + x); break;
+            default: break;
         }
-        switch (fn) {
-            case 0: a |= read(ea); set_nz(a); break;
-            case 1: a &= read(ea); set_nz(a); break;
-            case 2: a ^= read(ea); set_nz(a); break;
-            case 3: {
-                uint8_t d = read(ea);
-                uint16_t s = (uint16_t)(a + d + (has(FC) ? 1 : 0));
-                flag(FC, s & 0x100); flag(FV, (a ^ s) & (d ^ s) & 0x80);
-                a = (uint8_t)s; set_nz(a);
-                break;
-            }
-            case 4: write(ea, a); break;
-            case 5: a = read(ea); set_nz(a); break;
-            case 6: { uint16_t r = (uint16_t)(a - read(ea)); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
-            default: {
-                uint16_t d = read(ea);
-                uint16_t r = (uint16_t)(a - d - (has(FC) ? 0 : 1));
-                flag(FC, !(r & 0x100)); flag(FV, (a ^ r) & (~d ^ r) & 0x80);
-                a = (uint8_t)r; set_nz((uint8_t)r);
-                break;
-            }
-        }
-        return true;
     }
-    __device__ bool op_group2(uint8_t op) {
-        if ((op & 3) != 2) return false;
-        int fn = op >> 5, mode = (op >> 2) & 7;
-        bool xy = fn == 4 || fn == 5;
-        uint16_t ea = 0;
-        switch (mode) {
-            case 0: ea = pc++; break;
-            case 1: ea = read(pc++); break;
-            case 2: break;
-            case 3: ea = read16(pc); pc += 2; break;
-            case 5: ea = (uint8_t)(read(pc++) + (xy ? y : x)); break;
-            case 7: { ea = read16(pc); pc += 2; uint8_t ix = xy ? y : x; cross_penalty(ea, (uint16_t)(ea + ix), 1); ea = (uint16_t)(ea + ix); break; }
-            default: return false;
-        }
-        switch (fn) {
-            case 0: case 1: {
-                bool cin = has(FC) && fn == 1;
-                if (mode == 2) { flag(FC, a & 0x80); a = (uint8_t)((a << 1) | cin); set_nz(a); }
-                else { uint8_t d = read(ea); flag(FC, d & 0x80); d = (uint8_t)((d << 1) | cin); set_nz(d); write(ea, d); }
-                break;
+    // Operation of the type 0/1/2 families after their data read; sets Ins::wv for a data write.
+    __device__ __forceinline__ void execute(Ins& I) {
+        I.executed = true;
+        const uint8_t fn = I.fn, d = I.val;
+        if (I.fam == F_G1) {
+            switch (fn) {
+                case 0: a |= d; set_nz(a); break;
+                case 1: a &= d; set_nz(a); break;
+                case 2: a ^= d; set_nz(a); break;
+                case 3: {
+                    const uint16_t s = (uint16_t)(a + d + (has(FC) ? 1 : 0));
+                    flag(FC, s & 0x100); flag(FV, (a ^ s) & (d ^ s) & 0x80);
+                    a = (uint8_t)s; set_nz(a);
+                    break;
+                }
+                case 4: I.wv = a; break;
+                case 5: a = d; set_nz(a); break;
+                case 6: { const uint16_t r = (uint16_t)(a - d); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
+                default: {
+                    const uint16_t r = (uint16_t)(a - d - (has(FC) ? 0 : 1));
+                    flag(FC, !(r & 0x100)); flag(FV, (a ^ r) & (~d ^ r) & 0x80);
+                    a = (uint8_t)r; set_nz((uint8_t)r);
+                    break;
+                }
             }
-            case 2: case 3: {
-                bool cin = has(FC) && fn == 3;
-                if (mode == 2) { flag(FC, a & 1); a = (uint8_t)((a >> 1) | (cin << 7)); set_nz(a); }
-                else { uint8_t d = read(ea); flag(FC, d & 1); d = (uint8_t)((d >> 1) | (cin << 7)); set_nz(d); write(ea, d); }
-                break;
+        } else if (I.fam == F_G2) {
+            const bool acc = I.am == A_NONE;
+            switch (fn) {
+                case 0: case 1: case 2: case 3: {
+                    const bool cin = has(FC) && (fn & 1);
+                    const uint8_t s = acc ? a : d;
+                    uint8_t r;
+                    if (fn < 2) { flag(FC, s & 0x80); r = (uint8_t)((s << 1) | cin); }
+                    else { flag(FC, s & 1); r = (uint8_t)((s >> 1) | (cin << 7)); }
+                    set_nz(r);
+                    if (acc) a = r; else I.wv = r;
+                    break;
+                }
+                case 4: I.wv = x; break;
+                case 5: x = d; set_nz(x); break;
+                case 6: I.wv = (uint8_t)(d - 1); set_nz(I.wv); break;
+                default: I.wv = (uint8_t)(d + 1); set_nz(I.wv); break;
             }
-            case 4: write(ea, x); break;
-            case 5: x = read(ea); set_nz(x); break;
-            case 6: { uint8_t d = (uint8_t)(read(ea) - 1); set_nz(d); write(ea, d); break; }
-            default: { uint8_t d = (uint8_t)(read(ea) + 1); set_nz(d); write(ea, d); break; }
+        } else {
+            switch (fn) {
+                case 1: flag(FZ, !(a & d)); flag(FV, d & 0x40); flag(FN, d & 0x80); break;
+                case 4: I.wv = y; break;
+                case 5: y = d; set_nz(y); break;
+                case 6: { const uint16_t r = (uint16_t)(y - d); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
+                default: { const uint16_t r = (uint16_t)(x - d); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
+            }
         }
-        return true;
     }
-    __device__ int step_instruction() {
-        skip = 0;
-        uint8_t op = read(pc++);
-        instructions++;
-        if (op_implied(op) || op_branch(op) || op_group1(op) || op_group2(op) || op_group0(op)) skip += kCycles[op];
+    // the value v of bus step u arrived
+    __device__ __forceinline__ void consume(Ins& I, uint8_t u, uint8_t v) {
+        switch (u) {
+            case U_B1:
+                I.b1 = v; pc++;
+                if (I.fam == F_BR) {   // taken branch
+                    skip += 1;
+                    const uint16_t to = (uint16_t)(pc + (int8_t)v);
+                    cross_penalty(pc, to, 2);
+                    pc = to;
+                } else {
+                    finish_address(I);
+                }
+                break;
+            case U_W1: I.lo = v; break;
+            case U_W2:
+                I.hi = v;
+                if (I.fam == F_IMP) {
+                    if (I.op == 0x6c) I.ea = (uint16_t)(I.lo | v << 8);   // pointer of JMP (ind)
+                    else pc = (uint16_t)(I.lo | v << 8);                 // JMP / JSR target
+                } else {
+                    pc += 2;
+                    finish_address(I);
+                }
+                break;
+            case U_PLO: I.lo = v; break;
+            case U_PHI: pc = (uint16_t)(I.lo | v << 8); break;
+            case U_DR: I.val = v; break;
+            default: break;
+        }
+    }
+    // Next bus step of the instruction; operand bytes prefetched from PRG are taken without the bus.
+    // Returns U_START once the instruction is complete (cycles, exec_at and zero_skip are set then).
+    __device__ __forceinline__ uint8_t advance(Ins& I) {
+        uint8_t nx;
+        for (;;) {
+            nx = I.prog & 7;
+            I.prog >>= 3;
+            if (I.pf && nx >= U_B1 && nx <= U_W2) { consume(I, nx, nx == U_W2 ? I.pb2 : I.pb1); continue; }
+            break;
+        }
+        if (!I.executed && (nx == U_DW || nx == U_END)) execute(I);
+        if (nx != U_END) return nx;
+        if (I.ok) skip += cart.cyc[I.op];
         else bad_ops++;
-        return skip;
+        exec_at = cur + (skip >= 1 ? skip : 1);
+        zero_skip = skip <= 0;
+        return U_START;
     }
 
     // PPU calls from the current PPU position to (line, dot) on the frame timeline of
@@ -724,22 +804,14 @@ struct Console {
         return d;
     }
 
-    // Exact fast-forward of the sprite-0 wait loops `LDA $2002 / AND #$40 / BEQ|BNE *-5` (BEQ: wait
-    // for the hit, BNE: wait for the clear at the pre-render line). Iterations whose $2002 reads
-    // provably return the same value are not executed: they would only re-read an unchanged s0hit,
-    // clear an already clear vblank flag and set first_write, and the PPU is caught up lazily anyway.
-    // The span ends before the first dot where s0hit could change (sprite 0's first line, or the
-    // pre-render clear), before the NMI sync point and inside the frame. Returns true if it advanced.
-    __device__ bool poll_skip(int32_t j, int32_t end) {
-        if (pc < 0x8000 || pc > 0xfff8) return false;
-        if (prg(pc) != 0xad || prg(pc + 1) != 0x02 || prg(pc + 2) != 0x20 || prg(pc + 3) != 0x29 ||
-            prg(pc + 4) != 0x40 || prg(pc + 6) != 0xf9)
-            return false;
-        const uint8_t br = prg(pc + 5);
-        if (br != 0xf0 && br != 0xd0) return false;
-        cur = j;
-        advance_to(3 * (j + 1));                 // the sync the LDA $2002 at j performs
-        const bool wait_hit = br == 0xf0;
+    // Exact fast-forward of the sprite-0 wait loops `LDA $2002 / AND #$40 / BEQ|BNE *-5` at pc (BEQ:
+    // wait for the hit, BNE: wait for the clear at the pre-render line), with the PPU caught up to the
+    // read of the first iteration (at j). Iterations whose $2002 reads provably return the same value
+    // are not executed: they would only re-read an unchanged s0hit, clear an already clear vblank flag
+    // and set first_write, and the PPU is caught up lazily anyway. The span ends before the first dot
+    // where s0hit could change (sprite 0's first line, or the pre-render clear), before the NMI sync
+    // point and inside the frame. Returns true if it advanced.
+    __device__ __forceinline__ bool poll_skip(int32_t j, int32_t end, bool wait_hit) {
         if (wait_hit == (s0hit != 0)) return false;   // this read ends the loop: run it normally
         int32_t limit;                           // first PPU call count at which s0hit may differ
         if (wait_hit) {
@@ -782,40 +854,94 @@ struct Console {
         return true;
     }
 
-    // one nes-py Emulator::step (nes_core.hpp:1166-1204) with the exact `JMP *` idle fast-forward
-    __device__ void frame() {
+    // One nes-py Emulator::step (nes_core.hpp:1166-1204) with the exact `JMP *` idle fast-forward.
+    // Every lane runs the same loop body: at most one bus access per iteration, through one read
+    // and one write site, and one PPU catch-up site (`want`) for the NMI point, PPU-register
+    // accesses, the poll fast-forward and the frame end. Branching per opcode is confined to cheap
+    // register arithmetic, so a wave whose lanes run different instructions stays converged on the
+    // memory accesses.
+    __device__ __forceinline__ void frame() {
         const int32_t end = FRAME_ITERS;
-        while (exec_at < end) {
-            const int32_t j = exec_at;
-            if (3 * (j + 1) >= nmi_thresh) {
-                cur = j;
-                advance_to(3 * (j + 1));
-                if (exec_at != j) continue;
-            }
-            uint16_t here = pc;
-            if (here >= 0x8000 && prg(here) == 0x4c) {
-                uint16_t p1 = (uint16_t)(here + 1), p2 = (uint16_t)(here + 2);
-                uint8_t lo = p1 >= 0x8000 ? prg(p1) : 0xff, hi = p2 >= 0x8000 ? prg(p2) : 0xff;
-                if ((uint16_t)(lo | hi << 8) == here) {
-                    int32_t lim_end = end - j, lim_nmi = nmi_thresh - 3 * (j + 1);
-                    int32_t k1 = lim_end > 0 ? (lim_end + 2) / 3 : 0;
-                    int32_t k2 = lim_nmi > 0 ? (lim_nmi + 8) / 9 : 0;
-                    int32_t k = k1 < k2 ? k1 : k2;
+        Ins I;
+        I.pf = false; I.pb1 = I.pb2 = 0;
+        uint8_t u = U_START;
+        int32_t want = -1;
+        for (;;) {
+            if (want >= 0) { advance_to(want); want = -1; }
+            if (u == U_START) {
+                const int32_t j = exec_at;
+                if (j >= end) {
+                    if (ppu_calls < 3 * end) { want = 3 * end; continue; }
+                    break;
+                }
+                const int32_t tgt = 3 * (j + 1);
+                if (tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; continue; }
+                // PRG bytes at pc for the fast paths; the idle check reads 0xff past 0xffff
+                const bool in_prg = pc >= 0x8000;
+                uint8_t op0 = 0, q1 = 0xff, q2 = 0xff;
+                if (in_prg) {
+                    op0 = prg(pc);
+                    if (pc != 0xffff) q1 = prg((uint16_t)(pc + 1));
+                    if (pc < 0xfffe) q2 = prg((uint16_t)(pc + 2));
+                }
+                if (in_prg && op0 == 0x4c && (uint16_t)(q1 | q2 << 8) == pc) {
+                    const int32_t lim_end = end - j, lim_nmi = nmi_thresh - tgt;
+                    const int32_t k1 = lim_end > 0 ? (lim_end + 2) / 3 : 0;
+                    const int32_t k2 = lim_nmi > 0 ? (lim_nmi + 8) / 9 : 0;
+                    const int32_t k = k1 < k2 ? k1 : k2;
                     if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; continue; }
                 }
+                if (in_prg && op0 == 0xad && q1 == 0x02 && q2 == 0x20 && pc <= 0xfff8 && prg(pc + 3) == 0x29 &&
+                    prg(pc + 4) == 0x40 && prg(pc + 6) == 0xf9) {
+                    const uint8_t br = prg(pc + 5);
+                    if (br == 0xf0 || br == 0xd0) {
+                        if (ppu_calls < tgt) { want = tgt; continue; }   // the sync of the LDA $2002 at j
+                        if (poll_skip(j, end, br == 0xf0)) continue;
+                    }
+                }
+                cur = j;
+                skip = 0;
+                instructions++;
+                if (in_prg) {
+                    I.op = op0; I.pf = pc <= 0xfffd; I.pb1 = q1; I.pb2 = q2;
+                    pc++;
+                    decode(I);
+                    u = advance(I);
+                    if (u == U_START) continue;
+                } else {
+                    I.pf = false;
+                    u = U_OP;
+                }
             }
-            if (poll_skip(j, end)) continue;
-            cur = j;
-            int s = step_instruction();
-            exec_at = j + (s >= 1 ? s : 1);
-            zero_skip = s <= 0;
+            // the bus step u
+            uint16_t ad;
+            bool wr = false;
+            switch (u) {
+                case U_OP: case U_B1: case U_W1: ad = pc; break;
+                case U_W2: ad = (uint16_t)(pc + 1); break;
+                case U_PLO: ad = I.ea; break;
+                case U_PHI: ad = (uint16_t)((I.ea & 0xff00) | ((I.ea + 1) & 0xff)); break;
+                case U_DR: ad = I.ea; break;
+                default: ad = I.ea; wr = true; break;   // U_DW
+            }
+            if (needs_sync(ad, wr) && ppu_calls < 3 * (cur + 1)) { want = 3 * (cur + 1); continue; }
+            uint8_t v = 0;
+            if (wr) write(ad, I.wv);
+            else v = read(ad);
+            if (u == U_OP) {
+                I.op = v;
+                pc++;
+                decode(I);
+            } else {
+                consume(I, u, v);
+            }
+            u = advance(I);
         }
-        advance_to(3 * end);
         // rebase the frame-relative counters on the new frame start
         exec_at -= FRAME_ITERS;
         ppu_calls -= 3 * FRAME_ITERS;
         nmi_thresh -= 3 * FRAME_ITERS;
-        uint32_t lo = iter_lo + FRAME_ITERS;
+        const uint32_t lo = iter_lo + FRAME_ITERS;
         iter_hi += lo < iter_lo;
         iter_lo = lo;
     }
