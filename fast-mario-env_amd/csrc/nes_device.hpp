@@ -21,6 +21,7 @@ constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_
 constexpr int LDS_LANES = 64;                      // lanes sharing one block's per-lane LDS buffers
 constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
+constexpr int SLICE = 341;                          // PPU calls per frame slice (one scanline)
 constexpr int LINE_END = 341;
 constexpr int GRAY_PIX = 256 * 240;
 enum : uint8_t { FN = 0x01, FV = 0x02, FONE = 0x04, FB = 0x08, FD = 0x10, FI = 0x20, FZ = 0x40, FC = 0x80 };
@@ -855,26 +856,49 @@ struct Console {
     }
 
     // One nes-py Emulator::step (nes_core.hpp:1166-1204) with the exact `JMP *` idle fast-forward.
+    //
     // Every lane runs the same loop body: at most one bus access per iteration, through one read
     // and one write site, and one PPU catch-up site (`want`) for the NMI point, PPU-register
-    // accesses, the poll fast-forward and the frame end. Branching per opcode is confined to cheap
+    // accesses, the poll fast-forward and the frame slices. Branching per opcode is confined to
     // register arithmetic, so a wave whose lanes run different instructions stays converged on the
     // memory accesses.
+    //
+    // The frame is cut into slices of one scanline of PPU calls (SLICE). A lane only starts an
+    // instruction j whose catch-up point 3 (j + 1) is at most the slice end; once every lane of
+    // the wave is parked at the boundary, all of them catch their PPU up to it together, so the
+    // per-dot rendering runs with the whole wave active. This is the reference's catch-up PPU cut
+    // at more points (the PPU result does not depend on where it is caught up), and never past a
+    // parked lane's next catch-up point 3 (j + 1), so an NMI raised inside the slice catch-up sees
+    // exactly the CPU state of the reference's catch-up at the start of j.
     __device__ __forceinline__ void frame() {
-        const int32_t end = FRAME_ITERS;
+        const int32_t end = FRAME_ITERS, last_call = 3 * FRAME_ITERS;
         Ins I;
         I.pf = false; I.pb1 = I.pb2 = 0;
         uint8_t u = U_START;
         int32_t want = -1;
+        int32_t slice = SLICE < last_call ? SLICE : last_call;   // end of the current slice, in PPU calls
+        bool parked = false, synced = false;
         for (;;) {
             if (want >= 0) { advance_to(want); want = -1; }
+            if (__all(parked)) {
+                // The whole wave is at the slice boundary: catch up together (next iteration), then
+                // open the next slice. `slice` and `synced` are wave-uniform, so every lane takes
+                // the same path here.
+                if (!synced) {
+                    synced = true;
+                    want = ppu_calls < slice ? slice : -1;
+                    continue;
+                }
+                if (slice >= last_call) break;
+                slice = slice + SLICE < last_call ? slice + SLICE : last_call;
+                parked = synced = false;
+                continue;
+            }
+            if (parked) continue;
             if (u == U_START) {
                 const int32_t j = exec_at;
-                if (j >= end) {
-                    if (ppu_calls < 3 * end) { want = 3 * end; continue; }
-                    break;
-                }
                 const int32_t tgt = 3 * (j + 1);
+                if (j >= end || tgt > slice) { parked = true; continue; }
                 if (tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; continue; }
                 // PRG bytes at pc for the fast paths; the idle check reads 0xff past 0xffff
                 const bool in_prg = pc >= 0x8000;
