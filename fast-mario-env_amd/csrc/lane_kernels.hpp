@@ -51,9 +51,20 @@ __device__ __forceinline__ uint8_t round_sat(float v) {
     return (uint8_t)(iv < 0 ? 0 : iv > 255 ? 255 : iv);
 }
 
-// INTER_AREA output pixel o of one image. g0/g1: pixel p at g[p * stride]; g1 == nullptr: no max-pool.
-__device__ __forceinline__ uint8_t area_pixel(const uint8_t* g0, const uint8_t* g1, uint32_t stride, int o,
-                                              const AreaTables* T) {
+// Frame buffers (GRAY) hold 4 pixels per 32-bit word, lane-interleaved: pixel p of lane e of a
+// buffer with np lanes is byte ((p / 4) * np + e) * 4 + p % 4. An Image addresses one lane's frame
+// in such a buffer, or a plain row-major 256x240 frame when np == 0.
+struct Image {
+    const uint8_t* base;
+    uint32_t np, e;
+    __device__ __forceinline__ uint8_t operator()(uint32_t p) const {
+        return np ? base[((size_t)(p >> 2) * np + e) * 4 + (p & 3)] : base[p];
+    }
+};
+__host__ __device__ __forceinline__ size_t gray_lane_offset(uint32_t e) { return (size_t)e * 4; }
+
+// INTER_AREA output pixel o of one image, max-pooled with a second one if `pool`.
+__device__ __forceinline__ uint8_t area_pixel(const Image& g0, const Image& g1, bool pool, int o, const AreaTables* T) {
     const int dy = o / 84, dx = o - dy * 84;
     const int ny = T->yn[dy], nx = T->xn[dx];
     float acc = 0.f;
@@ -62,8 +73,8 @@ __device__ __forceinline__ uint8_t area_pixel(const uint8_t* g0, const uint8_t* 
         float row = 0.f;
         for (int k = 0; k < nx; k++) {
             const uint32_t p = (uint32_t)(sy * 256 + T->xs[dx * TAPS + k]);
-            uint8_t s = g0[(size_t)p * stride];
-            if (g1) { uint8_t s1 = g1[(size_t)p * stride]; s = s1 > s ? s1 : s; }
+            uint8_t s = g0(p);
+            if (pool) { uint8_t s1 = g1(p); s = s1 > s ? s1 : s; }
             row += (float)s * T->xw[dx * TAPS + k];
         }
         const float term = T->yw[dy * TAPS + j] * row;
@@ -108,7 +119,7 @@ struct BootArgs {
     uint32_t nlp;
     const int* levels;           // 3 * nl
     uint8_t* mem; uint32_t* sc;  // boot consoles [row * nlp + l]
-    uint8_t* gray;               // [pix * nlp + l]
+    uint8_t* gray;               // frame buffer of nlp lanes (4-pixel words)
     int64_t* x0; int64_t* t0;
     uint32_t* err;
 };
@@ -121,7 +132,7 @@ struct CacheArgs {
     const uint8_t* boot_mem; const uint32_t* boot_sc; const int64_t* x0; const int64_t* t0;
     uint8_t* mem; uint32_t* sc;          // cache consoles [row * ncp + c]
     uint8_t* snap_mem; uint32_t* snap_sc;
-    uint8_t* gray;                       // [(slot * GRAY_PIX + pix) * ncp + c]
+    uint8_t* gray;                       // 2 frame buffers of ncp lanes (4-pixel words)
     int64_t* cx; int64_t* ct; int32_t* clives; int32_t* cdraws; uint8_t* cboot;
     uint64_t* cframes; uint64_t* cinstr; uint32_t* cbad;
 };
@@ -134,7 +145,7 @@ struct StepArgs {
     uint8_t* mem; uint32_t* sc;
     uint8_t* snap_mem; uint32_t* snap_sc;
     uint32_t* ev;                 // env words [w * np + e]
-    uint8_t* gray;                // [(slot * GRAY_PIX + pix) * np + e]
+    uint8_t* gray;                // 2 frame buffers of np lanes (4-pixel words)
     const int64_t* actions;
     float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
 };
@@ -194,7 +205,7 @@ __device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e
 __device__ inline void boot_lane(const BootArgs& A, const LaneCtx& x, int l) {
     Console c;
     attach(c, x, A.mem + l, A.nlp);
-    c.gray = A.gray + l; c.render = true;
+    c.gray = A.gray + gray_lane_offset(l); c.render = true;
     c.power_on();
     auto fr = [&](uint8_t b) { c.joy_buttons0 = b; c.frame(); };
     const int w = A.levels[3 * l], s = A.levels[3 * l + 1], ar = A.levels[3 * l + 2];
@@ -234,7 +245,8 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     EnvRegs ev{};
     ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
     ev.prev = 0; ev.lives = -1; ev.shows_boot = true; ev.frames = 0; ev.draws = 0;
-    Stepper stp{c, ev, A.cfg, nullptr, A.gray + ci, A.gray + (size_t)GRAY_PIX * A.ncp + ci, live, snap, false};
+    Stepper stp{c, ev, A.cfg, nullptr, A.gray + gray_lane_offset(ci), A.gray + (size_t)GRAY_PIX * A.ncp + gray_lane_offset(ci),
+                live, snap, false};
     for (int j = 0; j < k; j++) {
         const bool want = j == k - 1;
         if (want) { c.store(A.sc, ci); copy_console(snap, live); }
@@ -265,7 +277,8 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     int64_t a64 = A.actions[e];
     const int act = (a64 >= 0 && a64 < 7) ? (int)a64 : 0;
     Region live{A.mem, A.sc, A.np, e}, snap{A.snap_mem, A.snap_sc, A.np, e};
-    Stepper stp{c, ev, A.cfg, &rng, A.gray + e, A.gray + (size_t)GRAY_PIX * A.np + e, live, snap, true};
+    Stepper stp{c, ev, A.cfg, &rng, A.gray + gray_lane_offset(e), A.gray + (size_t)GRAY_PIX * A.np + gray_lane_offset(e),
+                live, snap, true};
     bool tm;
     double r = stp.agent_step(act, true, &tm);
     ev.t++;
@@ -318,7 +331,7 @@ __device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
 __device__ inline void raw_lane(const RawArgs& A, const LaneCtx& x, uint32_t e) {
     Console c;
     attach(c, x, A.mem + e, A.np);
-    c.gray = A.screen + e;
+    c.gray = A.screen + gray_lane_offset(e);
     if (A.power_on) {
         c.power_on();
     } else {

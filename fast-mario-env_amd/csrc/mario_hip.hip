@@ -78,7 +78,7 @@ __global__ void __launch_bounds__(64) k_reset(ResetArgs A) {
 
 // Observation of a reset-cache entry or a boot state: the boot observation, or the resized last frame.
 struct SmallObsArgs {
-    const uint8_t* gray; uint32_t stride;     // pixel p of entry i at gray[p * stride + i]
+    const uint8_t* gray; uint32_t stride;     // frame buffer of `stride` lanes, entry i in lane i
     const uint8_t* use_boot;                  // per entry (nullable): take boot_obs[level(i)]
     const uint8_t* boot_obs; int nk;          // boot observations [level * OBS_PIX]
     uint8_t* out; int count;                  // [i * OBS_PIX + o]
@@ -90,14 +90,14 @@ __global__ void k_small_obs(SmallObsArgs A) {
     if (i >= A.count || o >= OBS_PIX) return;
     uint8_t v;
     if (A.use_boot && A.use_boot[i]) v = A.boot_obs[(size_t)(i / A.nk) * OBS_PIX + o];
-    else v = area_pixel(A.gray + i, nullptr, A.stride, o, A.T);
+    else v = area_pixel(Image{A.gray, A.stride, (uint32_t)i}, Image{}, false, o, A.T);
     A.out[(size_t)i * OBS_PIX + o] = v;
 }
 
 struct ObsArgs {
     int n; uint32_t np;
     const uint32_t* ev;
-    const uint8_t* gray;          // [(slot * GRAY_PIX + pix) * np + e]
+    const uint8_t* gray;          // 2 frame buffers of np lanes (4-pixel words)
     const uint8_t* boot_obs;      // [level * OBS_PIX + o]
     uint8_t* out;                 // [o * np + e]
     const AreaTables* T;
@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
         v = A.boot_obs[(size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + o];
     } else {
         const bool pool = A.ev[(size_t)E_POOLED * A.np + e] != 0;
-        v = area_pixel(A.gray + e, pool ? A.gray + (size_t)GRAY_PIX * A.np + e : nullptr, A.np, o, A.T);
+        v = area_pixel(Image{A.gray, A.np, e}, Image{A.gray + (size_t)GRAY_PIX * A.np, A.np, e}, pool, o, A.T);
     }
     A.out[(size_t)o * A.np + e] = v;
 }
@@ -184,12 +184,21 @@ __global__ void k_rows_out(const uint8_t* src, uint32_t np, int n, uint32_t rows
     out[(size_t)e * rows + r] = src[(size_t)r * np + e];
 }
 
+// Frame buffer (4-pixel words, lane-interleaved) -> env-major 240x256 frames. Threads: x = env, y = word.
+__global__ void k_frames_out(const uint8_t* src, uint32_t np, int n, uint8_t* out) {
+    const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
+    const uint32_t w = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (e >= (uint32_t)n || w >= GRAY_PIX / 4) return;
+    const uint32_t v = ((const uint32_t*)src)[(size_t)w * np + e];
+    for (int b = 0; b < 4; b++) out[(size_t)e * GRAY_PIX + 4 * w + b] = (uint8_t)(v >> (8 * b));
+}
+
 // 240x256 gray images (env-major) -> 84x84.
 __global__ void k_resize_images(const uint8_t* src, uint8_t* dst, int n, const AreaTables* T) {
     const int i = blockIdx.y;
     const int o = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n || o >= OBS_PIX) return;
-    dst[(size_t)i * OBS_PIX + o] = area_pixel(src + (size_t)i * GRAY_PIX, nullptr, 1, o, T);
+    dst[(size_t)i * OBS_PIX + o] = area_pixel(Image{src + (size_t)i * GRAY_PIX, 0, 0}, Image{}, false, o, T);
 }
 
 // ------------------------------------------------------------------ host side
@@ -577,8 +586,8 @@ int mh_raw_ram(MhRaw* h, uint8_t* d_out, void* stream) {
 }
 int mh_raw_screen(MhRaw* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
-    hipLaunchKernelGGL(k_rows_out, dim3(h->np / 64, GRAY_PIX / 4), dim3(256), 0, (hipStream_t)stream, h->screen, h->np,
-                       h->n, (uint32_t)GRAY_PIX, d_out);
+    hipLaunchKernelGGL(k_frames_out, dim3(h->np / 64, GRAY_PIX / 16), dim3(256), 0, (hipStream_t)stream, h->screen,
+                       h->np, h->n, d_out);
     CK(hipGetLastError());
     return 0;
 }

@@ -21,7 +21,6 @@ constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_
 constexpr int LDS_LANES = 64;                      // lanes sharing one block's per-lane LDS buffers
 constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
-constexpr int SLICE = 341;                          // PPU calls per frame slice (one scanline)
 constexpr int LINE_END = 341;
 constexpr int GRAY_PIX = 256 * 240;
 enum : uint8_t { FN = 0x01, FV = 0x02, FONE = 0x04, FB = 0x08, FD = 0x10, FI = 0x20, FZ = 0x40, FC = 0x80 };
@@ -61,7 +60,7 @@ struct Console {
     uint8_t* mem;            // MEM + e (row stride np)
     uint32_t np;
     Cart cart;
-    uint8_t* gray;           // GRAY slot + e (row stride np), written when render is on
+    uint8_t* gray;           // GRAY slot + 4 e: pixels 4i..4i+3 in the 32-bit word at gray + 4 i np
     const uint8_t* lut;      // palette value -> gray (LDS, 256 entries)
     bool render;
     // ---- CPU
@@ -437,47 +436,72 @@ struct Console {
         sp_line = py;
     }
 
+    // The background tile `rel` tiles after the one v addresses (coarse-x wrap into the neighbouring
+    // name table as in coarse_x_add): pattern planes and palette bits 2-3 (nes_core.hpp:467-483).
+    __device__ __forceinline__ void bg_tile(int rel, uint32_t& lo, uint32_t& hi, uint32_t& at) const {
+        const int tot = (v & 0x1f) + rel;
+        uint16_t vv = (uint16_t)((v & ~0x1f) | (tot & 31));
+        if ((tot >> 5) & 1) vv ^= 0x400;
+        const uint8_t tile = nametable((uint16_t)(0x2000 | (vv & 0x0fff)));
+        const uint16_t pa = (uint16_t)(((tile * 16) + ((vv >> 12) & 7)) | (bg_page << 12));
+        lo = cart.chr[pa];
+        hi = cart.chr[pa + 8];
+        const uint16_t aa = (uint16_t)(0x23c0 | (vv & 0x0c00) | ((vv >> 4) & 0x38) | ((vv >> 2) & 7));
+        const int sh = ((vv >> 4) & 4) | (vv & 2);
+        at = (nametable(aa) >> sh) & 3u;
+    }
+
     // Visible dots [x0, x1) with pixel output: gray values into the frame buffer (nes_core.hpp:467-513).
-    // Background fetches happen once per 8-dot tile; sprites come from the LDS line buffer.
-    __device__ void dots_drawn(int x0, int x1) {
+    // Pixels go in screen-aligned groups of 8, so every lane of a wave runs the same code whatever
+    // its fine scroll: a group spans two background tiles, kept as a 16-bit window per pattern plane
+    // (a PPU's shift registers), and the tile after them is fetched one group ahead. Sprites come
+    // from the LDS line buffer; four gray pixels are stored as one word.
+    __device__ __forceinline__ void dots_drawn(int x0, int x1) {
         const int py = scanline;
         materialize_sprites();
         if (pal_dirty) build_gray_palette();
         const bool spr = show_spr && nsl;
         if (spr && sp_line != py) build_sprite_line(py);
-        int px = x0;
-        while (px < x1) {
-            const int xf = (fine_x + px) & 7;
-            int span = 8 - xf;
-            if (span > x1 - px) span = x1 - px;
-            uint32_t lo = 0, hi = 0, at = 0;
-            if (show_bg) {
-                const uint8_t tile = nametable((uint16_t)(0x2000 | (v & 0x0fff)));
-                const uint16_t pa = (uint16_t)(((tile * 16) + ((v >> 12) & 7)) | (bg_page << 12));
-                lo = cart.chr[pa];
-                hi = cart.chr[pa + 8];
-                const uint16_t aa = (uint16_t)(0x23c0 | (v & 0x0c00) | ((v >> 4) & 0x38) | ((v >> 2) & 7));
-                const int sh = ((v >> 4) & 4) | (v & 2);
-                at = ((nametable(aa) >> sh) & 3u) << 2;
-            }
-            for (int j = 0; j < span; j++, px++) {
-                const int bit = 7 - (xf + j);
-                uint32_t pa = 0, bgop = 0;
-                if (!(hide_edge_bg && px < 8)) {
-                    bgop = ((lo >> bit) & 1u) | (((hi >> bit) & 1u) << 1);
-                    if (bgop) pa = bgop | at;
-                }
-                if (spr && !(hide_edge_spr && px < 8)) {
-                    const uint32_t c = lds_byte(lds_sp, px);
-                    if (c) {
-                        if ((c & 0x40) && bgop && !s0hit && show_bg) s0hit = 1;
-                        if (!bgop || (c & 0x20)) pa = c & 0x1f;
+        const int f = fine_x;
+        const int kb = (f + x0) >> 3;                 // line tile index of pixel x0 (the one v addresses)
+        const int g0 = x0 >> 3, g1 = (x1 + 7) >> 3;
+        uint32_t alo = 0, ahi = 0, aat = 0, blo = 0, bhi = 0, bat = 0;
+        if (show_bg) { bg_tile(g0 - kb, alo, ahi, aat); bg_tile(g0 + 1 - kb, blo, bhi, bat); }
+        uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g0) * np;   // word of pixels xq..xq+3
+        for (int g = g0; g < g1; g++) {
+            uint32_t clo = 0, chi = 0, cat = 0;
+            if (show_bg && g + 1 < g1) bg_tile(g + 2 - kb, clo, chi, cat);
+            // pixel 8g + b is bit 15 - b of the window, after the fine-scroll shift
+            const uint32_t wlo = ((alo << 8) | blo) << f, whi = ((ahi << 8) | bhi) << f;
+            for (int q = 0; q < 2; q++) {
+                const int xq = 8 * g + 4 * q;
+                const uint32_t spw = spr ? lds_sp[(xq >> 2) * LDS_LANES] : 0u;
+                uint32_t word = 0, keep = 0;
+                for (int b = 0; b < 4; b++) {
+                    const int bb = 4 * q + b, px = xq + b;
+                    const bool in = px >= x0 && px < x1;
+                    uint32_t bgop = ((wlo >> (15 - bb)) & 1u) | (((whi >> (15 - bb)) & 1u) << 1);
+                    if (hide_edge_bg && px < 8) bgop = 0;
+                    const uint32_t at = f + bb < 8 ? aat : bat;
+                    uint32_t pa = bgop ? (bgop | (at << 2)) : 0u;
+                    if (spr && !(hide_edge_spr && px < 8)) {
+                        const uint32_t c = (spw >> (8 * b)) & 0xffu;
+                        if (c) {
+                            if ((c & 0x40) && bgop && in && show_bg) s0hit = 1;
+                            if (!bgop || (c & 0x20)) pa = c & 0x1f;
+                        }
                     }
+                    word |= (uint32_t)lds_byte(lds_gp, (int)pa) << (8 * b);
+                    if (!in) keep |= 0xffu << (8 * b);
                 }
-                gray[(size_t)__umul24((uint32_t)(py * 256 + px), np)] = lds_byte(lds_gp, pa);
+                if (!keep) *wp = word;
+                else if (keep != 0xffffffffu) *wp = (*wp & keep) | (word & ~keep);
+                wp += np;
             }
-            if (show_bg && xf + span == 8) coarse_x_add(1);
+            alo = blo; ahi = bhi; aat = bat;
+            blo = clo; bhi = chi; bat = cat;
         }
+        if (show_bg) coarse_x_add(inc_count(x0, x1));
     }
 
     // NMI raised by PPU call `call` (1-based, frame-relative); nes_core.hpp:520-531
@@ -795,6 +819,17 @@ struct Console {
         return U_START;
     }
 
+    // End of the next frame slice: the PPU call after which dots 1..256 of the next render line are
+    // done (this line's if they are still ahead), capped at the frame end `cap`.
+    __device__ __forceinline__ int32_t next_slice(int32_t cap) const {
+        int line = 0;
+        if (pstate == ST_RENDER) line = pcyc < 257 ? scanline : scanline + 1;
+        int32_t d = line <= 239 ? calls_until(line, 257) : calls_until(0, 257);
+        if (d < 1) d = 1;
+        const int32_t s = ppu_calls + d;
+        return s < cap ? s : cap;
+    }
+
     // PPU calls from the current PPU position to (line, dot) on the frame timeline of
     // nmi_threshold() (pre-render line = -1, 262 x 341 calls); the one-dot-shorter odd pre-render
     // line is not modelled, so callers keep a margin. 0 means the very next call processes that dot.
@@ -863,20 +898,21 @@ struct Console {
     // register arithmetic, so a wave whose lanes run different instructions stays converged on the
     // memory accesses.
     //
-    // The frame is cut into slices of one scanline of PPU calls (SLICE). A lane only starts an
-    // instruction j whose catch-up point 3 (j + 1) is at most the slice end; once every lane of
-    // the wave is parked at the boundary, all of them catch their PPU up to it together, so the
-    // per-dot rendering runs with the whole wave active. This is the reference's catch-up PPU cut
-    // at more points (the PPU result does not depend on where it is caught up), and never past a
-    // parked lane's next catch-up point 3 (j + 1), so an NMI raised inside the slice catch-up sees
-    // exactly the CPU state of the reference's catch-up at the start of j.
+    // The frame is cut into slices that end right after the visible dots of a render line (and at
+    // the frame end). A lane only starts an instruction j whose catch-up point 3 (j + 1) is at most
+    // its slice end; once every lane of the wave is parked at its slice end, all of them catch their
+    // PPU up to it together, so each renders one whole line with the whole wave active. This is the
+    // reference's catch-up PPU cut at more points (the PPU result does not depend on where it is
+    // caught up), and never past a parked lane's next catch-up point 3 (j + 1), so an NMI raised
+    // inside the slice catch-up sees exactly the CPU state of the reference's catch-up at the start
+    // of j.
     __device__ __forceinline__ void frame() {
         const int32_t end = FRAME_ITERS, last_call = 3 * FRAME_ITERS;
         Ins I;
         I.pf = false; I.pb1 = I.pb2 = 0;
         uint8_t u = U_START;
         int32_t want = -1;
-        int32_t slice = SLICE < last_call ? SLICE : last_call;   // end of the current slice, in PPU calls
+        int32_t slice = next_slice(last_call);   // end of this lane's current slice, in PPU calls
         bool parked = false, synced = false;
         for (;;) {
             if (want >= 0) { advance_to(want); want = -1; }
@@ -889,9 +925,9 @@ struct Console {
                     want = ppu_calls < slice ? slice : -1;
                     continue;
                 }
-                if (slice >= last_call) break;
-                slice = slice + SLICE < last_call ? slice + SLICE : last_call;
-                parked = synced = false;
+                if (__all(slice >= last_call)) break;
+                if (slice < last_call) { slice = next_slice(last_call); parked = false; }
+                synced = false;
                 continue;
             }
             if (parked) continue;
