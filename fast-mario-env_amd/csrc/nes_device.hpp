@@ -359,8 +359,9 @@ struct Console {
         return (uint8_t)(((vbus_read(ad) >> xs) & 1) | (((vbus_read((uint16_t)(ad + 8)) >> xs) & 1) << 1));
     }
 
-    // visible dots [x0, x1) without pixel output (nes_core.hpp:394-413)
-    __device__ void dots_quiet(int x0, int x1) {
+    // Visible dots [x0, x1): sprite-0 hit and the coarse-x increments of v (nes_core.hpp:394-413).
+    // Rendered and unrendered frames both take the hit from here; dots_drawn only adds pixels.
+    __device__ __forceinline__ void dots_hit_scroll(int x0, int x1) {
         if (!show_bg) return;
         if (!s0hit && show_spr && sprite0_first()) {
             int sx = oam(3);
@@ -451,11 +452,12 @@ struct Console {
         at = (nametable(aa) >> sh) & 3u;
     }
 
-    // Visible dots [x0, x1) with pixel output: gray values into the frame buffer (nes_core.hpp:467-513).
-    // Pixels go in screen-aligned groups of 8, so every lane of a wave runs the same code whatever
-    // its fine scroll: a group spans two background tiles, kept as a 16-bit window per pattern plane
-    // (a PPU's shift registers), and the tile after them is fetched one group ahead. Sprites come
-    // from the LDS line buffer; four gray pixels are stored as one word.
+    // Pixels of visible dots [x0, x1): gray values into the frame buffer (nes_core.hpp:467-513), with
+    // v as it is at x0 (dots_hit_scroll advances it afterwards). Pixels go in screen-aligned groups
+    // of 8, so every lane of a wave runs the same code whatever its fine scroll: a group spans two
+    // background tiles, kept as a 16-bit window per pattern plane (a PPU's shift registers), and the
+    // tile after them is fetched one group ahead. Sprites come from the LDS line buffer, where the
+    // first opaque listed sprite of each x sits; four gray pixels are stored as one word.
     __device__ __forceinline__ void dots_drawn(int x0, int x1) {
         const int py = scanline;
         materialize_sprites();
@@ -486,10 +488,7 @@ struct Console {
                     uint32_t pa = bgop ? (bgop | (at << 2)) : 0u;
                     if (spr && !(hide_edge_spr && px < 8)) {
                         const uint32_t c = (spw >> (8 * b)) & 0xffu;
-                        if (c) {
-                            if ((c & 0x40) && bgop && in && show_bg) s0hit = 1;
-                            if (!bgop || (c & 0x20)) pa = c & 0x1f;
-                        }
+                        if (c && (!bgop || (c & 0x20))) pa = c & 0x1f;
                     }
                     word |= (uint32_t)lds_byte(lds_gp, (int)pa) << (8 * b);
                     if (!in) keep |= 0xffu << (8 * b);
@@ -501,7 +500,6 @@ struct Console {
             alo = blo; ahi = bhi; aat = bat;
             blo = clo; bhi = chi; bat = cat;
         }
-        if (show_bg) coarse_x_add(inc_count(x0, x1));
     }
 
     // NMI raised by PPU call `call` (1-based, frame-relative); nes_core.hpp:520-531
@@ -536,7 +534,7 @@ struct Console {
                 if (c >= 1 && c <= 256) {
                     int k = n < 257 - c ? n : 257 - c;
                     if (render) dots_drawn(c - 1, c - 1 + k);
-                    else dots_quiet(c - 1, c - 1 + k);
+                    dots_hit_scroll(c - 1, c - 1 + k);
                     pcyc += k; ppu_calls += k; n -= k;
                 } else if (c == 257) {
                     if (show_bg) fine_y_step();
