@@ -1,5 +1,5 @@
 #!/usr/bin/env python
-"""Headline benchmark: batched Super Mario Bros agent steps on one MI355X.
+"""Headline benchmark: batched Super Mario Bros agent steps on one MI355X (the full wrapper stack at 32768 envs).
 
     python bench.py [--steps K] [--warmup W] [--envs N] [--gpus 1]
 
@@ -32,7 +32,7 @@ for _p in (os.path.join(ROOT, "fast-mario-env_amd"), os.path.join(ROOT, "tests")
 
 METRIC = "agent env-steps/sec (skip=4) at 32768 envs on 1 MI355X; % HBM/VALU roofline"
 HBM_PEAK_GBS = 8000.0
-# bytes the kernels must move per env and agent step: console state read + write,
+# bytes k_step must move per env and agent step: console state read + write,
 # env words read + write, action, reward / term / trunc / info out; ep stats on episode end.
 STATE_BYTES = 4384 + 4 * 41
 ENV_WORD_BYTES = 4 * 30
@@ -75,7 +75,7 @@ def traffic_from_profiles(workload_key):
 
 
 def cpu_baseline(rom, seconds):
-    """The reference C++ thread pool (oracle/_ref) on the host cores, config-3 settings, bounded sample."""
+    """The reference C++ thread pool (oracle/_ref) on the host cores, headline settings, bounded sample."""
     import numpy as np
 
     from cpu_libs import OracleVec, RefVec, have_ref
@@ -109,16 +109,19 @@ def cpu_baseline(rom, seconds):
     except (OSError, StopIteration):
         pass
     return {"value": round(n * steps / dt, 1), "unit": "agent-steps/s", "cores": threads, "kind": kind,
-            "sample": f"{n} envs x {steps} timed steps after 3 warm-up steps ({dt:.1f} s), level 1-1, config-3 "
+            "sample": f"{n} envs x {steps} timed steps after 3 warm-up steps ({dt:.1f} s), level 1-1, headline "
                       f"wrapper settings; {model}; load1 {load1}"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--envs", type=int, default=32768)
+    ap.add_argument("--probe-copy-mib", type=int, default=0,
+                    help="before the steps, copy a buffer of this many MiB once (a kernel of known traffic "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -146,6 +149,13 @@ def main():
     gen.manual_seed(0)
     acts = torch.randint(0, 7, (args.warmup + args.steps, n), generator=gen, device="cuda:0", dtype=torch.int64)
     done_count = torch.zeros((), dtype=torch.int64, device="cuda:0")
+    if args.probe_copy_mib:
+        src = torch.ones(args.probe_copy_mib << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.probe_copy_mib} MiB device-to-device")
+        del src, dst
     for i in range(args.warmup):
         env.step(acts[i])
     torch.cuda.synchronize()
@@ -154,10 +164,12 @@ def main():
     env.timing(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    # progress lines need a device sync, which idles the GPU between steps: long runs only
+    every = args.steps // 4 if args.steps >= 400 else 0
     for i in range(args.steps):
         _, _, term, trunc, _ = env.step(acts[args.warmup + i])
         done_count += (term | trunc).sum()
-        if (i + 1) % max(1, args.steps // 4) == 0:
+        if every and (i + 1) % every == 0:
             torch.cuda.synchronize()
             log(f"step {i + 1}/{args.steps}")
     torch.cuda.synchronize()
@@ -170,7 +182,7 @@ def main():
     p_done = float(done_count.item()) / (n * args.steps)
     value = n * args.steps / dt
     k_step_ms = stages["k_step"] / max(1, timed)
-    workload = f"config3/{n}envs/1-1/rom:{rom_sha}"
+    workload = f"headline/{n}envs/1-1/rom:{rom_sha}"
     k_bytes = n * (K_STEP_BYTES + K_STEP_DONE_BYTES * p_done)
     achieved = k_bytes / (k_step_ms * 1e-3) / 1e9
     traffic = traffic_from_profiles(workload)
@@ -187,7 +199,7 @@ def main():
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic",
-        "config": {"workload": "BASELINE config 3 (headline): full wrapper stack", "envs": n, "level": "1-1",
+        "config": {"workload": "headline: full wrapper stack, 32768 envs of 1-1", "envs": n, "level": "1-1",
                    "rom": rom_name, "rom_sha1": rom_sha, "sticky": 0.25, "noop_max": 30, "skip": 4, "maxpool": True,
                    "frame_stack": 4, "max_steps": 2000, "seed": 0, "actions": "uniform {0..6}, torch.Generator seed 0"},
         "roofline": {"bound": "hbm", "kernel": "k_step", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,

@@ -112,7 +112,7 @@ def run_env(venv, actions):
 
 
 def config1_actions(steps=1000, n=32):
-    """actions uniform in {0..6} from default_rng(0), shape (32,), one draw per step."""
+    """Golden-trace workload: actions uniform in {0..6} from default_rng(0), shape (32,), one draw per step."""
     rng = np.random.default_rng(0)
     return [rng.integers(0, 7, n) for _ in range(steps)]
 
@@ -166,7 +166,7 @@ def main():
         assert np.array_equal(dst, dst2)
         res.append(digest(dst))
     out["meta"]["resize_seed0_40"] = res
-    # BASELINE config 1 on the synthetic ROM: 32 envs of 1-1, 1000 steps
+    # the golden-trace workload on the synthetic ROM: 32 envs of 1-1, 1000 steps
     n = 32
     ref = RefVec(mini, [decode_level("1-1")] * n, n, seed=0, frame_stack=4, skip=4, sticky=0.0, noop_max=0,
                  maxpool=False, max_steps=2000)

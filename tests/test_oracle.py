@@ -73,7 +73,7 @@ def test_rom_mode_golden(mode):
 
 
 def test_config1_golden():
-    """BASELINE config 1 (32 envs of 1-1, seed 0, no sticky / no-op / max-pool) on the synthetic ROM;
+    """The CPU golden-trace workload (32 envs of 1-1, seed 0, no sticky / no-op / max-pool) on the synthetic ROM;
     the first 250 steps by default, all 1000 with FME_TEST_SCALE >= 4."""
     g = GOLD["config1"]
     steps = min(1000, scaled(250))
