@@ -9,7 +9,7 @@ actions uniform in {0..6}, pre-generated on the device from torch.Generator seed
 real one when the reference's lookup finds it, else this repository's synthetic NROM stand-in
 (tests/golden/roms/mini_smb_vanilla.nes); the JSON line names which.
 
-One step = mh_step_async (snapshot copy, k_step, k_obs, k_reset, k_stack) on torch's current stream;
+One step = mh_step_async (k_step, k_obs, k_reset, k_stack) on torch's current stream;
 inputs are resident in HBM. K steps are timed between two device synchronizations after W warm-up
 steps. Stage times come from HIP events recorded on the same stream. The reference C++ FastVecEnv
 (oracle/_ref, the checker build of the reference) is timed on the host cores on a bounded sample of

@@ -115,7 +115,7 @@ struct Cfg {
     double sticky;
 };
 
-// Memory region of consoles with the same layout as the live state (used for snapshots / caches).
+// Memory region of consoles with the same layout as the live state (reset cache, boot states).
 struct Region {
     uint8_t* mem;       // row-major [row * np + idx]
     uint32_t* sc;       // [word * np + idx]
@@ -134,7 +134,7 @@ struct EnvRegs {
     int64_t x_last, time_last;
     int prev, lives, t, ep_len;
     double ep_ret;
-    bool shows_boot, pooled;
+    bool shows_boot, pooled, slot_swap;   // slot_swap: the last frame is in frame buffer 1
     uint64_t frames;
     uint32_t draws;     // sticky draws taken (counted by the reset-cache builder)
     Info info;
@@ -145,10 +145,8 @@ struct Stepper {
     EnvRegs& ev;
     const Cfg& cfg;
     Pcg* rng;             // null: draws are counted, not taken (reset cache: action 0 == prev 0)
-    uint8_t* gray0;       // frame K-1 (and every early-termination final frame)
-    uint8_t* gray1;       // frame K-2 (max-pool partner)
-    Region live, snap;    // the console's own region and its step-start snapshot
-    bool snapped;
+    uint8_t* gray0;       // frame buffer of frames K-1, K-3, ... of the agent step
+    uint8_t* gray1;       // frame buffer of frames K-2, K-4, ...
 
     __device__ __forceinline__ bool busy() { return smb_busy(c) || smb_world_over(c); }
     // _skip_change_area before the _skip_occupied_states loop (fastmario.cpp:297-300)
@@ -176,98 +174,76 @@ struct Stepper {
 
     // Sticky actions + frame skip + max-pool + early termination + life loss (fastmario.cpp:336-374),
     // with the hack frames of _skip_change_area / _skip_occupied_states (fastmario.cpp:297-308) after
-    // every agent frame that did not end the episode. On early termination the frames that were not
-    // rendered are re-emulated from the step-start snapshot, as the reference re-emulates them from its
-    // per-frame snapshots (fastmario.cpp:354-365). Written as a state machine around ONE console frame
-    // so that the emulator is inlined once.
+    // every agent frame that did not end the episode.
+    //
+    // When an observation is wanted, every agent frame (with its hack frames) is rendered, alternately
+    // into gray1 and gray0 so that frame K-1 lands in gray0 and K-2 in gray1. The reference renders only
+    // those two and, when the episode ends at an earlier frame `last`, restores its per-frame snapshots
+    // and re-emulates frame last-1 (with its hack frames, for the max-pool partner) and frame last with
+    // pixels on. Emulation is deterministic, so those re-emulated frames are exactly the frames already
+    // rendered here: the observation is taken from the two buffers (ev.slot_swap says which one holds
+    // `last`), and the counters add what the re-emulation would count. Written as a state machine
+    // around ONE console frame so that the emulator is inlined once.
     __device__ __forceinline__ double agent_step(int act0, bool want_obs, bool* term) {
-        enum : uint8_t { PH_MAIN, PH_BUSY, PH_REPLAY, PH_RBUSY, PH_FINAL };
         const int K = cfg.skip;
         const bool mp = cfg.maxpool != 0;
-        uint64_t acts = 0;
         double total = 0.0;
-        bool done = false;
-        int i = 0, last = 0, j = 0, guard = 0;
-        uint8_t ph = PH_MAIN;
-        bool hack_render = false, rj = false;
-        uint8_t* hack_slot = gray1;
-        uint64_t f0 = 0;
-        uint32_t i0 = 0, b0 = 0;
+        bool done = false, hack = false;
+        int i = 0, guard = 0;
+        bool render = false;
+        uint8_t* slot = gray0;
+        // frames, bad ops and instructions of agent frames i (cur_*) and i - 1 (prev_*), hack frames included
+        uint32_t cur_f = 0, cur_b = 0, cur_n = 0, prev_f = 0, prev_b = 0, prev_n = 0, b0 = 0, n0 = 0;
         for (;;) {
-            // ---- the frame to emulate
             uint8_t buttons = 0;
-            bool render = false;
-            uint8_t* slot = gray1;
-            if (ph == PH_MAIN) {
+            if (!hack) {
                 int act = act0;
                 if (cfg.sticky != 0.0) {
                     if (rng) { if (rng->random() < cfg.sticky) act = ev.prev; }
                     else ev.draws++;
                 }
                 ev.prev = act;
-                acts |= (uint64_t)act << (3 * i);
-                const bool last_frame = i == K - 1, pool_frame = mp && i == K - 2;
-                render = want_obs && (last_frame || pool_frame);
-                slot = last_frame ? gray0 : gray1;
+                render = want_obs;
+                slot = ((K - 1 - i) & 1) ? gray1 : gray0;
                 buttons = kButtons[act];
-            } else if (ph == PH_BUSY || ph == PH_RBUSY) {
-                c.st(ROW_RAM + 0x7a0, 0);
-                render = hack_render;
-                slot = hack_slot;
-            } else if (ph == PH_REPLAY) {
-                rj = mp && j == last - 1;
-                f0 = ev.frames; i0 = c.instructions; b0 = c.bad_ops;
-                buttons = kButtons[(acts >> (3 * j)) & 7];
-                render = rj;
+                cur_f = 0; b0 = c.bad_ops; n0 = c.instructions;
             } else {
-                buttons = kButtons[(acts >> (3 * last)) & 7];
-                render = true;
-                slot = gray0;
+                c.st(ROW_RAM + 0x7a0, 0);
             }
             c.joy_buttons0 = buttons;
             c.render = render;
             c.gray = slot;
             c.frame();
             ev.frames++;
+            cur_f++;
             if (render) ev.shows_boot = false;
-            // ---- what follows it
-            if (ph == PH_FINAL) break;
-            bool hack = false;   // another hack frame follows
-            if (ph == PH_MAIN) {
+            if (!hack) {
                 total += frame_reward(&done);
-                if (!done) { fix_change_area(); guard = 0; hack = true; }
-                hack_render = render; hack_slot = slot;
-            } else if (ph == PH_REPLAY) {
-                fix_change_area(); guard = 0; hack = true;
-                hack_render = rj; hack_slot = gray1;
-            } else {
-                hack = true;
+                if (!done) { fix_change_area(); guard = 0; }
             }
-            if (hack && busy()) {
-                if (++guard <= HACK_FRAME_LIMIT) { ph = ph == PH_MAIN || ph == PH_BUSY ? PH_BUSY : PH_RBUSY; continue; }
+            if (!done && busy()) {
+                if (++guard <= HACK_FRAME_LIMIT) { hack = true; continue; }
                 c.bad_ops |= ERR_HACK_LIMIT;
             }
-            if (ph == PH_MAIN || ph == PH_BUSY) {
-                // the agent frame i (and its hack frames) is complete
-                if (!done && i < K - 1) { i++; ph = PH_MAIN; continue; }
-                last = done ? i : K - 1;
-                if (!(want_obs && done && last < K - 1)) break;
-                copy_console(live, snap);
-                c.load(snap.sc, snap.idx);
-                j = 0;
-                ph = last > 0 ? PH_REPLAY : PH_FINAL;
-            } else {
-                // replayed frame j complete: count only the frames the reference re-emulates
-                if (!rj) {
-                    ev.frames = f0;
-                    c.instructions = i0;
-                    c.bad_ops = b0 | (c.bad_ops & ERR_HACK_LIMIT);
-                }
-                j++;
-                ph = j < last ? PH_REPLAY : PH_FINAL;
+            hack = false;
+            // agent frame i (and its hack frames) is complete
+            cur_b = c.bad_ops - b0; cur_n = c.instructions - n0;
+            if (done || i == K - 1) break;
+            prev_f = cur_f; prev_b = cur_b; prev_n = cur_n;
+            i++;
+        }
+        const int last = i;
+        if (want_obs) {
+            ev.pooled = mp && last >= 1;
+            ev.slot_swap = ((K - 1 - last) & 1) != 0;
+            if (done && last < K - 1) {
+                // the reference's re-emulation: frame last - 1 with its hack frames (max-pool), frame last
+                const bool two = mp && last >= 1;
+                ev.frames += 1 + (two ? prev_f : 0);
+                c.bad_ops += (cur_b & ~ERR_HACK_LIMIT) + (two ? (prev_b & ~ERR_HACK_LIMIT) : 0);
+                c.instructions += cur_n + (two ? prev_n : 0);
             }
         }
-        if (want_obs) ev.pooled = mp && last >= 1;
         bool tm = done;
         int life = (int)ev.info.v[2];
         if (ev.lives >= 0 && life < ev.lives) tm = true;

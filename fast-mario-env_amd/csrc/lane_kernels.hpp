@@ -131,7 +131,6 @@ struct CacheArgs {
     uint32_t nlp, ncp;
     const uint8_t* boot_mem; const uint32_t* boot_sc; const int64_t* x0; const int64_t* t0;
     uint8_t* mem; uint32_t* sc;          // cache consoles [row * ncp + c]
-    uint8_t* snap_mem; uint32_t* snap_sc;
     uint8_t* gray;                       // 2 frame buffers of ncp lanes (4-pixel words)
     int64_t* cx; int64_t* ct; int32_t* clives; int32_t* cdraws; uint8_t* cboot;
     uint64_t* cframes; uint64_t* cinstr; uint32_t* cbad;
@@ -143,7 +142,6 @@ struct StepArgs {
     int n;
     uint32_t np;
     uint8_t* mem; uint32_t* sc;
-    uint8_t* snap_mem; uint32_t* snap_sc;
     uint32_t* ev;                 // env words [w * np + e]
     uint8_t* gray;                // 2 frame buffers of np lanes (4-pixel words)
     const int64_t* actions;
@@ -180,7 +178,7 @@ __device__ __forceinline__ void load_env(EnvRegs& ev, const uint32_t* E, uint32_
     ev.prev = (int)w(E_PREV); ev.lives = (int)w(E_LIVES); ev.t = (int)w(E_T); ev.ep_len = (int)w(E_EP_LEN);
     uint64_t r = (uint64_t)w(E_EPRET_LO) | ((uint64_t)w(E_EPRET_HI) << 32);
     ev.ep_ret = __longlong_as_double((long long)r);
-    ev.shows_boot = w(E_SHOWS_BOOT) != 0; ev.pooled = w(E_POOLED) != 0;
+    ev.shows_boot = w(E_SHOWS_BOOT) != 0; ev.pooled = (w(E_POOLED) & 1) != 0; ev.slot_swap = (w(E_POOLED) & 2) != 0;
     ev.frames = 0; ev.draws = 0;
 }
 __device__ __forceinline__ void store_env(const EnvRegs& ev, uint32_t* E, uint32_t np, uint32_t e) {
@@ -191,7 +189,7 @@ __device__ __forceinline__ void store_env(const EnvRegs& ev, uint32_t* E, uint32
     w(E_EP_LEN, (uint32_t)ev.ep_len);
     uint64_t r = (uint64_t)__double_as_longlong(ev.ep_ret);
     w(E_EPRET_LO, (uint32_t)r); w(E_EPRET_HI, (uint32_t)(r >> 32));
-    w(E_SHOWS_BOOT, ev.shows_boot); w(E_POOLED, ev.pooled);
+    w(E_SHOWS_BOOT, ev.shows_boot); w(E_POOLED, (ev.pooled ? 1u : 0u) | (ev.slot_swap ? 2u : 0u));
 }
 __device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e, int lo_word, uint64_t add) {
     uint64_t v = (uint64_t)E[(size_t)lo_word * np + e] | ((uint64_t)E[(size_t)(lo_word + 1) * np + e] << 32);
@@ -237,7 +235,6 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     const int lvl = ci / A.nk, k = ci - lvl * A.nk;
     Region boot{(uint8_t*)A.boot_mem, (uint32_t*)A.boot_sc, A.nlp, (uint32_t)lvl};
     Region live{A.mem, A.sc, A.ncp, (uint32_t)ci};
-    Region snap{A.snap_mem, A.snap_sc, A.ncp, (uint32_t)ci};
     copy_console(live, boot);
     Console c;
     attach(c, x, A.mem + ci, A.ncp);
@@ -245,13 +242,10 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     EnvRegs ev{};
     ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
     ev.prev = 0; ev.lives = -1; ev.shows_boot = true; ev.frames = 0; ev.draws = 0;
-    Stepper stp{c, ev, A.cfg, nullptr, A.gray + gray_lane_offset(ci), A.gray + (size_t)GRAY_PIX * A.ncp + gray_lane_offset(ci),
-                live, snap, false};
+    Stepper stp{c, ev, A.cfg, nullptr, A.gray + gray_lane_offset(ci), A.gray + (size_t)GRAY_PIX * A.ncp + gray_lane_offset(ci)};
     for (int j = 0; j < k; j++) {
-        const bool want = j == k - 1;
-        if (want) { c.store(A.sc, ci); copy_console(snap, live); }
         bool term;
-        stp.agent_step(0, want, &term);
+        stp.agent_step(0, j == k - 1, &term);
         if (term) {
             copy_console(live, boot);
             c.load(A.sc, ci);
@@ -276,9 +270,7 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     rng.load(A.ev, A.np, e);
     int64_t a64 = A.actions[e];
     const int act = (a64 >= 0 && a64 < 7) ? (int)a64 : 0;
-    Region live{A.mem, A.sc, A.np, e}, snap{A.snap_mem, A.snap_sc, A.np, e};
-    Stepper stp{c, ev, A.cfg, &rng, A.gray + gray_lane_offset(e), A.gray + (size_t)GRAY_PIX * A.np + gray_lane_offset(e),
-                live, snap, true};
+    Stepper stp{c, ev, A.cfg, &rng, A.gray + gray_lane_offset(e), A.gray + (size_t)GRAY_PIX * A.np + gray_lane_offset(e)};
     bool tm;
     double r = stp.agent_step(act, true, &tm);
     ev.t++;
@@ -318,7 +310,7 @@ __device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
     copy_console(dst, src);
     EnvRegs ev{};
     ev.x_last = A.cx[ci]; ev.time_last = A.ct[ci]; ev.lives = A.clives[ci]; ev.prev = 0;
-    ev.t = 0; ev.ep_len = 0; ev.ep_ret = 0.0; ev.shows_boot = A.cboot[ci] != 0; ev.pooled = false;
+    ev.t = 0; ev.ep_len = 0; ev.ep_ret = 0.0; ev.shows_boot = A.cboot[ci] != 0; ev.pooled = false; ev.slot_swap = false;
     store_env(ev, E, A.np, e);
     E[E_RESET_IDX * np + e] = (uint32_t)ci;
     // the no-op steps count as emulated work, as on the reference CPU path

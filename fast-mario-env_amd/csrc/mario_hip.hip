@@ -1,9 +1,8 @@
 // mario_hip: batched Super Mario Bros env stepping on gfx950 — kernels and the C-ABI (include/mario_hip.h).
 //
-// One agent step of N envs is five stages on the caller's stream:
-//   hipMemcpyAsync  MEM/SC -> SNAP         step-start snapshot (early termination re-renders from it)
+// One agent step of N envs is four kernels on the caller's stream:
 //   k_step          one lane per env: sticky draw, K frames of 6502 + catch-up PPU, reward/done/info,
-//                   hack frames, gray rendering of the observed frame(s) into GRAY (lane-interleaved)
+//                   hack frames, gray rendering of every frame into two alternating frame buffers
 //   k_obs           one thread per (env, output pixel): 2-frame max + INTER_AREA 256x240 -> 84x84
 //   k_reset         one lane per env: finished envs take a cached (level, no-op count) start state
 //   k_stack         LDS-transposed frame-stack shift, final_obs, reset observation
@@ -103,7 +102,9 @@ struct ObsArgs {
     const AreaTables* T;
 };
 // New observation of every env: the boot observation right after a reset, else INTER_AREA of the last
-// frame, max-pooled with its partner frame (fastmario.cpp:377-386). Threads: x = env, y = pixel.
+// frame, max-pooled with its partner frame (fastmario.cpp:377-386). E_POOLED bit 0: pool; bit 1: the
+// last frame is in frame buffer 1 (the episode ended at an agent frame of the other parity than K-1).
+// Threads: x = env, y = pixel.
 __global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
     const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
     const int o = blockIdx.y * 4 + (threadIdx.x >> 6);
@@ -112,8 +113,11 @@ __global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
     if (A.ev[(size_t)E_SHOWS_BOOT * A.np + e]) {
         v = A.boot_obs[(size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + o];
     } else {
-        const bool pool = A.ev[(size_t)E_POOLED * A.np + e] != 0;
-        v = area_pixel(Image{A.gray, A.np, e}, Image{A.gray + (size_t)GRAY_PIX * A.np, A.np, e}, pool, o, A.T);
+        const uint32_t pw = A.ev[(size_t)E_POOLED * A.np + e];
+        const uint8_t* g0 = A.gray;
+        const uint8_t* g1 = A.gray + (size_t)GRAY_PIX * A.np;
+        if (pw & 2) { const uint8_t* t = g0; g0 = g1; g1 = t; }
+        v = area_pixel(Image{g0, A.np, e}, Image{g1, A.np, e}, (pw & 1) != 0, o, A.T);
     }
     A.out[(size_t)o * A.np + e] = v;
 }
@@ -254,13 +258,13 @@ struct MhEnv {
     DevBufs B;
     RomArgs R{};
     AreaTables* T = nullptr;
-    uint8_t *mem = nullptr, *snap_mem = nullptr, *gray = nullptr, *fresh = nullptr;
-    uint32_t *sc = nullptr, *snap_sc = nullptr, *ev = nullptr;
+    uint8_t *mem = nullptr, *gray = nullptr, *fresh = nullptr;
+    uint32_t *sc = nullptr, *ev = nullptr;
     uint8_t *boot_mem = nullptr, *boot_gray = nullptr, *boot_obs = nullptr;
     uint32_t* boot_sc = nullptr;
     int64_t *x0 = nullptr, *t0 = nullptr;
-    uint8_t *cmem = nullptr, *csnap_mem = nullptr, *cgray = nullptr, *cobs = nullptr, *cboot = nullptr;
-    uint32_t *csc = nullptr, *csnap_sc = nullptr;
+    uint8_t *cmem = nullptr, *cgray = nullptr, *cobs = nullptr, *cboot = nullptr;
+    uint32_t *csc = nullptr;
     int64_t *cx = nullptr, *ct = nullptr;
     int32_t *clives = nullptr, *cdraws = nullptr;
     uint64_t *cframes = nullptr, *cinstr = nullptr;
@@ -330,9 +334,7 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
     h->T = B.alloc<AreaTables>(1, good);
     int* d_levels = B.alloc<int>(lv.size(), good);
     h->mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
-    h->snap_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
     h->sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
-    h->snap_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
     h->ev = B.alloc<uint32_t>((size_t)E_COUNT * h->np, good);
     h->gray = B.alloc<uint8_t>((size_t)2 * GRAY_PIX * h->np, good);
     h->fresh = B.alloc<uint8_t>((size_t)OBS_PIX * h->np, good);
@@ -343,8 +345,6 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
     h->x0 = B.alloc<int64_t>(h->nl, good); h->t0 = B.alloc<int64_t>(h->nl, good);
     h->cmem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->ncp, good);
     h->csc = B.alloc<uint32_t>((size_t)S_COUNT * h->ncp, good);
-    h->csnap_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->ncp, good);
-    h->csnap_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->ncp, good);
     h->cgray = B.alloc<uint8_t>((size_t)2 * GRAY_PIX * h->ncp, good);
     h->cobs = B.alloc<uint8_t>((size_t)OBS_PIX * h->nc, good);
     h->cboot = B.alloc<uint8_t>(h->nc, good);
@@ -385,7 +385,7 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
     SmallObsArgs so{h->boot_gray, h->nlp, nullptr, nullptr, 1, h->boot_obs, h->nl, h->T};
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nl), dim3(256), 0, 0, so);
     CacheArgs ca{h->R, h->cfg, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
-                 h->cmem, h->csc, h->csnap_mem, h->csnap_sc, h->cgray, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
+                 h->cmem, h->csc, h->cgray, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
                  h->cframes, h->cinstr, h->cbad};
     hipLaunchKernelGGL(k_cache, dim3((h->nc + 63) / 64), dim3(64), 0, 0, ca);
     if (!ok(hipGetLastError(), "k_cache launch")) return fail();
@@ -435,24 +435,21 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     CK(hipSetDevice(h->device));
     hipStream_t s = (hipStream_t)stream;
     if (mark(h, s, 0)) return -1;
-    CK(hipMemcpyAsync(h->snap_mem, h->mem, (size_t)MEM_ROWS * h->np, hipMemcpyDeviceToDevice, s));
-    CK(hipMemcpyAsync(h->snap_sc, h->sc, (size_t)S_COUNT * h->np * 4, hipMemcpyDeviceToDevice, s));
-    if (mark(h, s, 1)) return -1;
-    StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->snap_mem, h->snap_sc, h->ev, h->gray, d_actions,
+    StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->ev, h->gray, d_actions,
                 h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len};
     hipLaunchKernelGGL(k_step, dim3(h->np / 64), dim3(64), 0, s, sa);
     CK(hipGetLastError());
-    if (mark(h, s, 2)) return -1;
+    if (mark(h, s, 1)) return -1;
     ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
     hipLaunchKernelGGL(k_obs, dim3(h->np / 64, OBS_PIX / 4), dim3(256), 0, s, oa);
     CK(hipGetLastError());
-    if (mark(h, s, 3)) return -1;
+    if (mark(h, s, 2)) return -1;
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(0));
     CK(hipGetLastError());
-    if (mark(h, s, 4)) return -1;
+    if (mark(h, s, 3)) return -1;
     hipLaunchKernelGGL(k_stack, dim3((OBS_PIX / 4 + 63) / 64, h->np / 64), dim3(256), 0, s, h->stack_args(0));
     CK(hipGetLastError());
-    if (mark(h, s, 5)) return -1;
+    if (mark(h, s, 4)) return -1;
     if (h->timing) h->timed_steps++;
     return 0;
 }
@@ -533,7 +530,7 @@ int mh_num_levels(MhEnv* h) { return h ? h->nl : -1; }
 int64_t mh_state_bytes(void) { return (int64_t)MEM_ROWS + 4LL * S_COUNT; }
 int64_t mh_env_bytes(MhEnv* h) {
     if (!h) return -1;
-    int64_t per = 2 * (MEM_ROWS + 4LL * S_COUNT) + 4LL * E_COUNT + 2LL * GRAY_PIX + OBS_PIX;
+    int64_t per = MEM_ROWS + 4LL * S_COUNT + 4LL * E_COUNT + 2LL * GRAY_PIX + OBS_PIX;
     return per * h->np / h->n;
 }
 

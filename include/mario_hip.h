@@ -9,7 +9,7 @@
  * Conventions
  *   - Plain C types only. `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *   - Output buffers are device pointers owned by the caller (e.g. torch tensors); the library
- *     writes them in place. Internal state (consoles, snapshots, reset cache) is owned by the library.
+ *     writes them in place. Internal state (consoles, frame buffers, reset cache) is owned by the library.
  *   - Functions returning int return 0 on success and -1 on failure; creators return NULL on
  *     failure. mh_last_error() then returns a message (thread-local, valid until the next call).
  *   - One host thread drives one handle. Calls on one stream are ordered; no call blocks except
@@ -66,11 +66,11 @@ int mh_step_wait(MhEnv* h, void* stream);
 void mh_destroy(MhEnv* h);
 
 /* Per-stage timing of mh_step_async with HIP events recorded on the step's own stream (no counterpart
- * in the reference; used by the benchmark). Stages: 0 step-start snapshot copy, 1 k_step (emulation +
- * render), 2 k_obs (max-pool + INTER_AREA), 3 k_reset, 4 k_stack. mh_timing(h, 1) clears and starts
+ * in the reference; used by the benchmark). Stages: 0 k_step (emulation + render), 1 k_obs (max-pool +
+ * INTER_AREA), 2 k_reset, 3 k_stack. mh_timing(h, 1) clears and starts
  * recording; mh_timing_read synchronizes and returns the summed milliseconds per stage and the number
  * of timed steps. */
-#define MH_STAGES 5
+#define MH_STAGES 4
 int mh_timing(MhEnv* h, int enable);
 int mh_timing_read(MhEnv* h, double* ms, int64_t* steps);
 
