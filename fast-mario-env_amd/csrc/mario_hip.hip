@@ -35,7 +35,7 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
     __shared__ uint8_t s_lut[256];                                  \
     __shared__ uint8_t s_cyc[256];                                  \
     __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
-    __shared__ uint32_t s_gp[LDS_GP_WORDS * LDS_LANES];
+    __shared__ uint32_t s_gp[(LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES];
 
 __device__ __forceinline__ LaneCtx lane_ctx(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_lut,
                                             const uint8_t* s_cyc, uint32_t* s_sp, uint32_t* s_gp) {

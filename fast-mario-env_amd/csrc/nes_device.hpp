@@ -20,6 +20,8 @@ namespace mh {
 constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
 constexpr int LDS_LANES = 64;                      // lanes sharing one block's per-lane LDS buffers
 constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
+constexpr int LDS_BG_WORDS = 18;                   // words per lane: background tile row (33 tiles + 33 attributes)
+constexpr int LDS_BG_ATTR = 36;                    // byte offset of the attributes in the tile row
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
 constexpr int LINE_END = 341;
 constexpr int GRAY_PIX = 256 * 240;
@@ -88,6 +90,8 @@ struct Console {
     bool pal_dirty;          // the LDS gray palette must be rebuilt
     uint32_t* lds_sp;        // per-lane sprite line buffer: word (x / 4) of this lane at lds_sp[(x / 4) * LDS_LANES]
     uint32_t* lds_gp;        // per-lane gray palette: word (i / 4) at lds_gp[(i / 4) * LDS_LANES]
+    uint32_t* lds_bg;        // per-lane background tile row (same word stride), valid for v's bits 0-11 == bg_key
+    int32_t bg_key;          // line-start v & 0xfff the tile row holds (-1: none)
 
     // ------------------------------------------------------------ interleaved memory
     __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mem[(size_t)__umul24(row, np)]; }
@@ -126,7 +130,7 @@ struct Console {
         nsl = (uint8_t)w(S_NSL); sl_lo = w(S_SL_LO); sl_hi = w(S_SL_HI);
         pcyc = (int32_t)w(S_PCYC); scanline = (int32_t)w(S_SCANLINE);
         v = (uint16_t)w(S_V); t = (uint16_t)w(S_T); inc = (uint16_t)w(S_INC);
-        pend_line = -1; sp_line = -1; pal_dirty = true;
+        pend_line = -1; sp_line = -1; pal_dirty = true; bg_key = -1;
         nmi_threshold();
     }
     __device__ void store(uint32_t* sc, uint32_t e) {
@@ -158,7 +162,7 @@ struct Console {
         long_spr = 0; nmi_en = 0; vblank = 0; show_bg = 1; show_spr = 1; even = 1;
         first_write = 1; bg_page = 0; spr_page = 0; v = 0; pcyc = 0; scanline = 0;
         oam_addr = 0; fine_x = 0; t = 0; inc = 1; pstate = ST_PRE; nsl = 0; sl_lo = sl_hi = 0;
-        pend_line = -1; sp_line = -1; pal_dirty = true;
+        pend_line = -1; sp_line = -1; pal_dirty = true; bg_key = -1;
         nmi_threshold();
     }
 
@@ -271,7 +275,7 @@ struct Console {
     }
     __device__ void vbus_write(uint16_t ad, uint8_t d) {
         if (ad < 0x2000) return;
-        if (ad < 0x3eff) st(ROW_VRAM + nt_row(ad), d);
+        if (ad < 0x3eff) { st(ROW_VRAM + nt_row(ad), d); bg_key = -1; }
         else if (ad < 0x3fff) { st(ROW_PAL + (ad == 0x3f10 ? 0 : (ad & 0x1f)), d); pal_dirty = true; }
     }
     __device__ __forceinline__ uint8_t nametable(uint16_t ad) const {
@@ -437,42 +441,70 @@ struct Console {
         sp_line = py;
     }
 
-    // The background tile `rel` tiles after the one v addresses (coarse-x wrap into the neighbouring
-    // name table as in coarse_x_add): pattern planes and palette bits 2-3 (nes_core.hpp:467-483).
-    __device__ __forceinline__ void bg_tile(int rel, uint32_t& lo, uint32_t& hi, uint32_t& at) const {
-        const int tot = (v & 0x1f) + rel;
-        uint16_t vv = (uint16_t)((v & ~0x1f) | (tot & 31));
-        if ((tot >> 5) & 1) vv ^= 0x400;
-        const uint8_t tile = nametable((uint16_t)(0x2000 | (vv & 0x0fff)));
-        const uint16_t pa = (uint16_t)(((tile * 16) + ((vv >> 12) & 7)) | (bg_page << 12));
+    // Background tile row of a line into the per-lane LDS cache: for tiles k = 0..32 from the line-start
+    // address v0 (coarse-x wrap into the neighbouring name table as in coarse_x_add), the tile index
+    // and the 2-bit attribute (nes_core.hpp:467-483). All 66 name-table reads are independent, so
+    // they are in flight together; a tile row serves the 8 scanlines of its coarse y.
+    __device__ __forceinline__ void fill_bg_row(uint16_t v0) {
+#pragma unroll
+        for (int w = 0; w < 9; w++) {
+            uint32_t tw = 0, aw = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int k = 4 * w + b;
+                if (k > 32) break;
+                const int tot = (v0 & 0x1f) + k;
+                uint16_t vv = (uint16_t)((v0 & ~0x1f) | (tot & 31));
+                if ((tot >> 5) & 1) vv ^= 0x400;
+                const uint32_t tile = nametable((uint16_t)(0x2000 | (vv & 0x0fff)));
+                const uint16_t aa = (uint16_t)(0x23c0 | (vv & 0x0c00) | ((vv >> 4) & 0x38) | ((vv >> 2) & 7));
+                const int sh = ((vv >> 4) & 4) | (vv & 2);
+                tw |= tile << (8 * b);
+                aw |= ((uint32_t)(nametable(aa) >> sh) & 3u) << (8 * b);
+            }
+            lds_bg[w * LDS_LANES] = tw;
+            lds_bg[(9 + w) * LDS_LANES] = aw;
+        }
+    }
+    // pattern planes and palette bits 2-3 of tile k of the cached row, for fine y `fy`
+    __device__ __forceinline__ void bg_tile(int k, int fy, uint32_t& lo, uint32_t& hi, uint32_t& at) const {
+        const uint32_t tile = lds_byte(lds_bg, k);
+        const uint16_t pa = (uint16_t)(((tile * 16) + fy) | (bg_page << 12));
         lo = cart.chr[pa];
         hi = cart.chr[pa + 8];
-        const uint16_t aa = (uint16_t)(0x23c0 | (vv & 0x0c00) | ((vv >> 4) & 0x38) | ((vv >> 2) & 7));
-        const int sh = ((vv >> 4) & 4) | (vv & 2);
-        at = (nametable(aa) >> sh) & 3u;
+        at = lds_byte(lds_bg, LDS_BG_ATTR + k);
     }
 
     // Pixels of visible dots [x0, x1): gray values into the frame buffer (nes_core.hpp:467-513), with
     // v as it is at x0 (dots_hit_scroll advances it afterwards). Pixels go in screen-aligned groups
     // of 8, so every lane of a wave runs the same code whatever its fine scroll: a group spans two
     // background tiles, kept as a 16-bit window per pattern plane (a PPU's shift registers), and the
-    // tile after them is fetched one group ahead. Sprites come from the LDS line buffer, where the
-    // first opaque listed sprite of each x sits; four gray pixels are stored as one word.
+    // tile after them is fetched one group ahead from the LDS tile row. Sprites come from the LDS line
+    // buffer, where the first opaque listed sprite of each x sits; four gray pixels are stored as one
+    // word.
     __device__ __forceinline__ void dots_drawn(int x0, int x1) {
         const int py = scanline;
         materialize_sprites();
         if (pal_dirty) build_gray_palette();
         const bool spr = show_spr && nsl;
         if (spr && sp_line != py) build_sprite_line(py);
-        const int f = fine_x;
-        const int kb = (f + x0) >> 3;                 // line tile index of pixel x0 (the one v addresses)
+        const int f = fine_x, fy = (v >> 12) & 7;
         const int g0 = x0 >> 3, g1 = (x1 + 7) >> 3;
+        if (show_bg) {
+            // line-start address: v addresses the tile of pixel x0, (f + x0) / 8 tiles into the line
+            const int kb = (f + x0) >> 3;
+            int c0 = (v & 0x1f) - kb;
+            uint16_t v0 = v;
+            if (c0 < 0) { c0 += 32; v0 ^= 0x400; }
+            v0 = (uint16_t)((v0 & ~0x1f) | c0);
+            if ((int32_t)(v0 & 0x0fff) != bg_key) { fill_bg_row(v0); bg_key = v0 & 0x0fff; }
+        }
         uint32_t alo = 0, ahi = 0, aat = 0, blo = 0, bhi = 0, bat = 0;
-        if (show_bg) { bg_tile(g0 - kb, alo, ahi, aat); bg_tile(g0 + 1 - kb, blo, bhi, bat); }
+        if (show_bg) { bg_tile(g0, fy, alo, ahi, aat); bg_tile(g0 + 1, fy, blo, bhi, bat); }
         uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g0) * np;   // word of pixels xq..xq+3
         for (int g = g0; g < g1; g++) {
             uint32_t clo = 0, chi = 0, cat = 0;
-            if (show_bg && g + 1 < g1) bg_tile(g + 2 - kb, clo, chi, cat);
+            if (show_bg && g + 1 < g1) bg_tile(g + 2, fy, clo, chi, cat);
             // pixel 8g + b is bit 15 - b of the window, after the fine-scroll shift
             const uint32_t wlo = ((alo << 8) | blo) << f, whi = ((ahi << 8) | bhi) << f;
             for (int q = 0; q < 2; q++) {
