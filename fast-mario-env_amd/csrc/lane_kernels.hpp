@@ -90,11 +90,11 @@ struct RomArgs {
     uint32_t nt_bits;        // bit k: name table k maps to VRAM $400
 };
 
-__device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_cyc) {
+__device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom, const uint32_t* s_dec) {
     Cart c;
     c.prg = s_rom;
     c.chr = s_rom + 0x8000;
-    c.cyc = s_cyc;
+    c.dec = s_dec;
     c.nt_bits = R.nt_bits;
     return c;
 }

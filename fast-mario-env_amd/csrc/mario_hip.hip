@@ -20,12 +20,12 @@ using namespace mh;
 
 namespace {
 
-// Stage PRG + CHR (40 KB) and the gray LUT in LDS; every thread of the block must call this.
-__device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint8_t* s_lut, uint8_t* s_cyc) {
+// Stage PRG + CHR (40 KB), the gray LUT and the decode table in LDS; every thread of the block must call this.
+__device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint8_t* s_lut, uint32_t* s_dec) {
     const uint4* src = (const uint4*)R.rom;
     uint4* dst = (uint4*)s_rom;
     for (int i = threadIdx.x; i < 0xa000 / 16; i += blockDim.x) dst[i] = src[i];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) { s_lut[i] = R.lut[i]; s_cyc[i] = kCycles[i]; }
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) { s_lut[i] = R.lut[i]; s_dec[i] = kDecode.w[i]; }
     __syncthreads();
 }
 
@@ -33,41 +33,41 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
 #define ROM_LDS                                                     \
     __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000]; \
     __shared__ uint8_t s_lut[256];                                  \
-    __shared__ uint8_t s_cyc[256];                                  \
+    __shared__ uint32_t s_dec[256];                                 \
     __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
     __shared__ uint32_t s_gp[(LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES];
 
 __device__ __forceinline__ LaneCtx lane_ctx(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_lut,
-                                            const uint8_t* s_cyc, uint32_t* s_sp, uint32_t* s_gp) {
-    return LaneCtx{make_cart(R, s_rom, s_cyc), s_lut, s_sp + threadIdx.x, s_gp + threadIdx.x};
+                                            const uint32_t* s_dec, uint32_t* s_sp, uint32_t* s_gp) {
+    return LaneCtx{make_cart(R, s_rom, s_dec), s_lut, s_sp + threadIdx.x, s_gp + threadIdx.x};
 }
 
 __global__ void __launch_bounds__(64) k_boot(BootArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut, s_cyc);
+    stage_rom(A.R, s_rom, s_lut, s_dec);
     const int l = blockIdx.x * blockDim.x + threadIdx.x;
-    if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), l);
+    if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), l);
 }
 
 __global__ void __launch_bounds__(64) k_cache(CacheArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut, s_cyc);
+    stage_rom(A.R, s_rom, s_lut, s_dec);
     const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), ci);
+    if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), ci);
 }
 
 __global__ void __launch_bounds__(64) k_step(StepArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut, s_cyc);
+    stage_rom(A.R, s_rom, s_lut, s_dec);
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), e);
+    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), e);
 }
 
 __global__ void __launch_bounds__(64) k_raw(RawArgs A) {
     ROM_LDS
-    stage_rom(A.R, s_rom, s_lut, s_cyc);
+    stage_rom(A.R, s_rom, s_lut, s_dec);
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_cyc, s_sp, s_gp), e);
+    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), e);
 }
 
 __global__ void __launch_bounds__(64) k_reset(ResetArgs A) {

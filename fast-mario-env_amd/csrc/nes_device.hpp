@@ -38,7 +38,7 @@ enum Scalar : int {
 };
 
 // Base cycles per opcode (data table of nes_core.hpp:42-51; 0 = not an official opcode).
-__device__ __constant__ static const uint8_t kCycles[256] = {
+constexpr uint8_t kCycleData[256] = {
     7, 6, 0, 0, 0, 3, 5, 0, 3, 2, 2, 0, 0, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
     6, 6, 0, 0, 3, 3, 5, 0, 4, 2, 2, 0, 4, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
     6, 6, 0, 0, 0, 3, 5, 0, 3, 2, 2, 0, 3, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
@@ -49,11 +49,124 @@ __device__ __constant__ static const uint8_t kCycles[256] = {
     2, 6, 0, 0, 3, 3, 5, 0, 2, 2, 2, 2, 4, 4, 6, 0, 2, 5, 0, 0, 0, 4, 6, 0, 2, 4, 0, 0, 0, 4, 7, 0,
 };
 
+// ---------------------------------------------------------------- decode table
+// One word per opcode with everything the fast instruction path needs, generated from the
+// reference's decode cascade (implied, branch, type 1, type 2, type 0; nes_core.hpp:619-1163):
+// addressing mode, page-cross rule, data read, ALU operation, source and destination register,
+// stack / control-flow operation, flag class and base cycles. Invalid opcodes keep their addressing
+// (type 0 with an invalid operation still consumes its operand bytes and page-cross cycle).
+namespace dec {
+enum : uint32_t { M_NONE = 0, M_IMM, M_ZP, M_ZPX, M_ZPY, M_ABS, M_ABSX, M_ABSY, M_INDX, M_INDY };
+enum : uint32_t { OP_PASS = 0, OP_ORA, OP_AND, OP_EOR, OP_ADC, OP_SBC, OP_CMP, OP_BIT, OP_ASL, OP_ROL, OP_LSR,
+                  OP_ROR, OP_INC, OP_DEC, OP_FLAG, OP_NOP };
+enum : uint32_t { R_M = 0, R_A, R_X, R_Y, R_SP };                       // R_M: the data operand
+enum : uint32_t { D_NONE = 0, D_A, D_X, D_Y, D_SP, D_MEM };
+enum : uint32_t { X_NONE = 0, X_BRK, X_JSR, X_RTS, X_RTI, X_PHA, X_PHP, X_PLA, X_PLP, X_JMP, X_JMPI, X_BRANCH };
+enum : uint32_t { FL_NONE = 0, FL_NZ, FL_NZC, FL_NZCV, FL_BIT, FL_OP };
+constexpr uint32_t PEN = 1u << 4, RD = 1u << 5, OK = 1u << 7;
+constexpr int ALU_SH = 8, SRC_SH = 12, DST_SH = 15, X_SH = 18, FL_SH = 22, FOP_SH = 25, CYC_SH = 28;
+
+constexpr uint32_t mk(uint32_t am, bool pen, bool rd, bool ok, uint32_t alu, uint32_t src, uint32_t dst,
+                      uint32_t x, uint32_t fl, uint32_t fop = 0) {
+    return am | (pen ? PEN : 0u) | (rd ? RD : 0u) | (ok ? OK : 0u) | alu << ALU_SH | src << SRC_SH |
+           dst << DST_SH | x << X_SH | fl << FL_SH | fop << FOP_SH;
+}
+constexpr uint32_t entry(int op) {
+    const int cc = op & 3, bbb = (op >> 2) & 7, fn = op >> 5;
+    const uint32_t cyc = (uint32_t)kCycleData[op] << CYC_SH;
+    switch (op) {   // the implied table (nes_core.hpp:630-690); flag ops: fop 0 CLC 1 SEC 2 CLI 3 SEI 4 CLV 5 CLD 6 SED
+        case 0x00: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_BRK, FL_NONE) | cyc;
+        case 0x08: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_PHP, FL_NONE) | cyc;
+        case 0x18: return mk(M_NONE, false, false, true, OP_FLAG, R_M, D_NONE, X_NONE, FL_OP, 0) | cyc;
+        case 0x20: return mk(M_ABS, false, false, true, OP_NOP, R_M, D_NONE, X_JSR, FL_NONE) | cyc;
+        case 0x28: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_PLP, FL_NONE) | cyc;
+        case 0x38: return mk(M_NONE, false, false, true, OP_FLAG, R_M, D_NONE, X_NONE, FL_OP, 1) | cyc;
+        case 0x40: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_RTI, FL_NONE) | cyc;
+        case 0x48: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_PHA, FL_NONE) | cyc;
+        case 0x4c: return mk(M_ABS, false, false, true, OP_NOP, R_M, D_NONE, X_JMP, FL_NONE) | cyc;
+        case 0x58: return mk(M_NONE, false, false, true, OP_FLAG, R_M, D_NONE, X_NONE, FL_OP, 2) | cyc;
+        case 0x60: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_RTS, FL_NONE) | cyc;
+        case 0x68: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_PLA, FL_NONE) | cyc;
+        case 0x6c: return mk(M_ABS, false, false, true, OP_NOP, R_M, D_NONE, X_JMPI, FL_NONE) | cyc;
+        case 0x78: return mk(M_NONE, false, false, true, OP_FLAG, R_M, D_NONE, X_NONE, FL_OP, 3) | cyc;
+        case 0x88: return mk(M_NONE, false, false, true, OP_DEC, R_Y, D_Y, X_NONE, FL_NZ) | cyc;
+        case 0x8a: return mk(M_NONE, false, false, true, OP_PASS, R_X, D_A, X_NONE, FL_NZ) | cyc;
+        case 0x98: return mk(M_NONE, false, false, true, OP_PASS, R_Y, D_A, X_NONE, FL_NZ) | cyc;
+        case 0x9a: return mk(M_NONE, false, false, true, OP_PASS, R_X, D_SP, X_NONE, FL_NONE) | cyc;
+        case 0xa8: return mk(M_NONE, false, false, true, OP_PASS, R_A, D_Y, X_NONE, FL_NZ) | cyc;
+        case 0xaa: return mk(M_NONE, false, false, true, OP_PASS, R_A, D_X, X_NONE, FL_NZ) | cyc;
+        case 0xb8: return mk(M_NONE, false, false, true, OP_FLAG, R_M, D_NONE, X_NONE, FL_OP, 4) | cyc;
+        case 0xba: return mk(M_NONE, false, false, true, OP_PASS, R_SP, D_X, X_NONE, FL_NZ) | cyc;
+        case 0xc8: return mk(M_NONE, false, false, true, OP_INC, R_Y, D_Y, X_NONE, FL_NZ) | cyc;
+        case 0xca: return mk(M_NONE, false, false, true, OP_DEC, R_X, D_X, X_NONE, FL_NZ) | cyc;
+        case 0xd8: return mk(M_NONE, false, false, true, OP_FLAG, R_M, D_NONE, X_NONE, FL_OP, 5) | cyc;
+        case 0xe8: return mk(M_NONE, false, false, true, OP_INC, R_X, D_X, X_NONE, FL_NZ) | cyc;
+        case 0xea: return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_NONE, FL_NONE) | cyc;
+        case 0xf8: return mk(M_NONE, false, false, true, OP_FLAG, R_M, D_NONE, X_NONE, FL_OP, 6) | cyc;
+        default: break;
+    }
+    if ((op & 0x1f) == 0x10) return mk(M_NONE, false, false, true, OP_NOP, R_M, D_NONE, X_BRANCH, FL_NONE) | cyc;
+    if (cc == 1) {
+        const uint32_t am = bbb == 0 ? M_INDX : bbb == 1 ? M_ZP : bbb == 2 ? M_IMM : bbb == 3 ? M_ABS
+                          : bbb == 4 ? M_INDY : bbb == 5 ? M_ZPX : bbb == 6 ? M_ABSY : M_ABSX;
+        const bool pen = fn != 4 && (bbb == 4 || bbb == 6 || bbb == 7);
+        switch (fn) {
+            case 0: return mk(am, pen, true, true, OP_ORA, R_A, D_A, X_NONE, FL_NZ) | cyc;
+            case 1: return mk(am, pen, true, true, OP_AND, R_A, D_A, X_NONE, FL_NZ) | cyc;
+            case 2: return mk(am, pen, true, true, OP_EOR, R_A, D_A, X_NONE, FL_NZ) | cyc;
+            case 3: return mk(am, pen, true, true, OP_ADC, R_A, D_A, X_NONE, FL_NZCV) | cyc;
+            case 4: return mk(am, pen, false, true, OP_PASS, R_A, D_MEM, X_NONE, FL_NONE) | cyc;
+            case 5: return mk(am, pen, true, true, OP_PASS, R_M, D_A, X_NONE, FL_NZ) | cyc;
+            case 6: return mk(am, pen, true, true, OP_CMP, R_A, D_NONE, X_NONE, FL_NZC) | cyc;
+            default: return mk(am, pen, true, true, OP_SBC, R_A, D_A, X_NONE, FL_NZCV) | cyc;
+        }
+    }
+    if (cc == 2 && bbb != 4 && bbb != 6) {
+        const bool xy = fn == 4 || fn == 5;
+        const uint32_t am = bbb == 0 ? M_IMM : bbb == 1 ? M_ZP : bbb == 2 ? M_NONE : bbb == 3 ? M_ABS
+                          : bbb == 5 ? (xy ? M_ZPY : M_ZPX) : (xy ? M_ABSY : M_ABSX);
+        const bool pen = bbb == 7, acc = bbb == 2;
+        if (fn < 4) {
+            const uint32_t alu = fn == 0 ? OP_ASL : fn == 1 ? OP_ROL : fn == 2 ? OP_LSR : OP_ROR;
+            return (acc ? mk(am, pen, false, true, alu, R_A, D_A, X_NONE, FL_NZC)
+                        : mk(am, pen, true, true, alu, R_M, D_MEM, X_NONE, FL_NZC)) | cyc;
+        }
+        switch (fn) {
+            case 4: return mk(am, pen, false, true, OP_PASS, R_X, D_MEM, X_NONE, FL_NONE) | cyc;
+            case 5: return mk(am, pen, true, true, OP_PASS, R_M, D_X, X_NONE, FL_NZ) | cyc;
+            case 6: return mk(am, pen, true, true, OP_DEC, R_M, D_MEM, X_NONE, FL_NZ) | cyc;
+            default: return mk(am, pen, true, true, OP_INC, R_M, D_MEM, X_NONE, FL_NZ) | cyc;
+        }
+    }
+    if (cc == 0 && (bbb & 1 || bbb == 0)) {
+        const uint32_t am = bbb == 0 ? M_IMM : bbb == 1 ? M_ZP : bbb == 3 ? M_ABS : bbb == 5 ? M_ZPX : M_ABSX;
+        const bool pen = bbb == 7;
+        switch (fn) {
+            case 1: return mk(am, pen, true, true, OP_BIT, R_A, D_NONE, X_NONE, FL_BIT) | cyc;
+            case 4: return mk(am, pen, false, true, OP_PASS, R_Y, D_MEM, X_NONE, FL_NONE) | cyc;
+            case 5: return mk(am, pen, true, true, OP_PASS, R_M, D_Y, X_NONE, FL_NZ) | cyc;
+            case 6: return mk(am, pen, true, true, OP_CMP, R_Y, D_NONE, X_NONE, FL_NZC) | cyc;
+            case 7: return mk(am, pen, true, true, OP_CMP, R_X, D_NONE, X_NONE, FL_NZC) | cyc;
+            default: return mk(am, pen, false, false, OP_NOP, R_M, D_NONE, X_NONE, FL_NONE) | cyc;
+        }
+    }
+    return mk(M_NONE, false, false, false, OP_NOP, R_M, D_NONE, X_NONE, FL_NONE) | cyc;
+}
+struct Table {
+    uint32_t w[256];
+    constexpr Table() : w() {
+        for (int i = 0; i < 256; i++) w[i] = entry(i);
+    }
+};
+}  // namespace dec
+
+__device__ __constant__ static const dec::Table kDecode{};
+
 // Read-only cartridge view: PRG/CHR in LDS, name-table offsets in registers (uniform).
 struct Cart {
     const uint8_t* prg;      // 0x8000 bytes (16 KB images mirrored)
     const uint8_t* chr;      // 0x2000 bytes
-    const uint8_t* cyc;      // kCycles (LDS copy)
+    const uint32_t* dec;     // decode words (LDS copy of kDecode)
     uint32_t nt_bits;        // bit k set: name table k ($2000 + k * $400) maps to VRAM $400, else to $000
 };
 
@@ -842,7 +955,7 @@ struct Console {
         }
         if (!I.executed && (nx == U_DW || nx == U_END)) execute(I);
         if (nx != U_END) return nx;
-        if (I.ok) skip += cart.cyc[I.op];
+        if (I.ok) skip += (int)((cart.dec[I.op] >> dec::CYC_SH) & 7u);
         else bad_ops++;
         exec_at = cur + (skip >= 1 ? skip : 1);
         zero_skip = skip <= 0;
@@ -858,6 +971,114 @@ struct Console {
         if (d < 1) d = 1;
         const int32_t s = ppu_calls + d;
         return s < cap ? s : cap;
+    }
+
+    // One whole instruction whose opcode and operand bytes are in PRG (pc <= 0xfffd), from its decode
+    // word: addressing, at most one data read and one data write through the bus, the ALU as register
+    // selects, and one small switch for the stack / control-flow operations. The order of the bus
+    // accesses is the reference's (pointer, data read, data write; JSR/BRK push before reading PRG,
+    // which cannot alias the stack). Returns false, with no effect, when a data access needs the PPU
+    // caught up first; the caller catches up to `tgt` and starts the instruction again.
+    __device__ __forceinline__ bool fast_instruction(int32_t j, int32_t tgt, uint8_t op, uint8_t b1, uint8_t b2) {
+        using namespace dec;
+        const uint32_t D = cart.dec[op];
+        const uint32_t am = D & 15u, xop = (D >> X_SH) & 15u, dst = (D >> DST_SH) & 7u;
+        const bool rd = (D & RD) != 0, wr = dst == D_MEM;
+        const uint16_t absv = (uint16_t)(b1 | b2 << 8);
+        uint16_t base = absv;
+        if (am == M_INDX || am == M_INDY) {   // pointer from the zero page
+            const uint8_t z = am == M_INDX ? (uint8_t)(b1 + x) : b1;
+            base = (uint16_t)(ram(z) | ram((uint8_t)(z + 1)) << 8);
+        }
+        const uint8_t idx = (am == M_ZPX || am == M_ABSX) ? x : (am == M_ZPY || am == M_ABSY || am == M_INDY) ? y : 0;
+        uint16_t ea;
+        if (am == M_ZP || am == M_ZPX || am == M_ZPY) ea = (uint8_t)(b1 + idx);
+        else if (am == M_IMM) ea = (uint16_t)(pc + 1);
+        else ea = (uint16_t)(base + idx);
+        const uint16_t p2 = (uint16_t)((absv & 0xff00) | ((absv + 1) & 0xff));   // JMP (ind): high byte, page wrap
+        const bool sync = xop == X_JMPI ? (needs_sync(absv, false) || needs_sync(p2, false))
+                                        : ((rd && needs_sync(ea, false)) || (wr && needs_sync(ea, true)));
+        if (sync && ppu_calls < tgt) return false;
+        cur = j;
+        skip = 0;
+        instructions++;
+        if (D & PEN) cross_penalty(base, (uint16_t)(base + idx), 1);
+        // data operand and ALU
+        const uint8_t m = rd && am != M_IMM ? read(ea) : b1;
+        const uint32_t alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, fl = (D >> FL_SH) & 7u;
+        const uint32_t rv = src == R_A ? a : src == R_X ? x : src == R_Y ? y : src == R_SP ? sp : m;
+        const uint32_t sv = rd ? m : rv;                          // operand of the unary operations
+        const uint32_t cin = (p & FC) ? 1u : 0u;
+        const uint32_t sum = a + m + cin;                         // ADC
+        const uint32_t dif = a - m - (1u - cin);                  // SBC
+        const uint32_t cmp = rv - m;                              // CMP / CPX / CPY
+        const bool left = alu == OP_ASL || alu == OP_ROL, right = alu == OP_LSR || alu == OP_ROR;
+        const uint32_t shl = (sv << 1) | (alu == OP_ROL ? cin : 0u);
+        const uint32_t shr = (sv >> 1) | (alu == OP_ROR ? cin << 7 : 0u);
+        const uint32_t res = alu == OP_ORA ? (a | m) : alu == OP_AND ? (a & m) : alu == OP_EOR ? (a ^ m)
+                           : alu == OP_ADC ? sum : alu == OP_SBC ? dif : alu == OP_CMP ? cmp
+                           : left ? shl : right ? shr : alu == OP_INC ? sv + 1 : alu == OP_DEC ? sv - 1 : sv;
+        const uint8_t r8 = (uint8_t)res;
+        const bool carry = alu == OP_ADC ? (sum & 0x100) != 0 : (alu == OP_SBC || alu == OP_CMP) ? !(res & 0x100)
+                         : left ? (sv & 0x80) != 0 : (sv & 1) != 0;
+        const bool ovf = alu == OP_ADC ? ((a ^ sum) & (m ^ sum) & 0x80) != 0 : ((a ^ dif) & (~(uint32_t)m ^ dif) & 0x80) != 0;
+        uint8_t np = p;
+        if (fl == FL_NZ || fl == FL_NZC || fl == FL_NZCV)
+            np = (uint8_t)((np & ~(FZ | FN)) | (r8 ? 0 : FZ) | (r8 & 0x80 ? FN : 0));
+        if (fl == FL_NZC || fl == FL_NZCV) np = carry ? (uint8_t)(np | FC) : (uint8_t)(np & ~FC);
+        if (fl == FL_NZCV) np = ovf ? (uint8_t)(np | FV) : (uint8_t)(np & ~FV);
+        if (fl == FL_BIT)
+            np = (uint8_t)((np & ~(FZ | FV | FN)) | ((a & m) ? 0 : FZ) | (m & 0x40 ? FV : 0) | (m & 0x80 ? FN : 0));
+        if (fl == FL_OP) {   // CLC SEC CLI SEI CLV CLD SED
+            const uint32_t fop = (D >> FOP_SH) & 7u;
+            const uint8_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;
+            np = (fop == 1 || fop == 3 || fop == 6) ? (uint8_t)(np | fm) : (uint8_t)(np & ~fm);
+        }
+        p = np;
+        a = dst == D_A ? r8 : a;
+        x = dst == D_X ? r8 : x;
+        y = dst == D_Y ? r8 : y;
+        sp = dst == D_SP ? r8 : sp;
+        if (wr) write(ea, r8);
+        // stack and control flow
+        uint16_t npc = (uint16_t)(pc + (am == M_NONE ? 1 : (am == M_ABS || am == M_ABSX || am == M_ABSY) ? 3 : 2));
+        if (xop != X_NONE) {
+            const uint16_t ret = (uint16_t)(pc + 2);
+            switch (xop) {
+                case X_BRK:
+                    push((uint8_t)(ret >> 8)); push((uint8_t)ret); push((uint8_t)(p | 0x30));
+                    p |= FI;
+                    npc = (uint16_t)(prg(0xfffe) | prg(0xffff) << 8);
+                    skip += 7;
+                    break;
+                case X_JSR: push((uint8_t)(ret >> 8)); push((uint8_t)ret); npc = absv; break;
+                case X_RTS: { const uint8_t lo = pull(); const uint8_t hi = pull(); npc = (uint16_t)((lo | hi << 8) + 1); break; }
+                case X_RTI: { p = pull(); const uint8_t lo = pull(); const uint8_t hi = pull(); npc = (uint16_t)(lo | hi << 8); break; }
+                case X_PHA: push(a); break;
+                case X_PHP: push(p); break;
+                case X_PLA: a = pull(); set_nz(a); break;
+                case X_PLP: p = pull(); break;
+                case X_JMP: npc = absv; break;
+                case X_JMPI: { const uint8_t lo = read(absv); const uint8_t hi = read(p2); npc = (uint16_t)(lo | hi << 8); break; }
+                default: {   // branch on N, V, C, Z (op bits 6-7) equal to op bit 5; 2 bytes
+                    const uint8_t fm = (op >> 6) == 0 ? FN : (op >> 6) == 1 ? FV : (op >> 6) == 2 ? FC : FZ;
+                    npc = ret;
+                    if (((p & fm) != 0) == ((op & 0x20) != 0)) {
+                        skip += 1;
+                        const uint16_t to = (uint16_t)(npc + (int8_t)b1);
+                        cross_penalty(npc, to, 2);
+                        npc = to;
+                    }
+                    break;
+                }
+            }
+        }
+        pc = npc;
+        if (D & OK) skip += (int)((D >> CYC_SH) & 7u);
+        else bad_ops++;
+        exec_at = j + (skip >= 1 ? skip : 1);
+        zero_skip = skip <= 0;
+        return true;
     }
 
     // PPU calls from the current PPU position to (line, dot) on the frame timeline of
@@ -988,6 +1209,10 @@ struct Console {
                         if (ppu_calls < tgt) { want = tgt; continue; }   // the sync of the LDA $2002 at j
                         if (poll_skip(j, end, br == 0xf0)) continue;
                     }
+                }
+                if (in_prg && pc <= 0xfffd) {
+                    if (!fast_instruction(j, tgt, op0, q1, q2)) want = tgt;
+                    continue;
                 }
                 cur = j;
                 skip = 0;
