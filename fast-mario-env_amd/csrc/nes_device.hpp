@@ -728,240 +728,6 @@ struct Console {
     __device__ __forceinline__ uint8_t pull() { sp++; return ram(0x100 | sp); }
     __device__ __forceinline__ void cross_penalty(uint16_t u, uint16_t w, int k) { if ((u & 0xff00) != (w & 0xff00)) skip += k; }
 
-    // Opcode families in the reference's decode order: implied, branch, type 1, type 2, type 0.
-    enum : uint8_t { F_IMP, F_BR, F_G1, F_G2, F_G0, F_BAD };
-    // addressing of the type 0/1/2 families
-    enum : uint8_t { A_NONE, A_IMM, A_ZP, A_ZPI, A_ABS, A_ABSI, A_INDX, A_INDY };
-    // Bus steps of an instruction. The steps after the current one are queued in Ins::prog, 3 bits
-    // each, lowest first: operand byte (B1), operand word (W1, W2), JMP-indirect pointer (PLO, PHI),
-    // data read (DR), data write (DW).
-    enum : uint8_t { U_END = 0, U_B1, U_W1, U_W2, U_PLO, U_PHI, U_DR, U_DW, U_OP, U_START };
-
-    // The instruction in flight.
-    struct Ins {
-        uint32_t prog;
-        uint16_t ea;
-        uint8_t op, fam, fn, am, idx, b1, lo, hi, val, wv, pb1, pb2;
-        bool pen, pf, ok, executed;
-    };
-
-    // the reference's implied-opcode table (nes_core.hpp:640-690)
-    __device__ __forceinline__ static bool is_implied(uint8_t op) {
-        const uint8_t cc = op & 3, bbb = (op >> 2) & 7, aaa = op >> 5;
-        if (cc == 0) return bbb == 2 || bbb == 6 || (bbb == 0 && aaa < 4) || op == 0x4c || op == 0x6c;
-        return cc == 2 && aaa >= 4 && (bbb == 2 || (bbb == 6 && aaa < 6));
-    }
-
-    // Decode the opcode (pc is past it): family, addressing, the queue of bus steps, and the whole
-    // effect of implied instructions without bus steps.
-    __device__ __forceinline__ void decode(Ins& I) {
-        const uint8_t op = I.op, cc = op & 3, bbb = (op >> 2) & 7, fn = op >> 5;
-        I.fn = fn; I.prog = 0; I.am = A_NONE; I.idx = 0; I.pen = false; I.ok = true; I.executed = false;
-        if (is_implied(op)) {
-            I.fam = F_IMP;
-            I.executed = true;
-            switch (op) {
-                case 0x00:
-                    pc++;
-                    push((uint8_t)(pc >> 8)); push((uint8_t)pc); push((uint8_t)(p | 0x30));
-                    p |= FI; pc = (uint16_t)(prg(0xfffe) | prg(0xffff) << 8); skip += 7;
-                    break;
-                case 0x08: push(p); break;
-                case 0x18: flag(FC, false); break;
-                case 0x20: { const uint16_t ret = (uint16_t)(pc + 1); push((uint8_t)(ret >> 8)); push((uint8_t)ret);
-                             I.prog = U_W1 | U_W2 << 3; break; }
-                case 0x28: p = pull(); break;
-                case 0x38: flag(FC, true); break;
-                case 0x40: { p = pull(); const uint8_t lo = pull(); const uint8_t hi = pull(); pc = (uint16_t)(lo | hi << 8); break; }
-                case 0x48: push(a); break;
-                case 0x4c: I.prog = U_W1 | U_W2 << 3; break;
-                case 0x58: flag(FI, false); break;
-                case 0x60: { const uint8_t lo = pull(); const uint8_t hi = pull(); pc = (uint16_t)((lo | hi << 8) + 1); break; }
-                case 0x68: a = pull(); set_nz(a); break;
-                case 0x6c: I.prog = U_W1 | U_W2 << 3 | U_PLO << 6 | U_PHI << 9; break;
-                case 0x78: flag(FI, true); break;
-                case 0x88: y--; set_nz(y); break;
-                case 0x8a: a = x; set_nz(a); break;
-                case 0x98: a = y; set_nz(a); break;
-                case 0x9a: sp = x; break;
-                case 0xa8: y = a; set_nz(y); break;
-                case 0xaa: x = a; set_nz(x); break;
-                case 0xb8: flag(FV, false); break;
-                case 0xba: x = sp; set_nz(x); break;
-                case 0xc8: y++; set_nz(y); break;
-                case 0xca: x--; set_nz(x); break;
-                case 0xd8: flag(FD, false); break;
-                case 0xe8: x++; set_nz(x); break;
-                case 0xf8: flag(FD, true); break;
-                default: break;   // 0xea NOP
-            }
-            return;
-        }
-        if ((op & 0x1f) == 0x10) {
-            I.fam = F_BR;
-            I.executed = true;
-            const uint8_t which = fn >> 1 == 0 ? FN : fn >> 1 == 1 ? FV : fn >> 1 == 2 ? FC : FZ;
-            if (has(which) == ((op & 0x20) != 0)) I.prog = U_B1;
-            else pc++;
-            return;
-        }
-        uint32_t data;   // data steps after the addressing steps
-        if (cc == 1) {
-            I.fam = F_G1;
-            I.am = bbb == 0 ? A_INDX : bbb == 1 ? A_ZP : bbb == 2 ? A_IMM : bbb == 3 ? A_ABS
-                 : bbb == 4 ? A_INDY : bbb == 5 ? A_ZPI : A_ABSI;
-            I.idx = bbb == 6 || bbb == 4 ? y : x;
-            I.pen = fn != 4;
-            data = fn == 4 ? U_DW : U_DR;
-        } else if (cc == 2 && bbb != 4 && bbb != 6) {
-            I.fam = F_G2;
-            I.am = bbb == 0 ? A_IMM : bbb == 1 ? A_ZP : bbb == 2 ? A_NONE : bbb == 3 ? A_ABS : bbb == 5 ? A_ZPI : A_ABSI;
-            I.idx = fn == 4 || fn == 5 ? y : x;
-            I.pen = true;
-            data = fn == 4 ? U_DW : fn == 5 ? U_DR : bbb == 2 ? U_END : (U_DR | U_DW << 3);
-        } else if (cc == 0 && (bbb & 1 || bbb == 0)) {
-            I.fam = F_G0;
-            I.am = bbb == 0 ? A_IMM : bbb == 1 ? A_ZP : bbb == 3 ? A_ABS : bbb == 5 ? A_ZPI : A_ABSI;
-            I.idx = x;
-            I.pen = true;
-            I.ok = fn == 1 || fn >= 4;
-            I.executed = !I.ok;   // an invalid operation still performs its addressing reads
-            data = !I.ok ? U_END : fn == 4 ? U_DW : U_DR;
-        } else {
-            I.fam = F_BAD;
-            I.ok = false;
-            I.executed = true;
-            return;
-        }
-        switch (I.am) {
-            case A_IMM: I.ea = pc++; I.prog = data; break;
-            case A_NONE: I.prog = data; break;
-            case A_ABS: case A_ABSI: I.prog = U_W1 | U_W2 << 3 | data << 6; break;
-            default: I.prog = U_B1 | data << 3; break;
-        }
-    }
-    // effective address once the operand bytes are in (type 0/1/2 families)
-    __device__ __forceinline__ void finish_address(Ins& I) {
-        const uint16_t w = (uint16_t)(I.lo | I.hi << 8);
-        switch (I.am) {
-            case A_ZP: I.ea = I.b1; break;
-            case A_ZPI: I.ea = (uint8_t)(I.b1 + I.idx); break;
-            case A_ABS: I.ea = w; break;
-            case A_ABSI: if (I.pen) cross_penalty(w, (uint16_t)(w + I.idx), 1); I.ea = (uint16_t)(w + I.idx); break;
-            case A_INDX: case A_INDY: {
-                const uint8_t z = I.am == A_INDX ? (uint8_t)(I.b1 + x) : I.b1;
-                const uint16_t base = (uint16_t)(ram(z) | ram((uint8_t)(z + 1)) << 8);
-                if (I.am == A_INDX) { I.ea = base; break; }
-                if (I.pen) cross_penalty(base, (uint16_t)(base + I.idx), 1);
-                I.ea = (uint16_t)(base + I.idx);
-                break;
-            }
-            default: break;
-        }
-    }
-    // Operation of the type 0/1/2 families after their data read; sets Ins::wv for a data write.
-    __device__ __forceinline__ void execute(Ins& I) {
-        I.executed = true;
-        const uint8_t fn = I.fn, d = I.val;
-        if (I.fam == F_G1) {
-            switch (fn) {
-                case 0: a |= d; set_nz(a); break;
-                case 1: a &= d; set_nz(a); break;
-                case 2: a ^= d; set_nz(a); break;
-                case 3: {
-                    const uint16_t s = (uint16_t)(a + d + (has(FC) ? 1 : 0));
-                    flag(FC, s & 0x100); flag(FV, (a ^ s) & (d ^ s) & 0x80);
-                    a = (uint8_t)s; set_nz(a);
-                    break;
-                }
-                case 4: I.wv = a; break;
-                case 5: a = d; set_nz(a); break;
-                case 6: { const uint16_t r = (uint16_t)(a - d); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
-                default: {
-                    const uint16_t r = (uint16_t)(a - d - (has(FC) ? 0 : 1));
-                    flag(FC, !(r & 0x100)); flag(FV, (a ^ r) & (~d ^ r) & 0x80);
-                    a = (uint8_t)r; set_nz((uint8_t)r);
-                    break;
-                }
-            }
-        } else if (I.fam == F_G2) {
-            const bool acc = I.am == A_NONE;
-            switch (fn) {
-                case 0: case 1: case 2: case 3: {
-                    const bool cin = has(FC) && (fn & 1);
-                    const uint8_t s = acc ? a : d;
-                    uint8_t r;
-                    if (fn < 2) { flag(FC, s & 0x80); r = (uint8_t)((s << 1) | cin); }
-                    else { flag(FC, s & 1); r = (uint8_t)((s >> 1) | (cin << 7)); }
-                    set_nz(r);
-                    if (acc) a = r; else I.wv = r;
-                    break;
-                }
-                case 4: I.wv = x; break;
-                case 5: x = d; set_nz(x); break;
-                case 6: I.wv = (uint8_t)(d - 1); set_nz(I.wv); break;
-                default: I.wv = (uint8_t)(d + 1); set_nz(I.wv); break;
-            }
-        } else {
-            switch (fn) {
-                case 1: flag(FZ, !(a & d)); flag(FV, d & 0x40); flag(FN, d & 0x80); break;
-                case 4: I.wv = y; break;
-                case 5: y = d; set_nz(y); break;
-                case 6: { const uint16_t r = (uint16_t)(y - d); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
-                default: { const uint16_t r = (uint16_t)(x - d); flag(FC, !(r & 0x100)); set_nz((uint8_t)r); break; }
-            }
-        }
-    }
-    // the value v of bus step u arrived
-    __device__ __forceinline__ void consume(Ins& I, uint8_t u, uint8_t v) {
-        switch (u) {
-            case U_B1:
-                I.b1 = v; pc++;
-                if (I.fam == F_BR) {   // taken branch
-                    skip += 1;
-                    const uint16_t to = (uint16_t)(pc + (int8_t)v);
-                    cross_penalty(pc, to, 2);
-                    pc = to;
-                } else {
-                    finish_address(I);
-                }
-                break;
-            case U_W1: I.lo = v; break;
-            case U_W2:
-                I.hi = v;
-                if (I.fam == F_IMP) {
-                    if (I.op == 0x6c) I.ea = (uint16_t)(I.lo | v << 8);   // pointer of JMP (ind)
-                    else pc = (uint16_t)(I.lo | v << 8);                 // JMP / JSR target
-                } else {
-                    pc += 2;
-                    finish_address(I);
-                }
-                break;
-            case U_PLO: I.lo = v; break;
-            case U_PHI: pc = (uint16_t)(I.lo | v << 8); break;
-            case U_DR: I.val = v; break;
-            default: break;
-        }
-    }
-    // Next bus step of the instruction; operand bytes prefetched from PRG are taken without the bus.
-    // Returns U_START once the instruction is complete (cycles, exec_at and zero_skip are set then).
-    __device__ __forceinline__ uint8_t advance(Ins& I) {
-        uint8_t nx;
-        for (;;) {
-            nx = I.prog & 7;
-            I.prog >>= 3;
-            if (I.pf && nx >= U_B1 && nx <= U_W2) { consume(I, nx, nx == U_W2 ? I.pb2 : I.pb1); continue; }
-            break;
-        }
-        if (!I.executed && (nx == U_DW || nx == U_END)) execute(I);
-        if (nx != U_END) return nx;
-        if (I.ok) skip += (int)((cart.dec[I.op] >> dec::CYC_SH) & 7u);
-        else bad_ops++;
-        exec_at = cur + (skip >= 1 ? skip : 1);
-        zero_skip = skip <= 0;
-        return U_START;
-    }
-
     // End of the next frame slice: the PPU call after which dots 1..256 of the next render line are
     // done (this line's if they are still ahead), capped at the frame end `cap`.
     __device__ __forceinline__ int32_t next_slice(int32_t cap) const {
@@ -973,15 +739,26 @@ struct Console {
         return s < cap ? s : cap;
     }
 
-    // One whole instruction whose opcode and operand bytes are in PRG (pc <= 0xfffd), from its decode
-    // word: addressing, at most one data read and one data write through the bus, the ALU as register
-    // selects, and one small switch for the stack / control-flow operations. The order of the bus
-    // accesses is the reference's (pointer, data read, data write; JSR/BRK push before reading PRG,
-    // which cannot alias the stack). Returns false, with no effect, when a data access needs the PPU
-    // caught up first; the caller catches up to `tgt` and starts the instruction again.
-    __device__ __forceinline__ bool fast_instruction(int32_t j, int32_t tgt, uint8_t op, uint8_t b1, uint8_t b2) {
+    // One whole instruction from its decode word: addressing, at most one data read and one data
+    // write through the bus, the ALU as register selects, and one small switch for the stack /
+    // control-flow operations, in the reference's bus order (operand bytes, pointer, data read, data
+    // write; JSR pushes before reading its operand, a branch reads its offset only when taken).
+    // `pf`: the opcode and both following bytes are in PRG (pc <= 0xfffd) and were read as op, q1, q2,
+    // which has no side effects; otherwise they are fetched through the bus, with the PPU caught up
+    // first because a fetch may hit a PPU register. Returns false, with no effect, when the PPU must be
+    // caught up to `tgt` first; the caller does that and starts the instruction again.
+    __device__ __forceinline__ bool instruction(int32_t j, int32_t tgt, bool pf, uint8_t op, uint8_t q1, uint8_t q2) {
         using namespace dec;
+        if (!pf && ppu_calls < tgt) return false;
+        if (!pf) op = read(pc);
         const uint32_t D = cart.dec[op];
+        const uint32_t xop0 = (D >> X_SH) & 15u;
+        uint8_t b1 = q1, b2 = q2;
+        if (!pf && xop0 != X_JSR && xop0 != X_BRANCH) {   // JSR and branches fetch below, in their order
+            const uint32_t am0 = D & 15u;
+            if (am0 != M_NONE) b1 = read((uint16_t)(pc + 1));
+            if (am0 == M_ABS || am0 == M_ABSX || am0 == M_ABSY) b2 = read((uint16_t)(pc + 2));
+        }
         const uint32_t am = D & 15u, xop = (D >> X_SH) & 15u, dst = (D >> DST_SH) & 7u;
         const bool rd = (D & RD) != 0, wr = dst == D_MEM;
         const uint16_t absv = (uint16_t)(b1 | b2 << 8);
@@ -998,7 +775,7 @@ struct Console {
         const uint16_t p2 = (uint16_t)((absv & 0xff00) | ((absv + 1) & 0xff));   // JMP (ind): high byte, page wrap
         const bool sync = xop == X_JMPI ? (needs_sync(absv, false) || needs_sync(p2, false))
                                         : ((rd && needs_sync(ea, false)) || (wr && needs_sync(ea, true)));
-        if (sync && ppu_calls < tgt) return false;
+        if (sync && ppu_calls < tgt) return false;   // only when pf: no bus access has happened yet
         cur = j;
         skip = 0;
         instructions++;
@@ -1051,7 +828,10 @@ struct Console {
                     npc = (uint16_t)(prg(0xfffe) | prg(0xffff) << 8);
                     skip += 7;
                     break;
-                case X_JSR: push((uint8_t)(ret >> 8)); push((uint8_t)ret); npc = absv; break;
+                case X_JSR:
+                    push((uint8_t)(ret >> 8)); push((uint8_t)ret);
+                    npc = pf ? absv : (uint16_t)(read((uint16_t)(pc + 1)) | read((uint16_t)(pc + 2)) << 8);
+                    break;
                 case X_RTS: { const uint8_t lo = pull(); const uint8_t hi = pull(); npc = (uint16_t)((lo | hi << 8) + 1); break; }
                 case X_RTI: { p = pull(); const uint8_t lo = pull(); const uint8_t hi = pull(); npc = (uint16_t)(lo | hi << 8); break; }
                 case X_PHA: push(a); break;
@@ -1065,7 +845,8 @@ struct Console {
                     npc = ret;
                     if (((p & fm) != 0) == ((op & 0x20) != 0)) {
                         skip += 1;
-                        const uint16_t to = (uint16_t)(npc + (int8_t)b1);
+                        const uint8_t off = pf ? b1 : read((uint16_t)(pc + 1));
+                        const uint16_t to = (uint16_t)(npc + (int8_t)off);
                         cross_penalty(npc, to, 2);
                         npc = to;
                     }
@@ -1143,11 +924,10 @@ struct Console {
 
     // One nes-py Emulator::step (nes_core.hpp:1166-1204) with the exact `JMP *` idle fast-forward.
     //
-    // Every lane runs the same loop body: at most one bus access per iteration, through one read
-    // and one write site, and one PPU catch-up site (`want`) for the NMI point, PPU-register
-    // accesses, the poll fast-forward and the frame slices. Branching per opcode is confined to
-    // register arithmetic, so a wave whose lanes run different instructions stays converged on the
-    // memory accesses.
+    // Every lane runs the same loop body: one whole instruction per iteration, and one PPU catch-up
+    // site (`want`) for the NMI point, PPU-register accesses, the poll fast-forward and the frame
+    // slices. Branching per opcode is confined to register arithmetic, so a wave whose lanes run
+    // different instructions stays converged on the memory accesses.
     //
     // The frame is cut into slices that end right after the visible dots of a render line (and at
     // the frame end). A lane only starts an instruction j whose catch-up point 3 (j + 1) is at most
@@ -1159,9 +939,6 @@ struct Console {
     // of j.
     __device__ __forceinline__ void frame() {
         const int32_t end = FRAME_ITERS, last_call = 3 * FRAME_ITERS;
-        Ins I;
-        I.pf = false; I.pb1 = I.pb2 = 0;
-        uint8_t u = U_START;
         int32_t want = -1;
         int32_t slice = next_slice(last_call);   // end of this lane's current slice, in PPU calls
         bool parked = false, synced = false;
@@ -1182,75 +959,34 @@ struct Console {
                 continue;
             }
             if (parked) continue;
-            if (u == U_START) {
-                const int32_t j = exec_at;
-                const int32_t tgt = 3 * (j + 1);
-                if (j >= end || tgt > slice) { parked = true; continue; }
-                if (tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; continue; }
-                // PRG bytes at pc for the fast paths; the idle check reads 0xff past 0xffff
-                const bool in_prg = pc >= 0x8000;
-                uint8_t op0 = 0, q1 = 0xff, q2 = 0xff;
-                if (in_prg) {
-                    op0 = prg(pc);
-                    if (pc != 0xffff) q1 = prg((uint16_t)(pc + 1));
-                    if (pc < 0xfffe) q2 = prg((uint16_t)(pc + 2));
-                }
-                if (in_prg && op0 == 0x4c && (uint16_t)(q1 | q2 << 8) == pc) {
-                    const int32_t lim_end = end - j, lim_nmi = nmi_thresh - tgt;
-                    const int32_t k1 = lim_end > 0 ? (lim_end + 2) / 3 : 0;
-                    const int32_t k2 = lim_nmi > 0 ? (lim_nmi + 8) / 9 : 0;
-                    const int32_t k = k1 < k2 ? k1 : k2;
-                    if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; continue; }
-                }
-                if (in_prg && op0 == 0xad && q1 == 0x02 && q2 == 0x20 && pc <= 0xfff8 && prg(pc + 3) == 0x29 &&
-                    prg(pc + 4) == 0x40 && prg(pc + 6) == 0xf9) {
-                    const uint8_t br = prg(pc + 5);
-                    if (br == 0xf0 || br == 0xd0) {
-                        if (ppu_calls < tgt) { want = tgt; continue; }   // the sync of the LDA $2002 at j
-                        if (poll_skip(j, end, br == 0xf0)) continue;
-                    }
-                }
-                if (in_prg && pc <= 0xfffd) {
-                    if (!fast_instruction(j, tgt, op0, q1, q2)) want = tgt;
-                    continue;
-                }
-                cur = j;
-                skip = 0;
-                instructions++;
-                if (in_prg) {
-                    I.op = op0; I.pf = pc <= 0xfffd; I.pb1 = q1; I.pb2 = q2;
-                    pc++;
-                    decode(I);
-                    u = advance(I);
-                    if (u == U_START) continue;
-                } else {
-                    I.pf = false;
-                    u = U_OP;
+            const int32_t j = exec_at;
+            const int32_t tgt = 3 * (j + 1);
+            if (j >= end || tgt > slice) { parked = true; continue; }
+            if (tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; continue; }
+            // PRG bytes at pc for the fast paths; the idle check reads 0xff past 0xffff
+            const bool in_prg = pc >= 0x8000;
+            uint8_t op0 = 0, q1 = 0xff, q2 = 0xff;
+            if (in_prg) {
+                op0 = prg(pc);
+                if (pc != 0xffff) q1 = prg((uint16_t)(pc + 1));
+                if (pc < 0xfffe) q2 = prg((uint16_t)(pc + 2));
+            }
+            if (in_prg && op0 == 0x4c && (uint16_t)(q1 | q2 << 8) == pc) {
+                const int32_t lim_end = end - j, lim_nmi = nmi_thresh - tgt;
+                const int32_t k1 = lim_end > 0 ? (lim_end + 2) / 3 : 0;
+                const int32_t k2 = lim_nmi > 0 ? (lim_nmi + 8) / 9 : 0;
+                const int32_t k = k1 < k2 ? k1 : k2;
+                if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; continue; }
+            }
+            if (in_prg && op0 == 0xad && q1 == 0x02 && q2 == 0x20 && pc <= 0xfff8 && prg(pc + 3) == 0x29 &&
+                prg(pc + 4) == 0x40 && prg(pc + 6) == 0xf9) {
+                const uint8_t br = prg(pc + 5);
+                if (br == 0xf0 || br == 0xd0) {
+                    if (ppu_calls < tgt) { want = tgt; continue; }   // the sync of the LDA $2002 at j
+                    if (poll_skip(j, end, br == 0xf0)) continue;
                 }
             }
-            // the bus step u
-            uint16_t ad;
-            bool wr = false;
-            switch (u) {
-                case U_OP: case U_B1: case U_W1: ad = pc; break;
-                case U_W2: ad = (uint16_t)(pc + 1); break;
-                case U_PLO: ad = I.ea; break;
-                case U_PHI: ad = (uint16_t)((I.ea & 0xff00) | ((I.ea + 1) & 0xff)); break;
-                case U_DR: ad = I.ea; break;
-                default: ad = I.ea; wr = true; break;   // U_DW
-            }
-            if (needs_sync(ad, wr) && ppu_calls < 3 * (cur + 1)) { want = 3 * (cur + 1); continue; }
-            uint8_t v = 0;
-            if (wr) write(ad, I.wv);
-            else v = read(ad);
-            if (u == U_OP) {
-                I.op = v;
-                pc++;
-                decode(I);
-            } else {
-                consume(I, u, v);
-            }
-            u = advance(I);
+            if (!instruction(j, tgt, in_prg && pc <= 0xfffd, op0, q1, q2)) want = tgt;
         }
         // rebase the frame-relative counters on the new frame start
         exec_at -= FRAME_ITERS;
