@@ -104,12 +104,13 @@ struct LaneCtx {
     Cart cart;
     const uint8_t* lut;
     uint32_t* sp;     // this lane's sprite line buffer (stride LDS_LANES words)
-    uint32_t* gp;     // this lane's gray palette, then its tile row (stride LDS_LANES words)
+    uint32_t* gp;     // this lane's gray palette, tile row and OAM (stride LDS_LANES words)
 };
 
 __device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* mem, uint32_t np) {
     c.mem = mem; c.np = np; c.cart = x.cart; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
     c.lds_bg = x.gp + LDS_GP_WORDS * LDS_LANES; c.bg_key = -1;
+    c.lds_oam = x.gp + (LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES;
     c.bad_ops = 0; c.instructions = 0;
     c.pend_line = -1; c.sp_line = -1; c.pal_dirty = true;
 }

@@ -35,39 +35,57 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
     __shared__ uint8_t s_lut[256];                                  \
     __shared__ uint32_t s_dec[256];                                 \
     __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
-    __shared__ uint32_t s_gp[(LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES];
+    __shared__ uint32_t s_gp[LDS_GP_REGION * LDS_LANES];
+
+// Env slot of this thread within its block (0 .. LDS_LANES-1), or -1 for a lane that carries no env.
+__device__ __forceinline__ int lane_slot() {
+    const int lane = threadIdx.x & 63;
+    return lane < ENVS_PER_WAVE ? (int)(threadIdx.x >> 6) * ENVS_PER_WAVE + lane : -1;
+}
 
 __device__ __forceinline__ LaneCtx lane_ctx(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_lut,
-                                            const uint32_t* s_dec, uint32_t* s_sp, uint32_t* s_gp) {
-    return LaneCtx{make_cart(R, s_rom, s_dec), s_lut, s_sp + threadIdx.x, s_gp + threadIdx.x};
+                                            const uint32_t* s_dec, uint32_t* s_sp, uint32_t* s_gp, int slot) {
+    return LaneCtx{make_cart(R, s_rom, s_dec), s_lut, s_sp + slot, s_gp + slot};
 }
 
-__global__ void __launch_bounds__(64) k_boot(BootArgs A) {
+constexpr int EMU_THREADS = 64 * WAVES_PER_BLOCK;
+// blocks of an emulator kernel over `count` envs
+static inline dim3 emu_grid(int count) { return dim3((unsigned)((count + LDS_LANES - 1) / LDS_LANES)); }
+
+__global__ void __launch_bounds__(EMU_THREADS) k_boot(BootArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
-    const int l = blockIdx.x * blockDim.x + threadIdx.x;
-    if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), l);
+    const int slot = lane_slot();
+    if (slot < 0) return;
+    const int l = (int)(blockIdx.x * LDS_LANES + slot);
+    if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), l);
 }
 
-__global__ void __launch_bounds__(64) k_cache(CacheArgs A) {
+__global__ void __launch_bounds__(EMU_THREADS) k_cache(CacheArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
-    const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), ci);
+    const int slot = lane_slot();
+    if (slot < 0) return;
+    const int ci = (int)(blockIdx.x * LDS_LANES + slot);
+    if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), ci);
 }
 
-__global__ void __launch_bounds__(64) k_step(StepArgs A) {
+__global__ void __launch_bounds__(EMU_THREADS) k_step(StepArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
-    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), e);
+    const int slot = lane_slot();
+    if (slot < 0) return;
+    const uint32_t e = (uint32_t)(blockIdx.x * LDS_LANES + slot);
+    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }
 
-__global__ void __launch_bounds__(64) k_raw(RawArgs A) {
+__global__ void __launch_bounds__(EMU_THREADS) k_raw(RawArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
-    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp), e);
+    const int slot = lane_slot();
+    if (slot < 0) return;
+    const uint32_t e = (uint32_t)(blockIdx.x * LDS_LANES + slot);
+    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }
 
 __global__ void __launch_bounds__(64) k_reset(ResetArgs A) {
@@ -380,14 +398,14 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     // boot every level, build the reset cache
     BootArgs ba{h->R, h->nl, h->nlp, d_levels, h->boot_mem, h->boot_sc, h->boot_gray, h->x0, h->t0, d_err};
-    hipLaunchKernelGGL(k_boot, dim3((h->nl + 63) / 64), dim3(64), 0, 0, ba);
+    hipLaunchKernelGGL(k_boot, emu_grid(h->nl), dim3(EMU_THREADS), 0, 0, ba);
     if (!ok(hipGetLastError(), "k_boot launch")) return fail();
     SmallObsArgs so{h->boot_gray, h->nlp, nullptr, nullptr, 1, h->boot_obs, h->nl, h->T};
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nl), dim3(256), 0, 0, so);
     CacheArgs ca{h->R, h->cfg, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
                  h->cmem, h->csc, h->cgray, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
                  h->cframes, h->cinstr, h->cbad};
-    hipLaunchKernelGGL(k_cache, dim3((h->nc + 63) / 64), dim3(64), 0, 0, ca);
+    hipLaunchKernelGGL(k_cache, emu_grid(h->nc), dim3(EMU_THREADS), 0, 0, ca);
     if (!ok(hipGetLastError(), "k_cache launch")) return fail();
     SmallObsArgs co{h->cgray, h->ncp, h->cboot, h->boot_obs, h->nk, h->cobs, h->nc, h->T};
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nc), dim3(256), 0, 0, co);
@@ -437,7 +455,7 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     if (mark(h, s, 0)) return -1;
     StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->ev, h->gray, d_actions,
                 h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len};
-    hipLaunchKernelGGL(k_step, dim3(h->np / 64), dim3(64), 0, s, sa);
+    hipLaunchKernelGGL(k_step, emu_grid(h->n), dim3(EMU_THREADS), 0, s, sa);
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
     ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
@@ -563,14 +581,14 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     h->R.nt_bits = 0;
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, 1};
-    hipLaunchKernelGGL(k_raw, dim3(h->np / 64), dim3(64), 0, 0, ra);
+    hipLaunchKernelGGL(k_raw, emu_grid(h->n), dim3(EMU_THREADS), 0, 0, ra);
     if (!ok(hipDeviceSynchronize(), "raw power-on")) { delete h; return nullptr; }
     return h;
 }
 int mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream) {
     if (!h || !d_buttons) return -1;
     RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, d_buttons, render, h->bad, h->instr, 0};
-    hipLaunchKernelGGL(k_raw, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, ra);
+    hipLaunchKernelGGL(k_raw, emu_grid(h->n), dim3(EMU_THREADS), 0, (hipStream_t)stream, ra);
     CK(hipGetLastError());
     return 0;
 }

@@ -18,10 +18,18 @@
 namespace mh {
 
 constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
-constexpr int LDS_LANES = 64;                      // lanes sharing one block's per-lane LDS buffers
+// Emulator launch shape: a 64-lane wave carries ENVS_PER_WAVE envs (its other lanes idle) and a block holds
+// WAVES_PER_BLOCK waves sharing one LDS copy of the cartridge. 32768 envs in full waves are 512 waves, which
+// leave half of the 1024 SIMDs of the chip empty; half-full waves put a wave on every SIMD and halve the lanes
+// whose divergent paths one wave has to walk.
+constexpr int ENVS_PER_WAVE = 32;
+constexpr int WAVES_PER_BLOCK = 4;
+constexpr int LDS_LANES = ENVS_PER_WAVE * WAVES_PER_BLOCK;  // env slots sharing one block's per-lane LDS buffers
 constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
 constexpr int LDS_BG_WORDS = 18;                   // words per lane: background tile row (33 tiles + 33 attributes)
 constexpr int LDS_BG_ATTR = 36;                    // byte offset of the attributes in the tile row
+constexpr int LDS_OAM_WORDS = 64;                  // words per lane: OAM (sprite i = word i: y, tile, attr, x)
+constexpr int LDS_GP_REGION = LDS_GP_WORDS + LDS_BG_WORDS + LDS_OAM_WORDS;   // palette, tile row, OAM
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
 constexpr int LINE_END = 341;
 constexpr int GRAY_PIX = 256 * 240;
@@ -204,13 +212,23 @@ struct Console {
     uint32_t* lds_sp;        // per-lane sprite line buffer: word (x / 4) of this lane at lds_sp[(x / 4) * LDS_LANES]
     uint32_t* lds_gp;        // per-lane gray palette: word (i / 4) at lds_gp[(i / 4) * LDS_LANES]
     uint32_t* lds_bg;        // per-lane background tile row (same word stride), valid for v's bits 0-11 == bg_key
+    uint32_t* lds_oam;       // per-lane OAM (same word stride): the live copy between load()/power_on() and store()
     int32_t bg_key;          // line-start v & 0xfff the tile row holds (-1: none)
 
     // ------------------------------------------------------------ interleaved memory
     __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mem[(size_t)__umul24(row, np)]; }
     __device__ __forceinline__ void st(uint32_t row, uint8_t val) { mem[(size_t)__umul24(row, np)] = val; }
     __device__ __forceinline__ uint8_t ram(uint32_t a) const { return ld(ROW_RAM + (a & 0x7ff)); }
-    __device__ __forceinline__ uint8_t oam(uint32_t i) const { return ld(ROW_OAM + (i & 0xff)); }
+    __device__ __forceinline__ uint8_t oam(uint32_t i) const {
+        i &= 0xff;
+        return ((const uint8_t*)lds_oam)[(i >> 2) * LDS_LANES * 4 + (i & 3)];
+    }
+    __device__ __forceinline__ void set_oam(uint32_t i, uint8_t val) {
+        i &= 0xff;
+        ((uint8_t*)lds_oam)[(i >> 2) * LDS_LANES * 4 + (i & 3)] = val;
+    }
+    // sprite k's four OAM bytes: y | tile << 8 | attr << 16 | x << 24
+    __device__ __forceinline__ uint32_t oam_sprite(int k) const { return lds_oam[k * LDS_LANES]; }
     __device__ __forceinline__ uint8_t pal(uint32_t i) const { return ld(ROW_PAL + (i & 0x1f)); }
     __device__ __forceinline__ uint8_t vram(uint32_t i) const { return ld(ROW_VRAM + (i & 0x7ff)); }
     __device__ __forceinline__ uint8_t sl(int k) const {
@@ -244,10 +262,19 @@ struct Console {
         pcyc = (int32_t)w(S_PCYC); scanline = (int32_t)w(S_SCANLINE);
         v = (uint16_t)w(S_V); t = (uint16_t)w(S_T); inc = (uint16_t)w(S_INC);
         pend_line = -1; sp_line = -1; pal_dirty = true; bg_key = -1;
+        for (int k = 0; k < LDS_OAM_WORDS; k++) {
+            const uint32_t r = ROW_OAM + 4 * k;
+            lds_oam[k * LDS_LANES] = (uint32_t)ld(r) | (uint32_t)ld(r + 1) << 8 | (uint32_t)ld(r + 2) << 16 |
+                                     (uint32_t)ld(r + 3) << 24;
+        }
         nmi_threshold();
     }
     __device__ void store(uint32_t* sc, uint32_t e) {
         materialize_sprites();
+        for (int k = 0; k < LDS_OAM_WORDS; k++) {
+            const uint32_t w = oam_sprite(k), r = ROW_OAM + 4 * k;
+            st(r, (uint8_t)w); st(r + 1, (uint8_t)(w >> 8)); st(r + 2, (uint8_t)(w >> 16)); st(r + 3, (uint8_t)(w >> 24));
+        }
         auto w = [&](int k, uint32_t val) { sc[(size_t)k * np + e] = val; };
         w(S_ITER_LO, iter_lo); w(S_ITER_HI, iter_hi); w(S_EXEC_REL, (uint32_t)exec_at);
         w(S_PC, pc); w(S_SP, sp); w(S_A, a); w(S_X, x); w(S_Y, y); w(S_P, p); w(S_ZERO_SKIP, zero_skip);
@@ -276,6 +303,7 @@ struct Console {
         first_write = 1; bg_page = 0; spr_page = 0; v = 0; pcyc = 0; scanline = 0;
         oam_addr = 0; fine_x = 0; t = 0; inc = 1; pstate = ST_PRE; nsl = 0; sl_lo = sl_hi = 0;
         pend_line = -1; sp_line = -1; pal_dirty = true; bg_key = -1;
+        for (int k = 0; k < LDS_OAM_WORDS; k++) lds_oam[k * LDS_LANES] = 0;
         nmi_threshold();
     }
 
@@ -311,7 +339,7 @@ struct Console {
                 case 0x2000: ctrl_write(val); sp_line = -1; break;
                 case 0x2001: mask_write(val); break;
                 case 0x2003: oam_addr = val; break;
-                case 0x2004: st(ROW_OAM + oam_addr, val); oam_addr++; sp_line = -1; break;
+                case 0x2004: set_oam(oam_addr, val); oam_addr++; sp_line = -1; break;
                 case 0x2005: scroll_write(val); break;
                 case 0x2006: addr_write(val); break;
                 case 0x2007: data_write(val); sp_line = -1; break;
@@ -323,8 +351,19 @@ struct Console {
             materialize_sprites();
             skip += 513 + (int)((iter_lo + (uint32_t)cur + 1u) & 1u);
             const uint16_t src = (uint16_t)(val << 8);
-            if (src < 0x2000)
-                for (int i = 0; i < 256; i++) st(ROW_OAM + ((oam_addr + i) & 0xff), ram(src + i));
+            if (src < 0x2000) {
+                if (!(oam_addr & 3)) {
+                    // word-aligned: sprite words straight from four RAM bytes each
+                    for (int k = 0; k < LDS_OAM_WORDS; k++) {
+                        const uint32_t a0 = src + 4 * k;
+                        lds_oam[((k + (oam_addr >> 2)) & 63) * LDS_LANES] =
+                            (uint32_t)ram(a0) | (uint32_t)ram(a0 + 1) << 8 | (uint32_t)ram(a0 + 2) << 16 |
+                            (uint32_t)ram(a0 + 3) << 24;
+                    }
+                } else {
+                    for (int i = 0; i < 256; i++) set_oam(oam_addr + i, ram(src + i));
+                }
+            }
             sp_line = -1;
             return;
         }
@@ -430,12 +469,28 @@ struct Console {
     // so the late evaluation gives the same list.
     __device__ void materialize_sprites() {
         if (pend_line < 0) return;
-        nsl = 0;
-        int h = long_spr ? 16 : 8;
-        for (int i = oam_addr / 4; i < 64 && nsl < 8; i++) {
-            int d = pend_line - (int)oam(i * 4);
-            if (d >= 0 && d < h) { set_sl(nsl, (uint8_t)i); nsl++; }
+        // in-range sprites as a 64-bit mask (bit i: pend_line - y_i in [0, h)), from index oam_addr / 4 on;
+        // the list is its first (at most 8) set bits, entries past the count keep their old values
+        const uint32_t h = long_spr ? 16u : 8u;
+        uint32_t mlo = 0, mhi = 0;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            mlo |= ((uint32_t)(pend_line - (int)(oam_sprite(i) & 0xffu)) < h ? 1u : 0u) << i;
+            mhi |= ((uint32_t)(pend_line - (int)(oam_sprite(32 + i) & 0xffu)) < h ? 1u : 0u) << i;
         }
+        const int i0 = oam_addr >> 2;
+        if (i0 < 32) mlo &= ~0u << i0;
+        else { mlo = 0; mhi &= ~0u << (i0 - 32); }
+        int n = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const bool has = (mlo | mhi) != 0;
+            const uint32_t i = mlo ? (uint32_t)__builtin_ctz(mlo) : 32u + (uint32_t)__builtin_ctz(mhi | 0x80000000u);
+            if (has) set_sl(k, (uint8_t)i);
+            n += has;
+            if (mlo) mlo &= mlo - 1; else mhi &= mhi - 1;
+        }
+        nsl = (uint8_t)n;
         pend_line = -1;
     }
     // "nsl > 0 && sl[0] == 0" without materializing: sprite 0 heads the list exactly when the
@@ -443,7 +498,7 @@ struct Console {
     __device__ __forceinline__ bool sprite0_first() const {
         if (pend_line < 0) return nsl > 0 && sl(0) == 0;
         if (oam_addr >= 4) return false;
-        int d = pend_line - (int)oam(0);
+        int d = pend_line - (int)(oam_sprite(0) & 0xffu);
         return d >= 0 && d < (long_spr ? 16 : 8);
     }
     __device__ uint8_t bg_colour(int px, uint8_t* pattern) const {
@@ -458,8 +513,9 @@ struct Console {
     }
     // sprite i's 2-bit pattern at (px, py), with C++ int semantics for stale lists (nes_core.hpp:369-391)
     __device__ uint8_t sprite_pattern(int i, int px, int py) const {
-        uint8_t sx = oam(i * 4 + 3);
-        uint8_t sy = (uint8_t)(oam(i * 4) + 1), tile = oam(i * 4 + 1), attr = oam(i * 4 + 2);
+        const uint32_t ow = oam_sprite(i);
+        uint8_t sx = (uint8_t)(ow >> 24);
+        uint8_t sy = (uint8_t)((ow & 0xffu) + 1), tile = (uint8_t)(ow >> 8), attr = (uint8_t)(ow >> 16);
         int h = long_spr ? 16 : 8;
         int xs = (px - sx) % 8, yo = (py - sy) % h;
         if (!(attr & 0x40)) xs ^= 7;
@@ -481,7 +537,7 @@ struct Console {
     __device__ __forceinline__ void dots_hit_scroll(int x0, int x1) {
         if (!show_bg) return;
         if (!s0hit && show_spr && sprite0_first()) {
-            int sx = oam(3);
+            int sx = (int)(oam_sprite(0) >> 24);
             int lo = x0 > sx ? x0 : sx;
             int hi = x1 < sx + 8 ? x1 : sx + 8;
             if (hide_edge_spr && lo < 8) lo = 8;
@@ -506,6 +562,13 @@ struct Console {
         return (hi - r + 7) / 8 - (lo - r + 7) / 8;
     }
 
+    // an optimization barrier: the value is materialized in a register here
+    __device__ __forceinline__ static void in_register(uint32_t& x) { asm volatile("" : "+v"(x)); }
+    // bytes of the 8-byte value hi:lo picked by the selector bytes of sel (each 0..7)
+    __device__ __forceinline__ static uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+        return __builtin_amdgcn_perm(hi, lo, sel);
+    }
+
     // ---- per-lane LDS buffers of the renderer
     __device__ __forceinline__ uint8_t lds_byte(const uint32_t* base, int i) const {
         return (uint8_t)(base[(i >> 2) * LDS_LANES] >> (8 * (i & 3)));
@@ -519,15 +582,18 @@ struct Console {
         }
         pal_dirty = false;
     }
-    // First opaque listed sprite per x of line py (nes_core.hpp:427-441): bits 0-4 palette address
-    // (0x10 | attr << 2 | pattern), bit 5 in front of the background, bit 6 sprite 0. The pattern row
-    // of each listed sprite is fetched once, with the addressing of sprite_pattern().
+    // First opaque listed sprite per x of line py (nes_core.hpp:427-441), one byte per x: bits 0-3 the
+    // sprite palette entry (attr << 2 | pattern, palette address 0x10 + it), bit 6 in front of the
+    // background, bit 7 set (a sprite pixel is here; 0: none). The pattern row of each listed sprite is
+    // fetched once, with the addressing of sprite_pattern().
     __device__ void build_sprite_line(int py) {
         for (int w = 0; w < LDS_SP_WORDS; w++) lds_sp[w * LDS_LANES] = 0;
         const int h = long_spr ? 16 : 8;
         for (int k = 0; k < nsl; k++) {
             const int i = sl(k);
-            const uint8_t sx = oam(i * 4 + 3), sy = (uint8_t)(oam(i * 4) + 1), tile = oam(i * 4 + 1), attr = oam(i * 4 + 2);
+            const uint32_t ow = oam_sprite(i);
+            const uint8_t sx = (uint8_t)(ow >> 24), sy = (uint8_t)((ow & 0xffu) + 1), tile = (uint8_t)(ow >> 8),
+                          attr = (uint8_t)(ow >> 16);
             int yo = (py - sy) % h;
             if (attr & 0x80) yo ^= (h - 1);
             uint16_t ad;
@@ -540,7 +606,7 @@ struct Console {
                 ad |= (tile & 1) << 12;
             }
             const uint8_t lo = vbus_read(ad), hi = vbus_read((uint16_t)(ad + 8));
-            const uint32_t tag = 0x10u | ((attr & 3u) << 2) | (attr & 0x20 ? 0u : 0x20u) | (i == 0 ? 0x40u : 0u);
+            const uint32_t tag = 0x80u | ((attr & 3u) << 2) | (attr & 0x20 ? 0u : 0x40u);
             const int xe = sx + 8 < 256 ? sx + 8 : 256;
             for (int px = sx; px < xe; px++) {
                 int xs = px - sx;
@@ -579,13 +645,24 @@ struct Console {
             lds_bg[(9 + w) * LDS_LANES] = aw;
         }
     }
-    // pattern planes and palette bits 2-3 of tile k of the cached row, for fine y `fy`
-    __device__ __forceinline__ void bg_tile(int k, int fy, uint32_t& lo, uint32_t& hi, uint32_t& at) const {
-        const uint32_t tile = lds_byte(lds_bg, k);
-        const uint16_t pa = (uint16_t)(((tile * 16) + fy) | (bg_page << 12));
+    // tile k of the cached row: index | attribute << 8
+    __device__ __forceinline__ uint32_t bg_tile_of(int k) const {
+        // byte loads: the values need no unpacking, so nothing waits for them before their use
+        const uint8_t* row = (const uint8_t*)lds_bg;
+        const uint32_t tile = row[(k >> 2) * LDS_LANES * 4 + (k & 3)];
+        const uint32_t at = row[((LDS_BG_ATTR + k) >> 2) * LDS_LANES * 4 + ((LDS_BG_ATTR + k) & 3)];
+        return tile | at << 8;
+    }
+    // Pattern planes of row fy of tile ta (bg_tile_of) and its gray table: byte p is the gray value of
+    // background pattern p (p = 0: the universal background, palette address 0; else palette address
+    // 4 at + p). pal[w]: gray values of palette addresses 4w .. 4w+3.
+    __device__ __forceinline__ void bg_planes(uint32_t ta, int fy, const uint32_t (&pal)[4], uint32_t& lo, uint32_t& hi,
+                                              uint32_t& gt) const {
+        const uint16_t pa = (uint16_t)((((ta & 0xffu) * 16) + fy) | (bg_page << 12));
         lo = cart.chr[pa];
         hi = cart.chr[pa + 8];
-        at = lds_byte(lds_bg, LDS_BG_ATTR + k);
+        const uint32_t w01 = (ta & 0x100u) ? pal[1] : pal[0], w23 = (ta & 0x100u) ? pal[3] : pal[2];
+        gt = (((ta & 0x200u) ? w23 : w01) & 0xffffff00u) | (pal[0] & 0xffu);
     }
 
     // Pixels of visible dots [x0, x1): gray values into the frame buffer (nes_core.hpp:467-513), with
@@ -593,8 +670,12 @@ struct Console {
     // of 8, so every lane of a wave runs the same code whatever its fine scroll: a group spans two
     // background tiles, kept as a 16-bit window per pattern plane (a PPU's shift registers), and the
     // tile after them is fetched one group ahead from the LDS tile row. Sprites come from the LDS line
-    // buffer, where the first opaque listed sprite of each x sits; four gray pixels are stored as one
-    // word.
+    // buffer, where the first opaque listed sprite of each x sits.
+    //
+    // Four pixels are one 32-bit word, a byte each, and are computed together without branches: the
+    // pattern bits of the four pixels are spread to the four bytes by a multiply, the background gray
+    // value is a byte permute of the two tiles' gray tables, a sprite pixel's gray value is a byte
+    // permute of the sprite palette's 16 gray values, and priority is a per-byte mask.
     __device__ __forceinline__ void dots_drawn(int x0, int x1) {
         const int py = scanline;
         materialize_sprites();
@@ -612,38 +693,86 @@ struct Console {
             v0 = (uint16_t)((v0 & ~0x1f) | c0);
             if ((int32_t)(v0 & 0x0fff) != bg_key) { fill_bg_row(v0); bg_key = v0 & 0x0fff; }
         }
-        uint32_t alo = 0, ahi = 0, aat = 0, blo = 0, bhi = 0, bat = 0;
-        if (show_bg) { bg_tile(g0, fy, alo, ahi, aat); bg_tile(g0 + 1, fy, blo, bhi, bat); }
-        uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g0) * np;   // word of pixels xq..xq+3
+        // gray values of the background palettes (addresses 0..15) and the sprite palettes (0x10 + 0..15)
+        uint32_t bp0 = lds_gp[0], bp1 = lds_gp[LDS_LANES], bp2 = lds_gp[2 * LDS_LANES], bp3 = lds_gp[3 * LDS_LANES];
+        // keep them in registers: a select of these loads must not become a load from a selected address
+        in_register(bp0); in_register(bp1); in_register(bp2); in_register(bp3);
+        const uint32_t ubg = bp0 & 0xffu;                // palette address 0: the universal background
+        uint32_t sp0 = 0, sp1 = 0, sp2 = 0, sp3 = 0;
+        if (spr) {
+            sp0 = lds_gp[4 * LDS_LANES]; sp1 = lds_gp[5 * LDS_LANES];
+            sp2 = lds_gp[6 * LDS_LANES]; sp3 = lds_gp[7 * LDS_LANES];
+        }
+        const bool any_spr = __any(spr);
+        const uint32_t bgpal[4] = {bp0, bp1, bp2, bp3};
+        // pixel bb of a group takes the second tile's attribute when f + bb >= 8: bytes bb >= 8 - f
+        const uint64_t second = f ? (~0ull << (8 * (8 - f))) : 0ull;
+        const uint32_t tsel0 = (uint32_t)second & 0x04040404u, tsel1 = (uint32_t)(second >> 32) & 0x04040404u;
+        // Software pipeline over the groups: group g needs tiles g and g + 1 (a, b). Iteration g fetches
+        // the planes of tile g + 2, the index of tile g + 3 and the sprite bytes of group g + 1, which
+        // are used one iteration later, so no LDS round trip sits between two groups.
+        uint32_t alo = 0, ahi = 0, agt = ubg, blo = 0, bhi = 0, bgt = ubg, nxt = 0;
+        if (show_bg) {
+            bg_planes(bg_tile_of(g0), fy, bgpal, alo, ahi, agt);
+            bg_planes(bg_tile_of(g0 + 1), fy, bgpal, blo, bhi, bgt);
+            if (g0 + 1 < g1) nxt = bg_tile_of(g0 + 2);
+        }
+        uint32_t s0 = 0, s1 = 0;                         // sprite bytes of the group's two words
+        if (spr) { s0 = lds_sp[(2 * g0) * LDS_LANES]; s1 = lds_sp[(2 * g0 + 1) * LDS_LANES]; }
+        uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g0) * np;   // word of pixels 8g .. 8g+3
         for (int g = g0; g < g1; g++) {
-            uint32_t clo = 0, chi = 0, cat = 0;
-            if (show_bg && g + 1 < g1) bg_tile(g + 2, fy, clo, chi, cat);
-            // pixel 8g + b is bit 15 - b of the window, after the fine-scroll shift
-            const uint32_t wlo = ((alo << 8) | blo) << f, whi = ((ahi << 8) | bhi) << f;
-            for (int q = 0; q < 2; q++) {
-                const int xq = 8 * g + 4 * q;
-                const uint32_t spw = spr ? lds_sp[(xq >> 2) * LDS_LANES] : 0u;
-                uint32_t word = 0, keep = 0;
-                for (int b = 0; b < 4; b++) {
-                    const int bb = 4 * q + b, px = xq + b;
-                    const bool in = px >= x0 && px < x1;
-                    uint32_t bgop = ((wlo >> (15 - bb)) & 1u) | (((whi >> (15 - bb)) & 1u) << 1);
-                    if (hide_edge_bg && px < 8) bgop = 0;
-                    const uint32_t at = f + bb < 8 ? aat : bat;
-                    uint32_t pa = bgop ? (bgop | (at << 2)) : 0u;
-                    if (spr && !(hide_edge_spr && px < 8)) {
-                        const uint32_t c = (spw >> (8 * b)) & 0xffu;
-                        if (c && (!bgop || (c & 0x20))) pa = c & 0x1f;
-                    }
-                    word |= (uint32_t)lds_byte(lds_gp, (int)pa) << (8 * b);
-                    if (!in) keep |= 0xffu << (8 * b);
-                }
-                if (!keep) *wp = word;
-                else if (keep != 0xffffffffu) *wp = (*wp & keep) | (word & ~keep);
-                wp += np;
+            uint32_t clo = 0, chi = 0, cgt = ubg, nn = 0;
+            if (show_bg && g + 1 < g1) {
+                bg_planes(nxt, fy, bgpal, clo, chi, cgt);
+                if (g + 2 < g1) nn = bg_tile_of(g + 3);
             }
-            alo = blo; ahi = bhi; aat = bat;
-            blo = clo; bhi = chi; bat = cat;
+            uint32_t t0 = 0, t1 = 0;
+            if (spr && g + 1 < g1) { t0 = lds_sp[(2 * g + 2) * LDS_LANES]; t1 = lds_sp[(2 * g + 3) * LDS_LANES]; }
+            // pixel 8g + bb is bit 15 - bb of the window after the fine-scroll shift; reversed: bit 16 + bb
+            const uint32_t rlo = __builtin_bitreverse32(((alo << 8) | blo) << f);
+            const uint32_t rhi = __builtin_bitreverse32(((ahi << 8) | bhi) << f);
+            const uint32_t keep_bg = (g == 0 && hide_edge_bg) ? 0u : ~0u;     // pixels 0-7 may hide either layer
+            const uint32_t keep_sp = (g == 0 && hide_edge_spr) ? 0u : ~0u;
+            uint32_t out[2];
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                // background pattern of the four pixels, one per byte (0..3)
+                const uint32_t nlo = (rlo >> (16 + 4 * q)) & 0xfu, nhi = (rhi >> (16 + 4 * q)) & 0xfu;
+                const uint32_t bgp = (((__umul24(nlo, 0x204081u) & 0x01010101u) |
+                                       ((__umul24(nhi, 0x204081u) & 0x01010101u) << 1))) & keep_bg;
+                uint32_t word = byte_perm(bgt, agt, bgp | (q ? tsel1 : tsel0));
+                if (any_spr) {
+                    const uint32_t c = q ? s1 : s0;
+                    const uint32_t opaque = (bgp + 0x7f7f7f7fu) & 0x80808080u;       // background pattern != 0
+                    const uint32_t take = c & (~opaque | (c << 1)) & 0x80808080u & keep_sp;
+                    const uint32_t tmask = take | (take - (take >> 7));
+                    const uint32_t sel = c & 0x07070707u;
+                    const uint32_t hi8 = (c << 4) & 0x80808080u;                    // entry 8..15
+                    const uint32_t hmask = hi8 | (hi8 - (hi8 >> 7));
+                    const uint32_t sg = (byte_perm(sp3, sp2, sel) & hmask) | (byte_perm(sp1, sp0, sel) & ~hmask);
+                    word = (sg & tmask) | (word & ~tmask);
+                }
+                out[q] = word;
+            }
+            const int xg = 8 * g;
+            if (xg >= x0 && xg + 8 <= x1) { wp[0] = out[0]; wp[np] = out[1]; }
+            else {
+                // a partial group: only the pixels in [x0, x1)
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const int xq = xg + 4 * q;
+                    const int lo = x0 > xq ? x0 - xq : 0, hi = x1 < xq + 4 ? x1 - xq : 4;
+                    if (lo < hi) {
+                        const uint32_t in = (uint32_t)((((1ull << (8 * hi)) - 1) >> (8 * lo)) << (8 * lo));
+                        uint32_t* w = wp + q * np;
+                        *w = (*w & ~in) | (out[q] & in);
+                    }
+                }
+            }
+            wp += 2 * np;
+            alo = blo; ahi = bhi; agt = bgt;
+            blo = clo; bhi = chi; bgt = cgt;
+            nxt = nn; s0 = t0; s1 = t1;
         }
     }
 
@@ -890,7 +1019,7 @@ struct Console {
             // frame); with OAM, oam_addr and sprite size fixed (the loop writes nothing) sprite 0 can
             // head one only for y0 <= m < y0 + h.
             if (sprite0_first() && pstate == ST_RENDER) return false;
-            const int y0 = oam(0), h = long_spr ? 16 : 8;
+            const int y0 = (int)(oam_sprite(0) & 0xffu), h = long_spr ? 16 : 8;
             const int m = pstate == ST_RENDER && scanline > y0 ? scanline : y0;
             if (m <= 239 && m < y0 + h) limit = ppu_calls + calls_until(m + 1, 1) - 2;
             else if (y0 <= 238) limit = ppu_calls + calls_until(y0 + 1, 1) - 2;   // next frame
