@@ -117,7 +117,7 @@ struct Cfg {
 
 // Memory region of consoles with the same layout as the live state (reset cache, boot states).
 struct Region {
-    uint8_t* mem;       // row-major [row * np + idx]
+    uint8_t* mem;       // row-major [row * np + idx], VRAM word-interleaved (vram_word_offset)
     uint32_t* sc;       // [word * np + idx]
     uint32_t np;
     uint32_t idx;
@@ -125,7 +125,10 @@ struct Region {
 
 __device__ inline void copy_console(const Region& dst, const Region& src) {
     for (uint32_t r = 0; r < MEM_ROWS; r++)
-        dst.mem[(size_t)r * dst.np + dst.idx] = src.mem[(size_t)r * src.np + src.idx];
+        if (r < ROW_VRAM || r >= ROW_VRAM + 2048) dst.mem[(size_t)r * dst.np + dst.idx] = src.mem[(size_t)r * src.np + src.idx];
+    for (uint32_t w = 0; w < 512; w++)
+        *(uint32_t*)(dst.mem + vram_word_offset(dst.np, dst.idx, w)) =
+            *(const uint32_t*)(src.mem + vram_word_offset(src.np, src.idx, w));
     for (int w = 0; w < S_COUNT; w++) dst.sc[(size_t)w * dst.np + dst.idx] = src.sc[(size_t)w * src.np + src.idx];
 }
 

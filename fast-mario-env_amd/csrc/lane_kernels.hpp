@@ -107,8 +107,10 @@ struct LaneCtx {
     uint32_t* gp;     // this lane's gray palette, tile row and OAM (stride LDS_LANES words)
 };
 
-__device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* mem, uint32_t np) {
-    c.mem = mem; c.np = np; c.cart = x.cart; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
+// console e of the memory block `mem` (np consoles)
+__device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* mem, uint32_t np, uint32_t e) {
+    c.mem = mem + e; c.vmem = mem + vram_word_offset(np, e, 0); c.np = np;
+    c.cart = x.cart; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
     c.lds_bg = x.gp + LDS_GP_WORDS * LDS_LANES; c.bg_key = -1;
     c.lds_oam = x.gp + (LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES;
     c.bad_ops = 0; c.instructions = 0;
@@ -204,7 +206,7 @@ __device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e
 // Power-on and title sequence with the target level written into RAM (fastmario.cpp:414-445).
 __device__ inline void boot_lane(const BootArgs& A, const LaneCtx& x, int l) {
     Console c;
-    attach(c, x, A.mem + l, A.nlp);
+    attach(c, x, A.mem, A.nlp, (uint32_t)l);
     c.gray = A.gray + gray_lane_offset(l); c.render = true;
     c.power_on();
     auto fr = [&](uint8_t b) { c.joy_buttons0 = b; c.frame(); };
@@ -239,7 +241,7 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     Region live{A.mem, A.sc, A.ncp, (uint32_t)ci};
     copy_console(live, boot);
     Console c;
-    attach(c, x, A.mem + ci, A.ncp);
+    attach(c, x, A.mem, A.ncp, (uint32_t)ci);
     c.load(A.sc, ci);
     EnvRegs ev{};
     ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
@@ -264,7 +266,7 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
 // One agent step of env e (fastmario.cpp:403-411 + 336-374).
 __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e) {
     Console c;
-    attach(c, x, A.mem + e, A.np);
+    attach(c, x, A.mem, A.np, e);
     c.load(A.sc, e);
     EnvRegs ev;
     load_env(ev, A.ev, A.np, e);
@@ -324,7 +326,7 @@ __device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
 // One nes-py frame of raw console e (fastmario.cpp:656-661); power_on != 0 boots it instead.
 __device__ inline void raw_lane(const RawArgs& A, const LaneCtx& x, uint32_t e) {
     Console c;
-    attach(c, x, A.mem + e, A.np);
+    attach(c, x, A.mem, A.np, e);
     c.gray = A.screen + gray_lane_offset(e);
     if (A.power_on) {
         c.power_on();
@@ -358,9 +360,10 @@ __device__ inline void canon_lane(const uint8_t* mem, const uint32_t* sc, uint32
     const uint32_t nsl = w(S_NSL);
     const uint64_t sl = (uint64_t)w(S_SL_LO) | ((uint64_t)w(S_SL_HI) << 32);
     for (uint32_t i = 0; i < 8; i++) o[69 + i] = i < nsl ? (uint8_t)(sl >> (8 * i)) : 0;
-    const uint32_t rows[4][3] = {{80, ROW_OAM, 256}, {336, ROW_PAL, 32}, {368, ROW_VRAM, 2048}, {2416, ROW_RAM, 2048}};
-    for (int k = 0; k < 4; k++)
+    const uint32_t rows[3][3] = {{80, ROW_OAM, 256}, {336, ROW_PAL, 32}, {2416, ROW_RAM, 2048}};
+    for (int k = 0; k < 3; k++)
         for (uint32_t i = 0; i < rows[k][2]; i++) o[rows[k][0] + i] = mem[(size_t)(rows[k][1] + i) * np + e];
+    for (uint32_t i = 0; i < 2048; i++) o[368 + i] = mem[vram_word_offset(np, e, i >> 2) + (i & 3)];
 }
 
 }  // namespace mh

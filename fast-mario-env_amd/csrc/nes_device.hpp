@@ -26,13 +26,19 @@ constexpr int ENVS_PER_WAVE = 32;
 constexpr int WAVES_PER_BLOCK = 4;
 constexpr int LDS_LANES = ENVS_PER_WAVE * WAVES_PER_BLOCK;  // env slots sharing one block's per-lane LDS buffers
 constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
-constexpr int LDS_BG_WORDS = 18;                   // words per lane: background tile row (33 tiles + 33 attributes)
-constexpr int LDS_BG_ATTR = 36;                    // byte offset of the attributes in the tile row
+constexpr int LDS_BG_WORDS = 20;                   // words per lane: two name-table rows (64 tiles) + their attributes
+constexpr int LDS_BG_ATTR = 64;                    // byte offset of the attribute bytes in the tile row
 constexpr int LDS_OAM_WORDS = 64;                  // words per lane: OAM (sprite i = word i: y, tile, attr, x)
 constexpr int LDS_GP_REGION = LDS_GP_WORDS + LDS_BG_WORDS + LDS_OAM_WORDS;   // palette, tile row, OAM
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
 constexpr int LINE_END = 341;
 constexpr int GRAY_PIX = 256 * 240;
+// Byte offset of VRAM word w (bytes 4w .. 4w+3) of console e in a memory block of np consoles. The VRAM
+// span of the block (rows ROW_VRAM .. ROW_VRAM + 2047 of the byte-row layout) holds 32-bit words, word w of
+// console e at index w np + e: one load fetches four consecutive VRAM bytes of a console.
+__device__ __forceinline__ size_t vram_word_offset(uint32_t np, uint32_t e, uint32_t w) {
+    return (size_t)ROW_VRAM * np + ((size_t)w * np + e) * 4;
+}
 enum : uint8_t { FN = 0x01, FV = 0x02, FONE = 0x04, FB = 0x08, FD = 0x10, FI = 0x20, FZ = 0x40, FC = 0x80 };
 enum : uint8_t { ST_PRE = 0, ST_RENDER = 1, ST_POST = 2, ST_VBLANK = 3 };
 
@@ -181,6 +187,7 @@ struct Cart {
 struct Console {
     // ---- memory views
     uint8_t* mem;            // MEM + e (row stride np)
+    uint8_t* vmem;           // this env's VRAM word 0 (word stride 4 np)
     uint32_t np;
     Cart cart;
     uint8_t* gray;           // GRAY slot + 4 e: pixels 4i..4i+3 in the 32-bit word at gray + 4 i np
@@ -211,9 +218,9 @@ struct Console {
     bool pal_dirty;          // the LDS gray palette must be rebuilt
     uint32_t* lds_sp;        // per-lane sprite line buffer: word (x / 4) of this lane at lds_sp[(x / 4) * LDS_LANES]
     uint32_t* lds_gp;        // per-lane gray palette: word (i / 4) at lds_gp[(i / 4) * LDS_LANES]
-    uint32_t* lds_bg;        // per-lane background tile row (same word stride), valid for v's bits 0-11 == bg_key
+    uint32_t* lds_bg;        // per-lane background tile row (same word stride), valid for v's bits 5-11 == bg_key
     uint32_t* lds_oam;       // per-lane OAM (same word stride): the live copy between load()/power_on() and store()
-    int32_t bg_key;          // line-start v & 0xfff the tile row holds (-1: none)
+    int32_t bg_key;          // name table and coarse y (v bits 5-11) of the tile row held (-1: none)
 
     // ------------------------------------------------------------ interleaved memory
     __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mem[(size_t)__umul24(row, np)]; }
@@ -230,7 +237,19 @@ struct Console {
     // sprite k's four OAM bytes: y | tile << 8 | attr << 16 | x << 24
     __device__ __forceinline__ uint32_t oam_sprite(int k) const { return lds_oam[k * LDS_LANES]; }
     __device__ __forceinline__ uint8_t pal(uint32_t i) const { return ld(ROW_PAL + (i & 0x1f)); }
-    __device__ __forceinline__ uint8_t vram(uint32_t i) const { return ld(ROW_VRAM + (i & 0x7ff)); }
+    // VRAM is word-interleaved: byte i of this env is byte i % 4 of 32-bit word i / 4, and word w sits at
+    // vmem + 4 w np (vmem: this env's word 0), so a name-table row is 8 word loads
+    __device__ __forceinline__ uint8_t vram(uint32_t i) const {
+        i &= 0x7ff;
+        return vmem[(size_t)__umul24(i >> 2, 4 * np) + (i & 3)];
+    }
+    __device__ __forceinline__ void set_vram(uint32_t i, uint8_t d) {
+        i &= 0x7ff;
+        vmem[(size_t)__umul24(i >> 2, 4 * np) + (i & 3)] = d;
+    }
+    __device__ __forceinline__ uint32_t vram_word(uint32_t w) const {
+        return *(const uint32_t*)(vmem + (size_t)__umul24(w & 0x1ff, 4 * np));
+    }
     __device__ __forceinline__ uint8_t sl(int k) const {
         return (uint8_t)((k < 4 ? sl_lo >> (8 * k) : sl_hi >> (8 * (k - 4))) & 0xff);
     }
@@ -292,7 +311,9 @@ struct Console {
 
     // power-on: zeroed machine, then CPU and PPU reset (nes_core.hpp:123-147)
     __device__ void power_on() {
-        for (uint32_t r = 0; r < MEM_ROWS; r++) st(r, 0);
+        for (uint32_t r = 0; r < MEM_ROWS; r++)
+            if (r < ROW_VRAM || r >= ROW_VRAM + 2048) st(r, 0);
+        for (uint32_t w = 0; w < 512; w++) *(uint32_t*)(vmem + (size_t)__umul24(w, 4 * np)) = 0;
         iter_lo = iter_hi = 0; exec_at = 0; ppu_calls = 0;
         joy_strobe0 = joy_strobe1 = 1; joy_buttons0 = joy_buttons1 = 0; joy_bits0 = joy_bits1 = 0;
         zero_skip = 0; a = x = y = 0; p = 0x34;
@@ -427,7 +448,7 @@ struct Console {
     }
     __device__ void vbus_write(uint16_t ad, uint8_t d) {
         if (ad < 0x2000) return;
-        if (ad < 0x3eff) { st(ROW_VRAM + nt_row(ad), d); bg_key = -1; }
+        if (ad < 0x3eff) { set_vram(nt_row(ad), d); bg_key = -1; }
         else if (ad < 0x3fff) { st(ROW_PAL + (ad == 0x3f10 ? 0 : (ad & 0x1f)), d); pal_dirty = true; }
     }
     __device__ __forceinline__ uint8_t nametable(uint16_t ad) const {
@@ -620,38 +641,38 @@ struct Console {
         sp_line = py;
     }
 
-    // Background tile row of a line into the per-lane LDS cache: for tiles k = 0..32 from the line-start
-    // address v0 (coarse-x wrap into the neighbouring name table as in coarse_x_add), the tile index
-    // and the 2-bit attribute (nes_core.hpp:467-483). All 66 name-table reads are independent, so
-    // they are in flight together; a tile row serves the 8 scanlines of its coarse y.
+    // Background tiles of a line into the per-lane LDS cache: the 32-tile name-table row at coarse y of
+    // v0's name table A (words 0-7) and of its horizontal neighbour B (words 8-15, where coarse x wraps
+    // to; nes_core.hpp:394-413), and the two attribute rows (words 16-19: bytes 0-7 A, 8-15 B). The row
+    // depends on v0's bits 5-11 only: lines of one coarse y share it whatever their scroll. 20 word
+    // loads, independent of each other.
     __device__ __forceinline__ void fill_bg_row(uint16_t v0) {
+        const uint32_t na = (v0 >> 10) & 3u, cy = (v0 >> 5) & 31u;
+        const uint32_t pa = ((cart.nt_bits >> na) & 1u) << 8, pb = ((cart.nt_bits >> (na ^ 1u)) & 1u) << 8;  // words
+        uint32_t w[LDS_BG_WORDS];
 #pragma unroll
-        for (int w = 0; w < 9; w++) {
-            uint32_t tw = 0, aw = 0;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int k = 4 * w + b;
-                if (k > 32) break;
-                const int tot = (v0 & 0x1f) + k;
-                uint16_t vv = (uint16_t)((v0 & ~0x1f) | (tot & 31));
-                if ((tot >> 5) & 1) vv ^= 0x400;
-                const uint32_t tile = nametable((uint16_t)(0x2000 | (vv & 0x0fff)));
-                const uint16_t aa = (uint16_t)(0x23c0 | (vv & 0x0c00) | ((vv >> 4) & 0x38) | ((vv >> 2) & 7));
-                const int sh = ((vv >> 4) & 4) | (vv & 2);
-                tw |= tile << (8 * b);
-                aw |= ((uint32_t)(nametable(aa) >> sh) & 3u) << (8 * b);
-            }
-            lds_bg[w * LDS_LANES] = tw;
-            lds_bg[(9 + w) * LDS_LANES] = aw;
+        for (int i = 0; i < 8; i++) {
+            w[i] = vram_word(pa + cy * 8 + i);
+            w[8 + i] = vram_word(pb + cy * 8 + i);
         }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            w[16 + i] = vram_word(pa + 0xf0 + (cy >> 2) * 2 + i);
+            w[18 + i] = vram_word(pb + 0xf0 + (cy >> 2) * 2 + i);
+        }
+#pragma unroll
+        for (int i = 0; i < LDS_BG_WORDS; i++) lds_bg[i * LDS_LANES] = w[i];
     }
-    // tile k of the cached row: index | attribute << 8
-    __device__ __forceinline__ uint32_t bg_tile_of(int k) const {
-        // byte loads: the values need no unpacking, so nothing waits for them before their use
+    // Tile k of the line whose row is cached (c0: the line's starting coarse x, cy: its coarse y):
+    // index | attribute << 8. Column c0 + k is in name table A below 32, else in B.
+    __device__ __forceinline__ uint32_t bg_tile_of(int k, uint32_t c0, uint32_t cy) const {
         const uint8_t* row = (const uint8_t*)lds_bg;
-        const uint32_t tile = row[(k >> 2) * LDS_LANES * 4 + (k & 3)];
-        const uint32_t at = row[((LDS_BG_ATTR + k) >> 2) * LDS_LANES * 4 + ((LDS_BG_ATTR + k) & 3)];
-        return tile | at << 8;
+        const uint32_t col = c0 + (uint32_t)k;                                   // 0 .. 63
+        const uint32_t tile = row[(col >> 2) * LDS_LANES * 4 + (col & 3)];
+        const uint32_t ab = LDS_BG_ATTR + (col >> 5) * 8 + ((col & 31) >> 2);   // attribute byte
+        const uint32_t at = row[(ab >> 2) * LDS_LANES * 4 + (ab & 3)];
+        const uint32_t sh = ((cy & 2u) << 1) | (col & 2u);
+        return tile | ((at >> sh) & 3u) << 8;
     }
     // Pattern planes of row fy of tile ta (bg_tile_of) and its gray table: byte p is the gray value of
     // background pattern p (p = 0: the universal background, palette address 0; else palette address
@@ -684,6 +705,7 @@ struct Console {
         if (spr && sp_line != py) build_sprite_line(py);
         const int f = fine_x, fy = (v >> 12) & 7;
         const int g0 = x0 >> 3, g1 = (x1 + 7) >> 3;
+        uint32_t bc0 = 0, bcy = 0;             // line-start coarse x and coarse y
         if (show_bg) {
             // line-start address: v addresses the tile of pixel x0, (f + x0) / 8 tiles into the line
             const int kb = (f + x0) >> 3;
@@ -691,7 +713,8 @@ struct Console {
             uint16_t v0 = v;
             if (c0 < 0) { c0 += 32; v0 ^= 0x400; }
             v0 = (uint16_t)((v0 & ~0x1f) | c0);
-            if ((int32_t)(v0 & 0x0fff) != bg_key) { fill_bg_row(v0); bg_key = v0 & 0x0fff; }
+            if ((int32_t)((v0 >> 5) & 0x7f) != bg_key) { fill_bg_row(v0); bg_key = (v0 >> 5) & 0x7f; }
+            bc0 = v0 & 31u; bcy = (v0 >> 5) & 31u;
         }
         // gray values of the background palettes (addresses 0..15) and the sprite palettes (0x10 + 0..15)
         uint32_t bp0 = lds_gp[0], bp1 = lds_gp[LDS_LANES], bp2 = lds_gp[2 * LDS_LANES], bp3 = lds_gp[3 * LDS_LANES];
@@ -713,9 +736,9 @@ struct Console {
         // are used one iteration later, so no LDS round trip sits between two groups.
         uint32_t alo = 0, ahi = 0, agt = ubg, blo = 0, bhi = 0, bgt = ubg, nxt = 0;
         if (show_bg) {
-            bg_planes(bg_tile_of(g0), fy, bgpal, alo, ahi, agt);
-            bg_planes(bg_tile_of(g0 + 1), fy, bgpal, blo, bhi, bgt);
-            if (g0 + 1 < g1) nxt = bg_tile_of(g0 + 2);
+            bg_planes(bg_tile_of(g0, bc0, bcy), fy, bgpal, alo, ahi, agt);
+            bg_planes(bg_tile_of(g0 + 1, bc0, bcy), fy, bgpal, blo, bhi, bgt);
+            if (g0 + 1 < g1) nxt = bg_tile_of(g0 + 2, bc0, bcy);
         }
         uint32_t s0 = 0, s1 = 0;                         // sprite bytes of the group's two words
         if (spr) { s0 = lds_sp[(2 * g0) * LDS_LANES]; s1 = lds_sp[(2 * g0 + 1) * LDS_LANES]; }
@@ -724,7 +747,7 @@ struct Console {
             uint32_t clo = 0, chi = 0, cgt = ubg, nn = 0;
             if (show_bg && g + 1 < g1) {
                 bg_planes(nxt, fy, bgpal, clo, chi, cgt);
-                if (g + 2 < g1) nn = bg_tile_of(g + 3);
+                if (g + 2 < g1) nn = bg_tile_of(g + 3, bc0, bcy);
             }
             uint32_t t0 = 0, t1 = 0;
             if (spr && g + 1 < g1) { t0 = lds_sp[(2 * g + 2) * LDS_LANES]; t1 = lds_sp[(2 * g + 3) * LDS_LANES]; }
