@@ -31,6 +31,11 @@ constexpr int LDS_BG_ATTR = 64;                    // byte offset of the attribu
 constexpr int LDS_OAM_WORDS = 64;                  // words per lane: OAM (sprite i = word i: y, tile, attr, x)
 constexpr int LDS_GP_REGION = LDS_GP_WORDS + LDS_BG_WORDS + LDS_OAM_WORDS;   // palette, tile row, OAM
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
+// Render lines per frame slice (a power of two). A wave runs its lanes' CPUs to the end of a group of
+// this many lines and then catches their PPUs up together; a wave iteration costs the slowest lane's
+// instruction, so longer slices let the lanes' per-line instruction counts average out, while a lane
+// that must catch up inside a slice (a PPU register access) renders those lines alone. 8 measured best.
+constexpr int SLICE_LINES = 8;
 constexpr int LINE_END = 341;
 constexpr int GRAY_PIX = 256 * 240;
 // Byte offset of VRAM word w (bytes 4w .. 4w+3) of console e in a memory block of np consoles. The VRAM
@@ -880,12 +885,14 @@ struct Console {
     __device__ __forceinline__ uint8_t pull() { sp++; return ram(0x100 | sp); }
     __device__ __forceinline__ void cross_penalty(uint16_t u, uint16_t w, int k) { if ((u & 0xff00) != (w & 0xff00)) skip += k; }
 
-    // End of the next frame slice: the PPU call after which dots 1..256 of the next render line are
-    // done (this line's if they are still ahead), capped at the frame end `cap`.
+    // End of the next frame slice: the PPU call after which dots 1..256 of the last line of the next
+    // group of SLICE_LINES render lines are done (the current group's if its last line is still ahead),
+    // capped at the frame end `cap`.
     __device__ __forceinline__ int32_t next_slice(int32_t cap) const {
         int line = 0;
         if (pstate == ST_RENDER) line = pcyc < 257 ? scanline : scanline + 1;
-        int32_t d = line <= 239 ? calls_until(line, 257) : calls_until(0, 257);
+        const int last = (line | (SLICE_LINES - 1)) < 239 ? (line | (SLICE_LINES - 1)) : 239;
+        int32_t d = line <= 239 ? calls_until(last, 257) : calls_until(SLICE_LINES - 1, 257);
         if (d < 1) d = 1;
         const int32_t s = ppu_calls + d;
         return s < cap ? s : cap;
@@ -1081,10 +1088,10 @@ struct Console {
     // slices. Branching per opcode is confined to register arithmetic, so a wave whose lanes run
     // different instructions stays converged on the memory accesses.
     //
-    // The frame is cut into slices that end right after the visible dots of a render line (and at
-    // the frame end). A lane only starts an instruction j whose catch-up point 3 (j + 1) is at most
-    // its slice end; once every lane of the wave is parked at its slice end, all of them catch their
-    // PPU up to it together, so each renders one whole line with the whole wave active. This is the
+    // The frame is cut into slices that end right after the visible dots of every SLICE_LINES-th render
+    // line (and at the frame end). A lane only starts an instruction j whose catch-up point 3 (j + 1) is
+    // at most its slice end; once every lane of the wave is parked at its slice end, all of them catch
+    // their PPU up to it together, so the slice's lines are rendered with the whole wave active. This is the
     // reference's catch-up PPU cut at more points (the PPU result does not depend on where it is
     // caught up), and never past a parked lane's next catch-up point 3 (j + 1), so an NMI raised
     // inside the slice catch-up sees exactly the CPU state of the reference's catch-up at the start
