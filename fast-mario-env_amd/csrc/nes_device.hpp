@@ -668,8 +668,9 @@ struct Console {
 #pragma unroll
         for (int i = 0; i < LDS_BG_WORDS; i++) lds_bg[i * LDS_LANES] = w[i];
     }
-    // Tile k of the line whose row is cached (c0: the line's starting coarse x, cy: its coarse y):
-    // index | attribute << 8. Column c0 + k is in name table A below 32, else in B.
+    // Tile k (0..32) of the line whose row is cached (c0: the line's starting coarse x, cy: its coarse
+    // y): index | attribute byte << 8 | the attribute's shift in it << 16, unpacked by bg_planes (the
+    // loads are not waited for here). Column c0 + k is in name table A below 32, else in B.
     __device__ __forceinline__ uint32_t bg_tile_of(int k, uint32_t c0, uint32_t cy) const {
         const uint8_t* row = (const uint8_t*)lds_bg;
         const uint32_t col = c0 + (uint32_t)k;                                   // 0 .. 63
@@ -677,7 +678,7 @@ struct Console {
         const uint32_t ab = LDS_BG_ATTR + (col >> 5) * 8 + ((col & 31) >> 2);   // attribute byte
         const uint32_t at = row[(ab >> 2) * LDS_LANES * 4 + (ab & 3)];
         const uint32_t sh = ((cy & 2u) << 1) | (col & 2u);
-        return tile | ((at >> sh) & 3u) << 8;
+        return tile | at << 8 | sh << 16;
     }
     // Pattern planes of row fy of tile ta (bg_tile_of) and its gray table: byte p is the gray value of
     // background pattern p (p = 0: the universal background, palette address 0; else palette address
@@ -687,8 +688,9 @@ struct Console {
         const uint16_t pa = (uint16_t)((((ta & 0xffu) * 16) + fy) | (bg_page << 12));
         lo = cart.chr[pa];
         hi = cart.chr[pa + 8];
-        const uint32_t w01 = (ta & 0x100u) ? pal[1] : pal[0], w23 = (ta & 0x100u) ? pal[3] : pal[2];
-        gt = (((ta & 0x200u) ? w23 : w01) & 0xffffff00u) | (pal[0] & 0xffu);
+        const uint32_t at = (ta >> (8 + (ta >> 16))) & 3u;
+        const uint32_t w01 = (at & 1u) ? pal[1] : pal[0], w23 = (at & 1u) ? pal[3] : pal[2];
+        gt = (((at & 2u) ? w23 : w01) & 0xffffff00u) | (pal[0] & 0xffu);
     }
 
     // Pixels of visible dots [x0, x1): gray values into the frame buffer (nes_core.hpp:467-513), with
@@ -738,24 +740,23 @@ struct Console {
         const uint32_t tsel0 = (uint32_t)second & 0x04040404u, tsel1 = (uint32_t)(second >> 32) & 0x04040404u;
         // Software pipeline over the groups: group g needs tiles g and g + 1 (a, b). Iteration g fetches
         // the planes of tile g + 2, the index of tile g + 3 and the sprite bytes of group g + 1, which
-        // are used one iteration later, so no LDS round trip sits between two groups.
-        uint32_t alo = 0, ahi = 0, agt = ubg, blo = 0, bhi = 0, bgt = ubg, nxt = 0;
-        if (show_bg) {
-            bg_planes(bg_tile_of(g0, bc0, bcy), fy, bgpal, alo, ahi, agt);
-            bg_planes(bg_tile_of(g0 + 1, bc0, bcy), fy, bgpal, blo, bhi, bgt);
-            if (g0 + 1 < g1) nxt = bg_tile_of(g0 + 2, bc0, bcy);
-        }
-        uint32_t s0 = 0, s1 = 0;                         // sprite bytes of the group's two words
-        if (spr) { s0 = lds_sp[(2 * g0) * LDS_LANES]; s1 = lds_sp[(2 * g0 + 1) * LDS_LANES]; }
+        // are used one iteration later, so no LDS round trip sits between two groups. The fetches are
+        // unconditional (indices clamped to the buffers; a layer that is off masks its values
+        // afterwards), so every iteration issues the same LDS operations.
+        uint32_t alo, ahi, agt, blo, bhi, bgt;
+        bg_planes(bg_tile_of(g0, bc0, bcy), fy, bgpal, alo, ahi, agt);
+        bg_planes(bg_tile_of(g0 + 1, bc0, bcy), fy, bgpal, blo, bhi, bgt);
+        uint32_t nxt = bg_tile_of(g0 + 2 < 32 ? g0 + 2 : 32, bc0, bcy);
+        if (!show_bg) { alo = ahi = blo = bhi = 0; agt = bgt = ubg; }
+        uint32_t s0 = lds_sp[(2 * g0) * LDS_LANES], s1 = lds_sp[(2 * g0 + 1) * LDS_LANES];   // the group's sprite bytes
+        if (!spr) s0 = s1 = 0;
         uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g0) * np;   // word of pixels 8g .. 8g+3
         for (int g = g0; g < g1; g++) {
-            uint32_t clo = 0, chi = 0, cgt = ubg, nn = 0;
-            if (show_bg && g + 1 < g1) {
-                bg_planes(nxt, fy, bgpal, clo, chi, cgt);
-                if (g + 2 < g1) nn = bg_tile_of(g + 3, bc0, bcy);
-            }
-            uint32_t t0 = 0, t1 = 0;
-            if (spr && g + 1 < g1) { t0 = lds_sp[(2 * g + 2) * LDS_LANES]; t1 = lds_sp[(2 * g + 3) * LDS_LANES]; }
+            uint32_t clo, chi, cgt;
+            bg_planes(nxt, fy, bgpal, clo, chi, cgt);
+            const uint32_t nn = bg_tile_of(g + 3 < 32 ? g + 3 : 32, bc0, bcy);
+            const int ws = 2 * g + 2 < 62 ? 2 * g + 2 : 62;
+            const uint32_t t0 = lds_sp[ws * LDS_LANES], t1 = lds_sp[(ws + 1) * LDS_LANES];
             // pixel 8g + bb is bit 15 - bb of the window after the fine-scroll shift; reversed: bit 16 + bb
             const uint32_t rlo = __builtin_bitreverse32(((alo << 8) | blo) << f);
             const uint32_t rhi = __builtin_bitreverse32(((ahi << 8) | bhi) << f);
@@ -799,8 +800,8 @@ struct Console {
             }
             wp += 2 * np;
             alo = blo; ahi = bhi; agt = bgt;
-            blo = clo; bhi = chi; bgt = cgt;
-            nxt = nn; s0 = t0; s1 = t1;
+            blo = show_bg ? clo : 0u; bhi = show_bg ? chi : 0u; bgt = show_bg ? cgt : ubg;
+            nxt = nn; s0 = spr ? t0 : 0u; s1 = spr ? t1 : 0u;
         }
     }
 
