@@ -83,6 +83,44 @@ __device__ __forceinline__ uint8_t area_pixel(const Image& g0, const Image& g1, 
     return round_sat(acc);
 }
 
+// INTER_AREA column dx of one image of a frame buffer (4-pixel words, word w of lane e at w np + e),
+// max-pooled with a second one if `pool`: out[dy * ostride] = output pixel (dy, dx) for dy = 0..83.
+// The float operations and their order are area_pixel's. A column's taps are at most 5 consecutive
+// source pixels (scale 256 / 84), so one source row needs two words per image.
+__device__ __forceinline__ void area_column(const uint32_t* g0, const uint32_t* g1, uint32_t np, uint32_t e,
+                                            bool pool, int dx, const AreaTables* T, uint8_t* out, size_t ostride) {
+    const int nx = T->xn[dx];
+    const int x0 = T->xs[dx * TAPS];
+    float w[5];
+#pragma unroll
+    for (int k = 0; k < 5; k++) w[k] = T->xw[dx * TAPS + k];
+    const uint32_t sh = (uint32_t)(x0 & 3) * 8, wa = (uint32_t)x0 >> 2, wb = wa < 63 ? wa + 1 : 63;
+    for (int dy = 0; dy < 84; dy++) {
+        const int ny = T->yn[dy];
+        float acc = 0.f;
+        for (int j = 0; j < ny; j++) {
+            const uint32_t sy = (uint32_t)T->ys[dy * TAPS + j];
+            const size_t ia = (size_t)(sy * 64 + wa) * np + e, ib = (size_t)(sy * 64 + wb) * np + e;
+            const uint64_t v0 = ((uint64_t)g0[ia] | (uint64_t)g0[ib] << 32) >> sh;
+            uint64_t v1 = 0;
+            if (pool) v1 = ((uint64_t)g1[ia] | (uint64_t)g1[ib] << 32) >> sh;
+            float row = 0.f;
+#pragma unroll
+            for (int k = 0; k < 5; k++) {
+                if (k < nx) {
+                    uint32_t s = (uint32_t)(v0 >> (8 * k)) & 0xffu;
+                    const uint32_t s1 = (uint32_t)(v1 >> (8 * k)) & 0xffu;
+                    if (pool && s1 > s) s = s1;
+                    row += (float)s * w[k];
+                }
+            }
+            const float term = T->yw[dy * TAPS + j] * row;
+            acc = j == 0 ? term : acc + term;
+        }
+        out[(size_t)dy * ostride] = round_sat(acc);
+    }
+}
+
 // ------------------------------------------------------------------ arguments
 struct RomArgs {
     const uint8_t* rom;      // 0x8000 PRG (mirrored) + 0x2000 CHR

@@ -784,7 +784,9 @@ struct Console {
                 out[q] = word;
             }
             const int xg = 8 * g;
-            if (xg >= x0 && xg + 8 <= x1) { wp[0] = out[0]; wp[np] = out[1]; }
+            // streaming stores: the frame buffers are read by the next kernel only, so they should not
+            // evict the console state from the L2
+            if (xg >= x0 && xg + 8 <= x1) { __builtin_nontemporal_store(out[0], wp); __builtin_nontemporal_store(out[1], wp + np); }
             else {
                 // a partial group: only the pixels in [x0, x1)
 #pragma unroll
