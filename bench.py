@@ -56,20 +56,32 @@ def pick_rom():
         return open(path, "rb").read(), "mini_smb_vanilla.nes (synthetic NROM stand-in; no SMB ROM on this machine)"
 
 
-def traffic_from_profiles(workload_key):
-    """HBM bytes per k_step launch from the committed rocprofv3 --pmc summary, if one exists for this workload."""
-    path = os.path.join(ROOT, "profiles", "k_step_pmc_traffic.md")
+def profile_values(name, workload_key):
+    """`- key: value` lines of a committed rocprofv3 summary under profiles/, if it covers this workload."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.isfile(path):
-        return None
+        return {}
     vals = {}
     for line in open(path):
         if ":" in line and line.strip().startswith("-"):
             k, v = line.strip("- \n").split(":", 1)
             vals[k.strip()] = v.strip()
-    if vals.get("workload") != workload_key:
-        return None
+    wl = vals.get("workload", "").split(";")[0].strip()
+    return vals if wl == workload_key else {}
+
+
+def traffic_from_profiles(workload_key):
+    """HBM bytes per k_step launch from the committed rocprofv3 --pmc summary, if one exists for this workload."""
     try:
-        return float(vals["hbm_bytes_per_launch"])
+        return float(profile_values("k_step_pmc_traffic.md", workload_key)["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def valu_issue_from_profiles(workload_key):
+    """k_step's VALU issue fraction from the committed rocprofv3 SQ-counter summary, if one exists."""
+    try:
+        return float(profile_values("k_step_sq_counters_headline.md", workload_key)["valu_issue_fraction"])
     except (KeyError, ValueError):
         return None
 
@@ -206,8 +218,10 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
                      "traffic": traffic,
                      "algorithmic_bytes_per_launch": round(k_bytes),
+                     "valu_issue_frac": valu_issue_from_profiles(workload),
                      "note": "k_step is bound by dependent VALU/LDS/memory latency per lane, not by HBM; "
-                             "VALU-issue utilization is in profiles/ (rocprofv3 SQ counters)"},
+                             "valu_issue_frac is SQ_INSTS_VALU x 4 cycles over 1024 SIMDs x duration x 2.4 GHz "
+                             "from the committed rocprofv3 SQ-counter summary in profiles/"},
         "stages_ms_per_step": {k: round(v / max(1, timed), 3) for k, v in stages.items()},
         "p_done": round(p_done, 5),
         "frames_per_step": round(frames / (n * args.steps), 3),
