@@ -1120,11 +1120,14 @@ struct Console {
                 synced = false;
                 continue;
             }
-            if (parked) continue;
+            // One action per lane and iteration, chosen through `act` rather than early exits from the
+            // loop body (each exit is a path whose state the next iteration must merge): park at the
+            // slice end, ask for a catch-up, fast-forward, or run one instruction.
             const int32_t j = exec_at;
             const int32_t tgt = 3 * (j + 1);
-            if (j >= end || tgt > slice) { parked = true; continue; }
-            if (tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; continue; }
+            bool act = !parked;
+            if (act && (j >= end || tgt > slice)) { parked = true; act = false; }
+            if (act && tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; act = false; }
             // PRG bytes at pc for the fast paths; the idle check reads 0xff past 0xffff
             const bool in_prg = pc >= 0x8000;
             uint8_t op0 = 0, q1 = 0xff, q2 = 0xff;
@@ -1133,22 +1136,22 @@ struct Console {
                 if (pc != 0xffff) q1 = prg((uint16_t)(pc + 1));
                 if (pc < 0xfffe) q2 = prg((uint16_t)(pc + 2));
             }
-            if (in_prg && op0 == 0x4c && (uint16_t)(q1 | q2 << 8) == pc) {
+            if (act && in_prg && op0 == 0x4c && (uint16_t)(q1 | q2 << 8) == pc) {
                 const int32_t lim_end = end - j, lim_nmi = nmi_thresh - tgt;
                 const int32_t k1 = lim_end > 0 ? (lim_end + 2) / 3 : 0;
                 const int32_t k2 = lim_nmi > 0 ? (lim_nmi + 8) / 9 : 0;
                 const int32_t k = k1 < k2 ? k1 : k2;
-                if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; continue; }
+                if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; act = false; }
             }
-            if (in_prg && op0 == 0xad && q1 == 0x02 && q2 == 0x20 && pc <= 0xfff8 && prg(pc + 3) == 0x29 &&
+            if (act && in_prg && op0 == 0xad && q1 == 0x02 && q2 == 0x20 && pc <= 0xfff8 && prg(pc + 3) == 0x29 &&
                 prg(pc + 4) == 0x40 && prg(pc + 6) == 0xf9) {
                 const uint8_t br = prg(pc + 5);
                 if (br == 0xf0 || br == 0xd0) {
-                    if (ppu_calls < tgt) { want = tgt; continue; }   // the sync of the LDA $2002 at j
-                    if (poll_skip(j, end, br == 0xf0)) continue;
+                    if (ppu_calls < tgt) { want = tgt; act = false; }   // the sync of the LDA $2002 at j
+                    else if (poll_skip(j, end, br == 0xf0)) act = false;
                 }
             }
-            if (!instruction(j, tgt, in_prg && pc <= 0xfffd, op0, q1, q2)) want = tgt;
+            if (act && !instruction(j, tgt, in_prg && pc <= 0xfffd, op0, q1, q2)) want = tgt;
         }
         // rebase the frame-relative counters on the new frame start
         exec_at -= FRAME_ITERS;
