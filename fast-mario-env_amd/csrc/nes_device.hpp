@@ -337,8 +337,8 @@ struct Console {
     // Accesses for which needs_sync() holds see the PPU caught up to 3 * (cur + 1): frame() syncs
     // before it issues them (the reference catches up inside the access; the target is the same).
     __device__ __forceinline__ static bool needs_sync(uint16_t ad, bool wr) {
-        if (ad >= 0x2000 && ad < 0x4000) return wr || (ad & 7) == 2 || (ad & 7) == 7;
-        return wr && ad == 0x4014;
+        const bool ppu = (ad & 0xe000) == 0x2000, r2 = (ad & 7) == 2, r7 = (ad & 7) == 7;
+        return (ppu & (wr | r2 | r7)) | (wr & (ad == 0x4014));
     }
     __device__ __forceinline__ uint8_t read(uint16_t ad) {
         if (ad >= 0x8000) return prg(ad);
@@ -923,20 +923,22 @@ struct Console {
         }
         const uint32_t am = D & 15u, xop = (D >> X_SH) & 15u, dst = (D >> DST_SH) & 7u;
         const bool rd = (D & RD) != 0, wr = dst == D_MEM;
+        // addressing as selects on mode-set bits (no branch except for the zero-page pointer loads)
+        const uint32_t mb = 1u << am;
+        constexpr uint32_t X_IDX = 1u << M_ZPX | 1u << M_ABSX, Y_IDX = 1u << M_ZPY | 1u << M_ABSY | 1u << M_INDY;
+        constexpr uint32_t ZP_EA = 1u << M_ZP | 1u << M_ZPX | 1u << M_ZPY, IND = 1u << M_INDX | 1u << M_INDY;
         const uint16_t absv = (uint16_t)(b1 | b2 << 8);
         uint16_t base = absv;
-        if (am == M_INDX || am == M_INDY) {   // pointer from the zero page
+        if (mb & IND) {   // pointer from the zero page
             const uint8_t z = am == M_INDX ? (uint8_t)(b1 + x) : b1;
             base = (uint16_t)(ram(z) | ram((uint8_t)(z + 1)) << 8);
         }
-        const uint8_t idx = (am == M_ZPX || am == M_ABSX) ? x : (am == M_ZPY || am == M_ABSY || am == M_INDY) ? y : 0;
-        uint16_t ea;
-        if (am == M_ZP || am == M_ZPX || am == M_ZPY) ea = (uint8_t)(b1 + idx);
-        else if (am == M_IMM) ea = (uint16_t)(pc + 1);
-        else ea = (uint16_t)(base + idx);
+        const uint32_t idx = (mb & X_IDX) ? (uint32_t)x : (mb & Y_IDX) ? (uint32_t)y : 0u;
+        const uint16_t ea = (mb & ZP_EA) ? (uint16_t)((b1 + idx) & 0xffu)
+                          : am == M_IMM ? (uint16_t)(pc + 1) : (uint16_t)(base + idx);
         const uint16_t p2 = (uint16_t)((absv & 0xff00) | ((absv + 1) & 0xff));   // JMP (ind): high byte, page wrap
-        const bool sync = xop == X_JMPI ? (needs_sync(absv, false) || needs_sync(p2, false))
-                                        : ((rd && needs_sync(ea, false)) || (wr && needs_sync(ea, true)));
+        const bool sync = xop == X_JMPI ? (needs_sync(absv, false) | needs_sync(p2, false))
+                                        : ((rd & needs_sync(ea, false)) | (wr & needs_sync(ea, true)));
         if (sync && ppu_calls < tgt) return false;   // only when pf: no bus access has happened yet
         cur = j;
         skip = 0;
@@ -945,44 +947,61 @@ struct Console {
         // data operand and ALU
         const uint8_t m = rd && am != M_IMM ? read(ea) : b1;
         const uint32_t alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, fl = (D >> FL_SH) & 7u;
-        const uint32_t rv = src == R_A ? a : src == R_X ? x : src == R_Y ? y : src == R_SP ? sp : m;
-        const uint32_t sv = rd ? m : rv;                          // operand of the unary operations
+        // Every choice below is a select on bits of the decode word: chains of equality tests on one small
+        // field would be lowered to a branch tree, i.e. exec-mask branches on every instruction.
+        const uint32_t regs = (uint32_t)a | (uint32_t)x << 8 | (uint32_t)y << 16 | (uint32_t)sp << 24;
+        const uint32_t rv = src ? (regs >> (8 * (src - 1))) & 0xffu : (uint32_t)m;   // R_A, R_X, R_Y, R_SP, or M
+        const uint32_t sv = rd ? (uint32_t)m : rv;                // operand of the unary operations
         const uint32_t cin = (p & FC) ? 1u : 0u;
         const uint32_t sum = a + m + cin;                         // ADC
         const uint32_t dif = a - m - (1u - cin);                  // SBC
         const uint32_t cmp = rv - m;                              // CMP / CPX / CPY
-        const bool left = alu == OP_ASL || alu == OP_ROL, right = alu == OP_LSR || alu == OP_ROR;
-        const uint32_t shl = (sv << 1) | (alu == OP_ROL ? cin : 0u);
-        const uint32_t shr = (sv >> 1) | (alu == OP_ROR ? cin << 7 : 0u);
-        const uint32_t res = alu == OP_ORA ? (a | m) : alu == OP_AND ? (a & m) : alu == OP_EOR ? (a ^ m)
-                           : alu == OP_ADC ? sum : alu == OP_SBC ? dif : alu == OP_CMP ? cmp
-                           : left ? shl : right ? shr : alu == OP_INC ? sv + 1 : alu == OP_DEC ? sv - 1 : sv;
+        const bool u0 = alu & 1u, u1 = alu & 2u, u2 = alu & 4u, u3 = alu & 8u;
+        const uint32_t rc = u0 ? cin : 0u;                        // ROL / ROR carry in
+        // OP_ results by the bits of alu: PASS ORA AND EOR ADC SBC CMP BIT ASL ROL LSR ROR INC DEC FLAG NOP
+        const uint32_t g0 = u0 ? (uint32_t)(a | m) : sv, g1 = u0 ? (uint32_t)(a ^ m) : (uint32_t)(a & m);
+        const uint32_t g2 = u0 ? dif : sum, g3 = u0 ? sv : cmp;
+        const uint32_t g4 = (sv << 1) | rc, g5 = (sv >> 1) | (rc << 7), g6 = u0 ? sv - 1 : sv + 1, g7 = sv;
+        const uint32_t h0 = u1 ? g1 : g0, h1 = u1 ? g3 : g2, h2 = u1 ? g5 : g4, h3 = u1 ? g7 : g6;
+        const uint32_t res = u3 ? (u2 ? h3 : h2) : (u2 ? h1 : h0);
         const uint8_t r8 = (uint8_t)res;
-        const bool carry = alu == OP_ADC ? (sum & 0x100) != 0 : (alu == OP_SBC || alu == OP_CMP) ? !(res & 0x100)
-                         : left ? (sv & 0x80) != 0 : (sv & 1) != 0;
-        const bool ovf = alu == OP_ADC ? ((a ^ sum) & (m ^ sum) & 0x80) != 0 : ((a ^ dif) & (~(uint32_t)m ^ dif) & 0x80) != 0;
-        uint8_t np = p;
-        if (fl == FL_NZ || fl == FL_NZC || fl == FL_NZCV)
-            np = (uint8_t)((np & ~(FZ | FN)) | (r8 ? 0 : FZ) | (r8 & 0x80 ? FN : 0));
-        if (fl == FL_NZC || fl == FL_NZCV) np = carry ? (uint8_t)(np | FC) : (uint8_t)(np & ~FC);
-        if (fl == FL_NZCV) np = ovf ? (uint8_t)(np | FV) : (uint8_t)(np & ~FV);
-        if (fl == FL_BIT)
-            np = (uint8_t)((np & ~(FZ | FV | FN)) | ((a & m) ? 0 : FZ) | (m & 0x40 ? FV : 0) | (m & 0x80 ? FN : 0));
-        if (fl == FL_OP) {   // CLC SEC CLI SEI CLV CLD SED
-            const uint32_t fop = (D >> FOP_SH) & 7u;
-            const uint8_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;
-            np = (fop == 1 || fop == 3 || fop == 6) ? (uint8_t)(np | fm) : (uint8_t)(np & ~fm);
-        }
-        p = np;
+        // carry: ADC bit 8 of the sum; SBC / CMP no borrow; ASL / ROL bit 7; LSR / ROR bit 0
+        const uint32_t c_sub = ((res >> 8) & 1u) ^ 1u, c_adc = (sum >> 8) & 1u;
+        const uint32_t carry = u3 ? (u1 ? (sv & 1u) : ((sv >> 7) & 1u)) : ((u0 | u1) ? c_sub : c_adc);
+        const uint32_t ovf = u0 ? ((a ^ dif) & (~(uint32_t)m ^ dif) & 0x80u) : ((a ^ sum) & (m ^ sum) & 0x80u);
+        // flag groups NONE NZ NZC NZCV BIT OP as masks of the bits they replace
+        const uint32_t nzv = (r8 ? 0u : FZ) | (r8 >> 7);          // FN is bit 0
+        const uint32_t fz = (a & m) ? 0u : FZ;
+        const uint32_t bitv = fz | (m & 0x40 ? FV : 0u) | (m >> 7);
+        const uint32_t fop = (D >> FOP_SH) & 7u;
+        const uint32_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;   // CLC SEC CLI SEI CLV CLD SED
+        const uint32_t fset = (fop == 1 || fop == 3 || fop == 6) ? fm : 0u;
+        uint32_t keep = 0xffu, set = 0u;
+        if ((0xeu >> fl) & 1u) { keep &= ~(uint32_t)(FZ | FN); set |= nzv; }             // NZ, NZC, NZCV
+        if ((0xcu >> fl) & 1u) { keep &= ~(uint32_t)FC; set |= carry ? FC : 0u; }        // NZC, NZCV
+        if (fl == FL_NZCV) { keep &= ~(uint32_t)FV; set |= ovf ? FV : 0u; }
+        if (fl == FL_BIT) { keep &= ~(uint32_t)(FZ | FV | FN); set |= bitv; }
+        if (fl == FL_OP) { keep &= ~fm; set |= fset; }
+        p = (uint8_t)((p & keep) | set);
         a = dst == D_A ? r8 : a;
         x = dst == D_X ? r8 : x;
         y = dst == D_Y ? r8 : y;
         sp = dst == D_SP ? r8 : sp;
         if (wr) write(ea, r8);
-        // stack and control flow
-        uint16_t npc = (uint16_t)(pc + (am == M_NONE ? 1 : (am == M_ABS || am == M_ABSX || am == M_ABSY) ? 3 : 2));
-        if (xop != X_NONE) {
-            const uint16_t ret = (uint16_t)(pc + 2);
+        // control flow: the next pc by instruction length, branches and JMP as selects
+        constexpr uint32_t ABS3 = 1u << M_ABS | 1u << M_ABSX | 1u << M_ABSY;
+        uint16_t npc = (uint16_t)(pc + (am == M_NONE ? 1 : (mb & ABS3) ? 3 : 2));
+        const uint16_t ret = (uint16_t)(pc + 2);
+        {   // branch on N, V, C, Z (op bits 6-7) equal to op bit 5; 2 bytes; the offset is read only when taken
+            const uint32_t fbit = (0x40800201u >> (8 * (op >> 6))) & 0xffu;   // FN FV FC FZ
+            const bool taken = (xop == X_BRANCH) & (((p & fbit) != 0) == ((op & 0x20) != 0));
+            uint8_t off = b1;
+            if (taken && !pf) off = read((uint16_t)(pc + 1));
+            const uint16_t to = (uint16_t)(ret + (int8_t)off);
+            npc = xop == X_BRANCH ? (taken ? to : ret) : xop == X_JMP ? absv : npc;
+            skip += taken ? (((ret ^ to) & 0xff00) ? 3 : 1) : 0;
+        }
+        if (xop != X_NONE && xop != X_BRANCH && xop != X_JMP) {   // stack operations and JMP (ind)
             switch (xop) {
                 case X_BRK:
                     push((uint8_t)(ret >> 8)); push((uint8_t)ret); push((uint8_t)(p | 0x30));
@@ -1000,20 +1019,8 @@ struct Console {
                 case X_PHP: push(p); break;
                 case X_PLA: a = pull(); set_nz(a); break;
                 case X_PLP: p = pull(); break;
-                case X_JMP: npc = absv; break;
                 case X_JMPI: { const uint8_t lo = read(absv); const uint8_t hi = read(p2); npc = (uint16_t)(lo | hi << 8); break; }
-                default: {   // branch on N, V, C, Z (op bits 6-7) equal to op bit 5; 2 bytes
-                    const uint8_t fm = (op >> 6) == 0 ? FN : (op >> 6) == 1 ? FV : (op >> 6) == 2 ? FC : FZ;
-                    npc = ret;
-                    if (((p & fm) != 0) == ((op & 0x20) != 0)) {
-                        skip += 1;
-                        const uint8_t off = pf ? b1 : read((uint16_t)(pc + 1));
-                        const uint16_t to = (uint16_t)(npc + (int8_t)off);
-                        cross_penalty(npc, to, 2);
-                        npc = to;
-                    }
-                    break;
-                }
+                default: break;
             }
         }
         pc = npc;
