@@ -1112,7 +1112,16 @@ struct Console {
         int32_t slice = next_slice(last_call);   // end of this lane's current slice, in PPU calls
         bool parked = false, synced = false;
         for (;;) {
-            if (want >= 0) { advance_to(want); want = -1; }
+            if (__any(want >= 0)) {
+                // Every lane catches up with the one that must, each to its own next catch-up point
+                // 3 (j + 1) (the reference's point before its instruction j; an NMI due by then is raised
+                // exactly as in the lane's own catch-up), at most its slice end: the lines pending in
+                // the wave are rendered together instead of by one lane at a time.
+                int32_t t = want;
+                if (t < 0) { const int32_t nx = 3 * (exec_at + 1); t = nx < slice ? nx : slice; }
+                advance_to(t);
+                want = -1;
+            }
             if (__all(parked)) {
                 // The whole wave is at the slice boundary: catch up together (next iteration), then
                 // open the next slice. `slice` and `synced` are wave-uniform, so every lane takes
