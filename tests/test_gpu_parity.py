@@ -66,6 +66,12 @@ def test_raw_program_fuzz(seed):
     _raw_run(fuzz.program_rom(seed), 4, scaled(80), seed=seed, backup_p=0.05)
 
 
+def test_raw_program_fuzz_two_waves():
+    # 40 consoles: a full 32-env wave and a partial one, so catch-ups that one lane forces on the others of
+    # its wave (PPU register accesses at different points) are compared across many lanes
+    _raw_run(fuzz.program_rom(3), 40, scaled(40), seed=3, backup_p=0.05)
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_raw_random_fuzz(seed):
     _raw_run(fuzz.random_rom(seed), 4, scaled(40), seed=seed, render_p=0.5, backup_p=0.05)
@@ -88,11 +94,20 @@ def _levels(names):
 
 @pytest.mark.parametrize("config", list(CONFIGS))
 def test_env_vs_oracle(config):
+    _env_run(["1-1", "1-1", "4-1", "8-4", "2-3", "1-2", "1-1", "5-2"], config, scaled(150))
+
+
+def test_env_vs_oracle_two_waves():
+    # 40 envs (a full 32-env wave and a partial one) with the headline wrappers
+    names = ["1-1", "4-1", "8-4", "2-3", "1-2", "5-2", "3-3", "7-1"] * 5
+    _env_run(names, "headline", scaled(60))
+
+
+def _env_run(names, config, steps):
     import torch
 
     from fast_mario_env_amd import HipVecEnv
     kw = CONFIGS[config]
-    names = ["1-1", "1-1", "4-1", "8-4", "2-3", "1-2", "1-1", "5-2"]
     n = len(names)
     cpu = OracleVec(MINI, _levels(names), n, seed=7, **kw)
     gpu = HipVecEnv(names, n, seed=7, rom=MINI, **kw)
@@ -102,7 +117,7 @@ def test_env_vs_oracle(config):
     assert np.array_equal(gpu.canon().cpu().numpy(), np.stack([cpu.canon(i) for i in range(n)])), "reset state"
     rng = np.random.default_rng(130)
     eps = 0
-    for t in range(scaled(150)):
+    for t in range(steps):
         a = rng.choice(7, n, p=ACTION_P)
         o1, r1, te1, tr1, i1 = cpu.step(a)
         o2, r2, te2, tr2, i2 = gpu.step(torch.from_numpy(a).cuda())
