@@ -841,6 +841,20 @@ struct Console {
                     if (render) dots_drawn(c - 1, c - 1 + k);
                     dots_hit_scroll(c - 1, c - 1 + k);
                     pcyc += k; ppu_calls += k; n -= k;
+                    c = pcyc;
+                }
+                if (n <= 0) {
+                    // the calls ran out inside the visible dots
+                } else if (c == 257 && n >= LINE_END - 256) {
+                    // the rest of the line in one step when all of it is due: dot 257 (fine y), dot 258
+                    // (copy_h), dots 259..340, and the line end (85 calls), as the cases below would
+                    if (show_bg) fine_y_step();
+                    if (show_bg && show_spr) copy_h();
+                    pend_line = scanline;   // sprite evaluation for the next line (materialized lazily)
+                    sp_line = -1;
+                    scanline++;
+                    pcyc = 1; ppu_calls += LINE_END - 256; n -= LINE_END - 256;
+                    if (scanline >= 240) pstate = ST_POST;
                 } else if (c == 257) {
                     if (show_bg) fine_y_step();
                     pcyc++; ppu_calls++; n--;
