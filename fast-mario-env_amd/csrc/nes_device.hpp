@@ -1015,28 +1015,28 @@ struct Console {
             npc = xop == X_BRANCH ? (taken ? to : ret) : xop == X_JMP ? absv : npc;
             skip += taken ? (((ret ^ to) & 0xff00) ? 3 : 1) : 0;
         }
-        if (xop != X_NONE && xop != X_BRANCH && xop != X_JMP) {   // stack operations and JMP (ind)
-            switch (xop) {
-                case X_BRK:
-                    push((uint8_t)(ret >> 8)); push((uint8_t)ret); push((uint8_t)(p | 0x30));
-                    p |= FI;
-                    npc = (uint16_t)(prg(0xfffe) | prg(0xffff) << 8);
-                    skip += 7;
-                    break;
-                case X_JSR:
-                    push((uint8_t)(ret >> 8)); push((uint8_t)ret);
-                    npc = pf ? absv : (uint16_t)(read((uint16_t)(pc + 1)) | read((uint16_t)(pc + 2)) << 8);
-                    break;
-                case X_RTS: { const uint8_t lo = pull(); const uint8_t hi = pull(); npc = (uint16_t)((lo | hi << 8) + 1); break; }
-                case X_RTI: { p = pull(); const uint8_t lo = pull(); const uint8_t hi = pull(); npc = (uint16_t)(lo | hi << 8); break; }
-                case X_PHA: push(a); break;
-                case X_PHP: push(p); break;
-                case X_PLA: a = pull(); set_nz(a); break;
-                case X_PLP: p = pull(); break;
-                case X_JMPI: { const uint8_t lo = read(absv); const uint8_t hi = read(p2); npc = (uint16_t)(lo | hi << 8); break; }
-                default: break;
-            }
+        // Stack operations as at most three pushes or three pulls with predicated accesses (the pulls are
+        // in flight together), then their results as selects: BRK, JSR, PHA, PHP push; RTI, RTS, PLA, PLP pull.
+        if (xop >= X_BRK && xop <= X_PLP) {
+            const uint32_t npush = xop == X_BRK ? 3u : xop == X_JSR ? 2u : (xop == X_PHA || xop == X_PHP) ? 1u : 0u;
+            const uint32_t npull = xop == X_RTI ? 3u : xop == X_RTS ? 2u : (xop == X_PLA || xop == X_PLP) ? 1u : 0u;
+            const uint8_t v0 = (xop == X_BRK || xop == X_JSR) ? (uint8_t)(ret >> 8) : xop == X_PHA ? a : p;
+            if (npush > 0) st(ROW_RAM + (0x100 | sp), v0);
+            if (npush > 1) st(ROW_RAM + (0x100 | (uint8_t)(sp - 1)), (uint8_t)ret);
+            if (npush > 2) st(ROW_RAM + (0x100 | (uint8_t)(sp - 2)), (uint8_t)(p | 0x30));
+            uint8_t u0 = 0, u1 = 0, u2 = 0;
+            if (npull > 0) u0 = ram(0x100 | (uint8_t)(sp + 1));
+            if (npull > 1) u1 = ram(0x100 | (uint8_t)(sp + 2));
+            if (npull > 2) u2 = ram(0x100 | (uint8_t)(sp + 3));
+            sp = (uint8_t)(sp - npush + npull);
+            if (xop == X_BRK) { p |= FI; npc = (uint16_t)(prg(0xfffe) | prg(0xffff) << 8); skip += 7; }
+            if (xop == X_JSR) npc = pf ? absv : (uint16_t)(read((uint16_t)(pc + 1)) | read((uint16_t)(pc + 2)) << 8);
+            if (xop == X_RTS) npc = (uint16_t)((u0 | u1 << 8) + 1);
+            if (xop == X_RTI) { p = u0; npc = (uint16_t)(u1 | u2 << 8); }
+            if (xop == X_PLA) { a = u0; set_nz(a); }
+            if (xop == X_PLP) p = u0;
         }
+        if (xop == X_JMPI) { const uint8_t lo = read(absv); const uint8_t hi = read(p2); npc = (uint16_t)(lo | hi << 8); }
         pc = npc;
         if (D & OK) skip += (int)((D >> CYC_SH) & 7u);
         else bad_ops++;
