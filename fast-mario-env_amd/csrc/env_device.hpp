@@ -132,6 +132,21 @@ __device__ inline void copy_console(const Region& dst, const Region& src) {
     for (int w = 0; w < S_COUNT; w++) dst.sc[(size_t)w * dst.np + dst.idx] = src.sc[(size_t)w * src.np + src.idx];
 }
 
+// copy_console by the `lanes` lanes of a wave together, lane `lane` taking every lanes-th byte row, VRAM
+// word and register word: one console is a few thousand independent accesses, too many for one lane.
+__device__ inline void copy_console_wave(const Region& dst, const Region& src, uint32_t lane, uint32_t lanes) {
+    constexpr uint32_t BYTE_ROWS = MEM_ROWS - 2048;   // every row but the VRAM span
+    for (uint32_t i = lane; i < BYTE_ROWS; i += lanes) {
+        const uint32_t r = i < (uint32_t)ROW_VRAM ? i : i + 2048;
+        dst.mem[(size_t)r * dst.np + dst.idx] = src.mem[(size_t)r * src.np + src.idx];
+    }
+    for (uint32_t w = lane; w < 512; w += lanes)
+        *(uint32_t*)(dst.mem + vram_word_offset(dst.np, dst.idx, w)) =
+            *(const uint32_t*)(src.mem + vram_word_offset(src.np, src.idx, w));
+    for (uint32_t w = lane; w < (uint32_t)S_COUNT; w += lanes)
+        dst.sc[(size_t)w * dst.np + dst.idx] = src.sc[(size_t)w * src.np + src.idx];
+}
+
 // One env's layer state in registers.
 struct EnvRegs {
     int64_t x_last, time_last;

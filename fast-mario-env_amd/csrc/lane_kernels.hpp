@@ -334,11 +334,12 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
 }
 
 // Auto-reset (fastmario.cpp:389-401): k = integers(noop_max + 1) from the env's stream, the draws of
-// the k no-op steps are skipped, and the cached state of (level, k) is installed.
-__device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
+// the k no-op steps are skipped, and the cached state of (level, k) is installed. Returns the cache
+// entry whose console the env takes (the caller copies it, see copy_console_wave), or -1.
+__device__ inline int reset_lane(const ResetArgs& A, uint32_t e) {
     uint32_t* E = A.ev;
     const size_t np = A.np;
-    if (!A.all && !E[E_DONE * np + e]) { E[E_RESET_IDX * np + e] = 0xffffffffu; return; }
+    if (!A.all && !E[E_DONE * np + e]) { E[E_RESET_IDX * np + e] = 0xffffffffu; return -1; }
     Pcg rng;
     rng.load(E, A.np, e);
     int k = 0;
@@ -348,8 +349,6 @@ __device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
     if (A.cfg.sticky != 0.0)
         for (int d = 0; d < A.cdraws[ci]; d++) rng.next64();
     rng.store(E, A.np, e);
-    Region dst{A.mem, A.sc, A.np, e}, src{(uint8_t*)A.cmem, (uint32_t*)A.csc, A.ncp, (uint32_t)ci};
-    copy_console(dst, src);
     EnvRegs ev{};
     ev.x_last = A.cx[ci]; ev.time_last = A.ct[ci]; ev.lives = A.clives[ci]; ev.prev = 0;
     ev.t = 0; ev.ep_len = 0; ev.ep_ret = 0.0; ev.shows_boot = A.cboot[ci] != 0; ev.pooled = false; ev.slot_swap = false;
@@ -359,6 +358,7 @@ __device__ inline void reset_lane(const ResetArgs& A, uint32_t e) {
     add_counter(E, A.np, e, E_FRAMES_LO, A.cframes[ci]);
     add_counter(E, A.np, e, E_INSTR_LO, A.cinstr[ci]);
     E[E_BAD * np + e] += A.cbad[ci];
+    return ci;
 }
 
 // One nes-py frame of raw console e (fastmario.cpp:656-661); power_on != 0 boots it instead.

@@ -88,9 +88,20 @@ __global__ void __launch_bounds__(EMU_THREADS) k_raw(RawArgs A) {
     if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }
 
+// One wave of 64 envs per block: each lane draws its env's reset, then the wave copies the chosen cache
+// consoles one env at a time with all 64 lanes.
 __global__ void __launch_bounds__(64) k_reset(ResetArgs A) {
-    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)A.n) reset_lane(A, e);
+    const uint32_t e = blockIdx.x * 64 + threadIdx.x;
+    const int ci = e < (uint32_t)A.n ? reset_lane(A, e) : -1;
+    uint64_t m = __ballot(ci >= 0);
+    while (m) {
+        const int l = __builtin_ctzll(m);
+        m &= m - 1;
+        const uint32_t el = (uint32_t)__shfl((int)e, l);
+        const int cl = __shfl(ci, l);
+        copy_console_wave(Region{A.mem, A.sc, A.np, el}, Region{(uint8_t*)A.cmem, (uint32_t*)A.csc, A.ncp, (uint32_t)cl},
+                          threadIdx.x, 64);
+    }
 }
 
 // Observation of a reset-cache entry or a boot state: the boot observation, or the resized last frame.
