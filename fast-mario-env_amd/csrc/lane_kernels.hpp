@@ -122,10 +122,13 @@ __device__ __forceinline__ void area_column(const uint32_t* g0, const uint32_t* 
 }
 
 // ------------------------------------------------------------------ arguments
+constexpr int MAX_CHR_BANKS = 4;   // ROMs per env instance: one PRG, a CHR bank each (the rom_mode variants)
+
 struct RomArgs {
-    const uint8_t* rom;      // 0x8000 PRG (mirrored) + 0x2000 CHR
+    const uint8_t* rom;      // 0x8000 PRG (mirrored) + n_chr x 0x2000 CHR
     const uint8_t* lut;      // 256
     uint32_t nt_bits;        // bit k: name table k maps to VRAM $400
+    int n_chr;               // CHR banks, 1 .. MAX_CHR_BANKS
 };
 
 __device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom, const uint32_t* s_dec) {
@@ -145,10 +148,11 @@ struct LaneCtx {
     uint32_t* gp;     // this lane's gray palette, tile row and OAM (stride LDS_LANES words)
 };
 
-// console e of the memory block `mem` (np consoles)
-__device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* mem, uint32_t np, uint32_t e) {
+// console e of the memory block `mem` (np consoles), on CHR bank `bank` of the staged cartridge
+__device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* mem, uint32_t np, uint32_t e,
+                                       uint32_t bank = 0) {
     c.mem = mem + e; c.vmem = mem + vram_word_offset(np, e, 0); c.np = np;
-    c.cart = x.cart; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
+    c.cart = x.cart; c.cart.chr += bank * 0x2000u; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
     c.lds_bg = x.gp + LDS_GP_WORDS * LDS_LANES; c.bg_key = -1;
     c.lds_oam = x.gp + (LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES;
     c.bad_ops = 0; c.instructions = 0;
@@ -160,6 +164,7 @@ struct BootArgs {
     int nl;
     uint32_t nlp;
     const int* levels;           // 3 * nl
+    const uint8_t* key_bank;     // nl: CHR bank of each (level, ROM) key
     uint8_t* mem; uint32_t* sc;  // boot consoles [row * nlp + l]
     uint8_t* gray;               // frame buffer of nlp lanes (4-pixel words)
     int64_t* x0; int64_t* t0;
@@ -169,6 +174,7 @@ struct BootArgs {
 struct CacheArgs {
     RomArgs R;
     Cfg cfg;
+    const uint8_t* key_bank;     // CHR bank of each (level, ROM) key
     int nl, nk, nc;
     uint32_t nlp, ncp;
     const uint8_t* boot_mem; const uint32_t* boot_sc; const int64_t* x0; const int64_t* t0;
@@ -188,6 +194,7 @@ struct StepArgs {
     uint8_t* gray;                // 2 frame buffers of np lanes (4-pixel words)
     const int64_t* actions;
     float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
+    const uint8_t* key_bank;      // CHR bank of each (level, ROM) key (E_LEVEL)
 };
 
 struct ResetArgs {
@@ -244,7 +251,7 @@ __device__ __forceinline__ void add_counter(uint32_t* E, uint32_t np, uint32_t e
 // Power-on and title sequence with the target level written into RAM (fastmario.cpp:414-445).
 __device__ inline void boot_lane(const BootArgs& A, const LaneCtx& x, int l) {
     Console c;
-    attach(c, x, A.mem, A.nlp, (uint32_t)l);
+    attach(c, x, A.mem, A.nlp, (uint32_t)l, A.key_bank[l]);
     c.gray = A.gray + gray_lane_offset(l); c.render = true;
     c.power_on();
     auto fr = [&](uint8_t b) { c.joy_buttons0 = b; c.frame(); };
@@ -279,7 +286,7 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     Region live{A.mem, A.sc, A.ncp, (uint32_t)ci};
     copy_console(live, boot);
     Console c;
-    attach(c, x, A.mem, A.ncp, (uint32_t)ci);
+    attach(c, x, A.mem, A.ncp, (uint32_t)ci, A.key_bank[lvl]);
     c.load(A.sc, ci);
     EnvRegs ev{};
     ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
@@ -304,7 +311,7 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
 // One agent step of env e (fastmario.cpp:403-411 + 336-374).
 __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e) {
     Console c;
-    attach(c, x, A.mem, A.np, e);
+    attach(c, x, A.mem, A.np, e, A.key_bank[A.ev[(size_t)E_LEVEL * A.np + e]]);
     c.load(A.sc, e);
     EnvRegs ev;
     load_env(ev, A.ev, A.np, e);

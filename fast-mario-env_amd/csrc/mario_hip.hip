@@ -20,18 +20,20 @@ using namespace mh;
 
 namespace {
 
-// Stage PRG + CHR (40 KB), the gray LUT and the decode table in LDS; every thread of the block must call this.
+// Stage PRG and the CHR banks (32 KB + 8 KB each), the gray LUT and the decode table in LDS; every thread of
+// the block must call this.
 __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint8_t* s_lut, uint32_t* s_dec) {
     const uint4* src = (const uint4*)R.rom;
     uint4* dst = (uint4*)s_rom;
-    for (int i = threadIdx.x; i < 0xa000 / 16; i += blockDim.x) dst[i] = src[i];
+    const int words = (0x8000 + R.n_chr * 0x2000) / 16;
+    for (int i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) { s_lut[i] = R.lut[i]; s_dec[i] = kDecode.w[i]; }
     __syncthreads();
 }
 
 // Block-shared LDS of the emulator kernels: the cartridge, the gray LUT and per-lane render buffers.
 #define ROM_LDS                                                     \
-    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0xa000]; \
+    __shared__ __attribute__((aligned(16))) uint8_t s_rom[0x8000 + MAX_CHR_BANKS * 0x2000]; \
     __shared__ uint8_t s_lut[256];                                  \
     __shared__ uint32_t s_dec[256];                                 \
     __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
@@ -228,6 +230,23 @@ __global__ void k_frames_out(const uint8_t* src, uint32_t np, int n, uint8_t* ou
     for (int b = 0; b < 4; b++) out[(size_t)e * GRAY_PIX + 4 * w + b] = (uint8_t)(v >> (8 * b));
 }
 
+// Frame buffer of palette values -> env-major 240x256x3 RGB24 through a 64-entry RGB table (a palette value
+// is taken & 63, as nes-py's screen). Threads: x = env, y = word of 4 pixels.
+__global__ void k_frames_rgb(const uint8_t* src, uint32_t np, int n, const uint8_t* rgb64, uint8_t* out) {
+    __shared__ uint8_t tab[64 * 3];
+    for (int i = threadIdx.x; i < 64 * 3; i += blockDim.x) tab[i] = rgb64[i];
+    __syncthreads();
+    const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
+    const uint32_t w = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (e >= (uint32_t)n || w >= GRAY_PIX / 4) return;
+    const uint32_t v = ((const uint32_t*)src)[(size_t)w * np + e];
+    uint8_t* o = out + ((size_t)e * GRAY_PIX + 4 * w) * 3;
+    for (int b = 0; b < 4; b++) {
+        const uint32_t c = (v >> (8 * b)) & 63u;
+        o[3 * b] = tab[3 * c]; o[3 * b + 1] = tab[3 * c + 1]; o[3 * b + 2] = tab[3 * c + 2];
+    }
+}
+
 // 240x256 gray images (env-major) -> 84x84.
 __global__ void k_resize_images(const uint8_t* src, uint8_t* dst, int n, const AreaTables* T) {
     const int i = blockIdx.y;
@@ -295,6 +314,7 @@ struct MhEnv {
     uint32_t* boot_sc = nullptr;
     int64_t *x0 = nullptr, *t0 = nullptr;
     uint8_t *cmem = nullptr, *cgray = nullptr, *cobs = nullptr, *cboot = nullptr;
+    uint8_t* key_bank = nullptr;     // CHR bank of each (level, ROM) key
     uint32_t *csc = nullptr;
     int64_t *cx = nullptr, *ct = nullptr;
     int32_t *clives = nullptr, *cdraws = nullptr;
@@ -333,37 +353,71 @@ const char* mh_last_error(void) { return g_err.c_str(); }
 MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, const uint8_t* lut,
                  int skip, int max_steps, double sticky, int noop_max, int maxpool, int frame_stack,
                  const uint64_t* rng, int device) {
+    return mh_create_roms(rom, &rom_len, 1, nullptr, n, levels, lut, skip, max_steps, sticky, noop_max, maxpool,
+                          frame_stack, rng, device);
+}
+
+MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, const int32_t* env_rom, int n,
+                      const int* levels, const uint8_t* lut, int skip, int max_steps, double sticky, int noop_max,
+                      int maxpool, int frame_stack, const uint64_t* rng, int device) {
     g_err.clear();
     if (n < 1 || skip < 1 || skip > MAX_SKIP || frame_stack < 1 || frame_stack > 16 || noop_max < 0 ||
-        max_steps < 1 || !(sticky >= 0.0 && sticky <= 1.0) || !levels || !lut || !rng) {
+        max_steps < 1 || !(sticky >= 0.0 && sticky <= 1.0) || !levels || !lut || !rng || !roms || !rom_lens ||
+        n_roms < 1 || n_roms > MAX_CHR_BANKS || (n_roms > 1 && !env_rom)) {
         g_err = "invalid arguments";
         return nullptr;
     }
+    // the cartridge image: ROM 0's PRG, then the CHR of every ROM; the ROMs must agree on PRG and mirroring
     std::vector<uint8_t> img;
     uint16_t nt[4];
-    if (!load_cart(rom, rom_len, img, nt)) return nullptr;
+    int64_t off = 0;
+    for (int r = 0; r < n_roms; r++) {
+        std::vector<uint8_t> one;
+        uint16_t ntr[4];
+        if (!load_cart(roms + off, rom_lens[r], one, ntr)) return nullptr;
+        off += rom_lens[r];
+        if (r == 0) {
+            img.assign(one.begin(), one.begin() + 0x8000);
+            memcpy(nt, ntr, sizeof(nt));
+        } else if (memcmp(img.data(), one.data(), 0x8000) != 0 || memcmp(nt, ntr, sizeof(nt)) != 0) {
+            g_err = "per-env ROMs must share PRG and mirroring (rom_mode variants differ in CHR only)";
+            return nullptr;
+        }
+        img.insert(img.end(), one.begin() + 0x8000, one.begin() + 0xa000);
+    }
+    for (int i = 0; i < n && env_rom; i++)
+        if (env_rom[i] < 0 || env_rom[i] >= n_roms) { g_err = "env ROM index out of range"; return nullptr; }
     CKN(hipSetDevice(device));
     MhEnv* h = new MhEnv();
     auto fail = [&]() -> MhEnv* { delete h; return nullptr; };
     bool good = true;
     h->n = n; h->K = frame_stack; h->device = device; h->np = pad64(n);
     h->cfg = Cfg{skip, max_steps, noop_max, maxpool ? 1 : 0, sticky};
-    // distinct levels in order of first appearance (fastmario.cpp:584-593)
+    // distinct (level, ROM) keys in order of first appearance (levels: fastmario.cpp:584-593); a key has its
+    // own boot state and reset-cache entries
     std::vector<int> lv, env_level(n);
+    std::vector<uint8_t> key_bank;
     for (int i = 0; i < n; i++) {
+        const int ri = env_rom ? env_rom[i] : 0;
         int li = -1;
-        for (size_t k = 0; k < lv.size() / 3; k++)
-            if (lv[3 * k] == levels[3 * i] && lv[3 * k + 1] == levels[3 * i + 1] && lv[3 * k + 2] == levels[3 * i + 2]) li = (int)k;
-        if (li < 0) { li = (int)lv.size() / 3; lv.insert(lv.end(), levels + 3 * i, levels + 3 * i + 3); }
+        for (size_t k = 0; k < key_bank.size(); k++)
+            if (lv[3 * k] == levels[3 * i] && lv[3 * k + 1] == levels[3 * i + 1] && lv[3 * k + 2] == levels[3 * i + 2] &&
+                key_bank[k] == ri) li = (int)k;
+        if (li < 0) {
+            li = (int)key_bank.size();
+            lv.insert(lv.end(), levels + 3 * i, levels + 3 * i + 3);
+            key_bank.push_back((uint8_t)ri);
+        }
         env_level[i] = li;
     }
     h->nl = (int)lv.size() / 3; h->nlp = pad64(h->nl);
     h->nk = noop_max + 1; h->nc = h->nl * h->nk; h->ncp = pad64(h->nc);
     auto& B = h->B;
-    uint8_t* d_rom = B.alloc<uint8_t>(0xa000, good);
+    uint8_t* d_rom = B.alloc<uint8_t>(img.size(), good);
     uint8_t* d_lut = B.alloc<uint8_t>(256, good);
     h->T = B.alloc<AreaTables>(1, good);
     int* d_levels = B.alloc<int>(lv.size(), good);
+    h->key_bank = B.alloc<uint8_t>(key_bank.size(), good);
     h->mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
     h->sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
     h->ev = B.alloc<uint32_t>((size_t)E_COUNT * h->np, good);
@@ -400,22 +454,23 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
         w(E_RNG_HAS32) = (uint32_t)r[4]; w(E_RNG_HALF) = (uint32_t)r[5];
         w(E_LIVES) = 0xffffffffu; w(E_SHOWS_BOOT) = 1; w(E_RESET_IDX) = 0xffffffffu;
     }
-    if (!ok(hipMemcpy(d_rom, img.data(), 0xa000, hipMemcpyHostToDevice), "upload rom") ||
+    if (!ok(hipMemcpy(d_rom, img.data(), img.size(), hipMemcpyHostToDevice), "upload rom") ||
+        !ok(hipMemcpy(h->key_bank, key_bank.data(), key_bank.size(), hipMemcpyHostToDevice), "upload key banks") ||
         !ok(hipMemcpy(d_lut, lut, 256, hipMemcpyHostToDevice), "upload lut") ||
         !ok(hipMemcpy(h->T, &T, sizeof(T), hipMemcpyHostToDevice), "upload tables") ||
         !ok(hipMemcpy(d_levels, lv.data(), lv.size() * sizeof(int), hipMemcpyHostToDevice), "upload levels") ||
         !ok(hipMemcpy(h->ev, ev.data(), ev.size() * 4, hipMemcpyHostToDevice), "upload env words"))
         return fail();
-    h->R.rom = d_rom; h->R.lut = d_lut;
+    h->R.rom = d_rom; h->R.lut = d_lut; h->R.n_chr = n_roms;
     h->R.nt_bits = 0;
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     // boot every level, build the reset cache
-    BootArgs ba{h->R, h->nl, h->nlp, d_levels, h->boot_mem, h->boot_sc, h->boot_gray, h->x0, h->t0, d_err};
+    BootArgs ba{h->R, h->nl, h->nlp, d_levels, h->key_bank, h->boot_mem, h->boot_sc, h->boot_gray, h->x0, h->t0, d_err};
     hipLaunchKernelGGL(k_boot, emu_grid(h->nl), dim3(EMU_THREADS), 0, 0, ba);
     if (!ok(hipGetLastError(), "k_boot launch")) return fail();
     SmallObsArgs so{h->boot_gray, h->nlp, nullptr, nullptr, 1, h->boot_obs, h->nl, h->T};
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nl), dim3(256), 0, 0, so);
-    CacheArgs ca{h->R, h->cfg, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
+    CacheArgs ca{h->R, h->cfg, h->key_bank, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
                  h->cmem, h->csc, h->cgray, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
                  h->cframes, h->cinstr, h->cbad};
     hipLaunchKernelGGL(k_cache, emu_grid(h->nc), dim3(EMU_THREADS), 0, 0, ca);
@@ -467,7 +522,7 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     if (mark(h, s, 0)) return -1;
     StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->ev, h->gray, d_actions,
-                h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len};
+                h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len, h->key_bank};
     hipLaunchKernelGGL(k_step, emu_grid(h->n), dim3(EMU_THREADS), 0, s, sa);
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
@@ -590,7 +645,7 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     for (int i = 0; i < 256; i++) ident[i] = (uint8_t)i;
     if (!ok(hipMemcpy(d_rom, img.data(), 0xa000, hipMemcpyHostToDevice), "upload rom") ||
         !ok(hipMemcpy(d_lut, ident, 256, hipMemcpyHostToDevice), "upload lut")) { delete h; return nullptr; }
-    h->R.rom = d_rom; h->R.lut = d_lut;
+    h->R.rom = d_rom; h->R.lut = d_lut; h->R.n_chr = 1;
     h->R.nt_bits = 0;
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, 1};
@@ -616,6 +671,13 @@ int mh_raw_screen(MhRaw* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
     hipLaunchKernelGGL(k_frames_out, dim3(h->np / 64, GRAY_PIX / 16), dim3(256), 0, (hipStream_t)stream, h->screen,
                        h->np, h->n, d_out);
+    CK(hipGetLastError());
+    return 0;
+}
+int mh_raw_screen_rgb(MhRaw* h, const uint8_t* d_rgb64, uint8_t* d_out, void* stream) {
+    if (!h || !d_rgb64 || !d_out) { g_err = "null handle or buffer"; return -1; }
+    hipLaunchKernelGGL(k_frames_rgb, dim3(h->np / 64, GRAY_PIX / 16), dim3(256), 0, (hipStream_t)stream, h->screen,
+                       h->np, h->n, d_rgb64, d_out);
     CK(hipGetLastError());
     return 0;
 }

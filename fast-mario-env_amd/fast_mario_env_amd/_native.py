@@ -40,6 +40,8 @@ def lib() -> ctypes.CDLL:
     L.mh_last_error.restype = ctypes.c_char_p
     L.mh_create.restype = _P
     L.mh_create.argtypes = [_P, _i64, _i32, _P, _P, _i32, _i32, _dbl, _i32, _i32, _i32, _P, _i32]
+    L.mh_create_roms.restype = _P
+    L.mh_create_roms.argtypes = [_P, _P, _i32, _P, _i32, _P, _P, _i32, _i32, _dbl, _i32, _i32, _i32, _P, _i32]
     L.mh_set_buffers.argtypes = [_P] * 9
     for f in ("mh_reset", "mh_step_wait"):
         getattr(L, f).argtypes = [_P, _P]
@@ -57,6 +59,7 @@ def lib() -> ctypes.CDLL:
     L.mh_raw_frame.argtypes = [_P, _P, _i32, _P]
     for f in ("mh_raw_ram", "mh_raw_screen", "mh_raw_canon"):
         getattr(L, f).argtypes = [_P, _P, _P]
+    L.mh_raw_screen_rgb.argtypes = [_P, _P, _P, _P]
     for f in ("mh_raw_backup", "mh_raw_restore"):
         getattr(L, f).argtypes = [_P, _P]
     for f in ("mh_raw_bad_ops", "mh_raw_instructions"):

@@ -108,9 +108,11 @@ class HipVecEnv:
 
     Args mirror CudaVecEnv: level ("w-s" or a list of N levels), n_envs, seed, sticky, noop_max,
     max_steps, skip, frame_stack, device, rom_path, rom_mode, env_offset (env i uses the PCG64 stream
-    seed*1000 + env_offset + i). Beyond CudaVecEnv: maxpool, any frame_stack in 1..16 and every
-    rom_mode. `block`, `extra_opts`, `kernel` and `render_kernel` select CUDA kernel variants in the
-    reference; they are accepted for compatibility and have no effect here.
+    seed*1000 + env_offset + i). Beyond CudaVecEnv: maxpool, any frame_stack in 1..16, every rom_mode,
+    and a rom_mode per env (a list of N modes; the variants share PRG, so one workgroup holds them all).
+    `rom` gives ROM bytes directly: bytes for every env, or a dict mode -> bytes. `block`, `extra_opts`,
+    `kernel` and `render_kernel` select CUDA kernel variants in the reference; they are accepted for
+    compatibility and have no effect here.
 
     reset() -> obs; step(actions) -> (obs, rew f32, term bool, trunc bool, info). info maps
     INFO_FIELDS to int32 (N,) views of info_t, plus ep_ret f64 / ep_len i32 / final_obs, valid where
@@ -120,16 +122,13 @@ class HipVecEnv:
     def __init__(self, level="1-1", n_envs=1024, seed=0, sticky=0.0, noop_max=0, max_steps=2000, skip=4,
                  frame_stack=4, device="cuda", block=64, rom_path=None, rom_mode="vanilla", extra_opts=(),
                  kernel="v2", env_offset=0, render_kernel="k_render2", maxpool=False, rom=None):
-        torch = self._torch = _torch()
+        # arguments first (ValueError), then the device (RuntimeError without a ROCm GPU)
         if not 1 <= skip <= 16:
             raise ValueError("skip must be in 1..16")
         if not 1 <= frame_stack <= 16:
             raise ValueError("frame_stack must be in 1..16")
         if not 0.0 <= float(sticky) <= 1.0:
             raise ValueError("sticky must be in [0, 1]")
-        self.dev = torch.device(device)
-        if self.dev.index is None:
-            self.dev = torch.device("cuda", torch.cuda.current_device())
         self.n = n = int(n_envs)
         self.num_envs = n
         self.k = frame_stack
@@ -138,18 +137,40 @@ class HipVecEnv:
             raise ValueError(f"got {len(levels)} levels for {n} envs")
         self.levels = levels
         lv = np.array([decode_level(x) for x in levels], np.int32).reshape(-1)
-        rom_bytes = bytes(rom) if rom is not None else load_rom(rom_path, rom_mode)
-        check_rom(rom_bytes)
-        self._rom = np.frombuffer(rom_bytes, np.uint8).copy()
+        modes = [rom_mode] * n if isinstance(rom_mode, str) else list(rom_mode)
+        if len(modes) != n:
+            raise ValueError(f"got {len(modes)} rom modes for {n} envs")
+        distinct = list(dict.fromkeys(modes))           # ROM index = order of first appearance
+        if len(distinct) > 4:
+            raise ValueError(f"at most 4 rom modes per instance, got {len(distinct)}")
+        torch = self._torch = _torch()
+        self.dev = torch.device(device)
+        if self.dev.index is None:
+            self.dev = torch.device("cuda", torch.cuda.current_device())
+        roms = []
+        for m in distinct:
+            if isinstance(rom, dict):
+                b = bytes(rom[m])
+            elif rom is not None:
+                b = bytes(rom)
+            else:
+                b = load_rom(rom_path, m)
+            check_rom(b)
+            roms.append(b)
+        self.rom_modes = modes
+        self._rom = np.frombuffer(b"".join(roms), np.uint8).copy()
+        self._rom_lens = np.array([len(b) for b in roms], np.int64)
+        self._env_rom = np.array([distinct.index(m) for m in modes], np.int32)
         self._lut = gray_lut()
         rng = np.array([rng_state(seed * 1000 + env_offset + i) for i in range(n)], np.uint64).reshape(-1)
         L = lib()
         with torch.cuda.device(self.dev):
-            self.h = L.mh_create(self._rom.ctypes.data, len(self._rom), n, lv.ctypes.data, self._lut.ctypes.data,
-                                 skip, max_steps, float(sticky), int(noop_max), int(bool(maxpool)), frame_stack,
-                                 rng.ctypes.data, self.dev.index)
+            self.h = L.mh_create_roms(self._rom.ctypes.data, self._rom_lens.ctypes.data, len(roms),
+                                      self._env_rom.ctypes.data, n, lv.ctypes.data, self._lut.ctypes.data,
+                                      skip, max_steps, float(sticky), int(noop_max), int(bool(maxpool)), frame_stack,
+                                      rng.ctypes.data, self.dev.index)
         if not self.h:
-            raise RuntimeError(f"mh_create failed: {_native.last_error()}")
+            raise RuntimeError(f"mh_create_roms failed: {_native.last_error()}")
         z = lambda *s, dt: torch.zeros(*s, dtype=dt, device=self.dev)  # noqa: E731
         self.actions = z(n, dt=torch.int64)
         self.obs = z(n, frame_stack, OBS_HW, OBS_HW, dt=torch.uint8)
@@ -402,6 +423,18 @@ class HipRawNES:
     @property
     def screen(self):
         return self._out(lib().mh_raw_screen, (self.n, 240, 256))
+
+    @property
+    def screen_rgb(self):
+        """(N, 240, 256, 3) uint8 RGB24 device tensor: the screen through nes-py's palette, as nes-py's own
+        screen array."""
+        torch = self._torch
+        if getattr(self, "_rgb64", None) is None:
+            self._rgb64 = torch.from_numpy(palette_rgb().reshape(-1).copy()).to(self.dev)
+        out = torch.empty(self.n, 240, 256, 3, dtype=torch.uint8, device=self.dev)
+        check(lib().mh_raw_screen_rgb(self.h, _ptr(self._rgb64), _ptr(out), _stream(torch, self.dev)),
+              "mh_raw_screen_rgb")
+        return out
 
     def canon(self):
         return self._out(lib().mh_raw_canon, (self.n, CANON_BYTES))

@@ -46,6 +46,16 @@ MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, 
                  int skip, int max_steps, double sticky, int noop_max, int maxpool, int frame_stack,
                  const uint64_t* rng, int device);
 
+/* mh_create with a ROM per env: the per-env rom_mode that CudaVecEnv refuses (vec_env.py:250-269) and
+ * FastVecEnv takes once per instance (env.py:113-160, rom.py:46-61). The ROMs are the rom_mode variants
+ * of one game: they must share PRG and mirroring (their CHR differs), at most 4.
+ *   roms          the n_roms iNES images back to back, host memory; rom_lens their sizes
+ *   env_rom       n ints, the ROM index of each env (NULL: every env on ROM 0)
+ * Each distinct (level, ROM) gets its own boot state and reset-cache entries. */
+MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, const int32_t* env_rom, int n,
+                      const int* levels, const uint8_t* lut, int skip, int max_steps, double sticky, int noop_max,
+                      int maxpool, int frame_stack, const uint64_t* rng, int device);
+
 /* Output buffers (device pointers, caller-owned). Replaces fm_set_buffers (fastmario.cpp:603-609).
  *   obs, fin  n * frame_stack * 84 * 84 u8 (stacked observations; final stack of finished episodes)
  *   rew       n f32;  term, trunc  n u8 (0/1);  info  n * 10 i32
@@ -100,6 +110,10 @@ MhRaw*  mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device);
 int     mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream);
 int     mh_raw_ram(MhRaw* h, uint8_t* d_out, void* stream);        /* n * 2048 */
 int     mh_raw_screen(MhRaw* h, uint8_t* d_out, void* stream);     /* n * 240 * 256 palette values */
+/* The screen as RGB24, n * 240 * 256 * 3 bytes, through the 64-entry RGB table d_rgb64 (device, 192 bytes;
+   palette values taken & 63). Replaces reading fm_raw_screen (fastmario.cpp:665) and mapping it through
+   the palette table of fm_palette (fastmario.cpp:632) on the host, which nes-py's RGB screen is. */
+int     mh_raw_screen_rgb(MhRaw* h, const uint8_t* d_rgb64, uint8_t* d_out, void* stream);
 int     mh_raw_canon(MhRaw* h, uint8_t* d_out, void* stream);      /* n * MH_CANON_BYTES */
 int     mh_raw_backup(MhRaw* h, void* stream);
 int     mh_raw_restore(MhRaw* h, void* stream);

@@ -92,6 +92,37 @@ def test_bindings_cover_header():
         assert s in src, f"{s} has no ctypes binding"
 
 
+def test_create_roms_validates_before_the_gpu():
+    """mh_create_roms rejects ROMs that differ in PRG (per-env rom_mode variants differ in CHR only) and a
+    bad env ROM index, with a message, before it touches a device."""
+    L = ctypes.CDLL(_native.lib_path())
+    L.mh_create_roms.restype = ctypes.c_void_p
+    L.mh_last_error.restype = ctypes.c_char_p
+    import fuzz
+    n = 2
+    lv = np.array([1, 1, 1] * n, np.int32)
+    lut = fme.gray_lut()
+    rng = np.zeros(6 * n, np.uint64)
+    P = ctypes.c_void_p
+
+    def create(roms, env_rom):
+        blob = np.frombuffer(b"".join(roms), np.uint8).copy()
+        lens = np.array([len(b) for b in roms], np.int64)
+        er = np.array(env_rom, np.int32)
+        return L.mh_create_roms(P(blob.ctypes.data), P(lens.ctypes.data), len(roms), P(er.ctypes.data), n,
+                                P(lv.ctypes.data), P(lut.ctypes.data), 4, 2000, ctypes.c_double(0.0), 0, 0, 4,
+                                P(rng.ctypes.data), 0)
+    mini = open(rom_path("vanilla"), "rb").read()
+    assert not create([mini, fuzz.program_rom(0)], [0, 1])
+    assert b"share PRG" in L.mh_last_error()
+    assert not create([mini, open(rom_path("pixel"), "rb").read()], [0, 2])
+    assert b"out of range" in L.mh_last_error()
+    with pytest.raises(ValueError, match="rom modes"):
+        fme.HipVecEnv("1-1", 3, rom_mode=["vanilla", "pixel"])
+    with pytest.raises(ValueError, match="at most 4"):
+        fme.HipVecEnv("1-1", 5, rom_mode=["vanilla", "pixel", "downsample", "rectangle", "other"])
+
+
 @pytest.mark.skipif(HAVE_GPU, reason="checks the no-GPU error path")
 def test_no_cpu_fallback():
     """Without a GPU the product raises; there is no silent CPU path."""

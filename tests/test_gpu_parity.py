@@ -24,10 +24,11 @@ def _first_diff(a, b):
     return d[:8].tolist()
 
 
-def _raw_run(rom, n, frames, seed, render_p=0.5, backup_p=0.0):
+def _raw_run(rom, n, frames, seed, render_p=0.5, backup_p=0.0, rgb=False):
     import torch
 
-    from fast_mario_env_amd import HipRawNES
+    from fast_mario_env_amd import HipRawNES, palette_rgb
+    pal = palette_rgb()
     gpu = HipRawNES(rom, n)
     cpu = [OracleRaw(rom) for _ in range(n)]
     rng = np.random.default_rng(seed)
@@ -53,12 +54,16 @@ def _raw_run(rom, n, frames, seed, render_p=0.5, backup_p=0.0):
             assert np.array_equal(canon[i], c.canon()), (f, i, "canon", _first_diff(canon[i], c.canon()))
             if render:
                 assert np.array_equal(scr[i], c.screen), (f, i, "screen", _first_diff(scr[i], c.screen))
+        if render and rgb:   # RGB24 screen (the raw-emulator workload's output): nes-py's palette of the oracle's
+            rgb_gpu = gpu.screen_rgb.cpu().numpy()
+            for i, c in enumerate(cpu):
+                assert np.array_equal(rgb_gpu[i], pal[c.screen & 63]), (f, i, "rgb screen")
     assert gpu.bad_ops() == sum(c.bad_ops() for c in cpu)
     assert gpu.instructions() == sum(c.instructions() for c in cpu)
 
 
 def test_raw_mini_smb():
-    _raw_run(MINI, 8, scaled(120), seed=1)
+    _raw_run(MINI, 8, scaled(120), seed=1, rgb=True)
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
@@ -95,6 +100,38 @@ def _levels(names):
 @pytest.mark.parametrize("config", list(CONFIGS))
 def test_env_vs_oracle(config):
     _env_run(["1-1", "1-1", "4-1", "8-4", "2-3", "1-2", "1-1", "5-2"], config, scaled(150))
+
+
+def test_env_rom_modes_per_env():
+    """A rom_mode per env (the divergence-stress workload's cycling over the four variants): every env against
+    its own one-env oracle on its mode's ROM, with its own PCG64 stream (env_offset = its index)."""
+    import torch
+
+    from build_roms import MODES
+    from fast_mario_env_amd import HipVecEnv
+    kw = CONFIGS["headline"]
+    names = ["1-1", "4-1", "1-1", "8-4", "2-3", "1-1", "1-2", "5-2"]
+    n = len(names)
+    modes = [MODES[i % len(MODES)] for i in range(n)]
+    roms = {m: open(rom_path(m), "rb").read() for m in MODES}
+    gpu = HipVecEnv(names, n, seed=7, rom=roms, rom_mode=modes, **kw)
+    cpu = [OracleVec(roms[modes[i]], _levels([names[i]]), 1, seed=7, env_offset=i, **kw) for i in range(n)]
+    o2 = gpu.reset().cpu().numpy()
+    for i in range(n):
+        assert np.array_equal(cpu[i].reset()[0], o2[i]), (i, "reset obs")
+    rng = np.random.default_rng(131)
+    for t in range(scaled(60)):
+        a = rng.choice(7, n, p=ACTION_P)
+        gpu.step(torch.from_numpy(a).cuda())
+        o2, r2, te2, tr2, i2 = (x.cpu().numpy() for x in (gpu.obs, gpu.rew, gpu.term, gpu.trunc, gpu.info_t))
+        ram = gpu.ram().cpu().numpy()
+        for i in range(n):
+            o1, r1, te1, tr1, i1 = cpu[i].step(a[i:i + 1])
+            assert r1[0] == r2[i] and te1[0] == te2[i] and tr1[0] == tr2[i], (t, i, modes[i], "reward/done")
+            assert np.array_equal(i1[0], i2[i]), (t, i, modes[i], "info")
+            assert np.array_equal(cpu[i].ram(0), ram[i]), (t, i, modes[i], "ram")
+            assert np.array_equal(o1[0], o2[i]), (t, i, modes[i], "obs")
+    assert gpu.bad_ops() == 0
 
 
 def test_env_vs_oracle_two_waves():
