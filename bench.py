@@ -125,6 +125,46 @@ def cpu_baseline(rom, seconds):
                       f"wrapper settings; {model}; load1 {load1}"}
 
 
+def run_ppo(args, rom, rom_name, rom_sha):
+    """PPO rollout workload (config 5): the headline envs feeding a random-init bf16 Nature CNN, Gumbel-max
+    actions from seed 3, 128-step rollouts with frame-deduplicated storage and GAE (0.99, 0.95)."""
+    import torch
+
+    from fast_mario_env_amd import HipVecEnv
+    from fast_mario_env_amd.rollout import Rollout, make_net
+    n, T = args.envs, args.ppo_steps
+    env = HipVecEnv("1-1", n, seed=0, sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4,
+                    maxpool=True, rom=rom, device="cuda:0")
+    env.reset()
+    net = make_net(seed=0)
+    warm = Rollout(env, net, T=4, seed=3)
+    warm.collect()
+    warm.advantages()
+    del warm
+    ro = Rollout(env, net, T=T, seed=3)
+    torch.cuda.synchronize()
+    log(f"PPO rollout: {n} envs x {T} steps")
+    t0 = time.perf_counter()
+    env_ms = ro.collect()
+    adv, ret = ro.advantages()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out = {
+        "metric": "end-to-end env-steps/sec of a PPO rollout (bf16 Nature CNN policy) at 32768 envs on 1 MI355X",
+        "value": round(n * T / dt, 1), "unit": "env-steps/s", "n_gpus": 1, "steps": T, "warmup": 4,
+        "ms_per_step": round(dt * 1e3 / T, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8 env / bf16 policy", "data": "synthetic",
+        "config": {"workload": "ppo rollout: headline envs + Nature CNN, 128-step rollouts", "envs": n,
+                   "rollout_steps": T, "rom": rom_name, "rom_sha1": rom_sha, "policy": "Nature CNN, random init, bf16",
+                   "sampling": "Gumbel-max, torch.Generator seed 3", "gae": [0.99, 0.95],
+                   "storage": "newest frame per step (frame-deduplicated)"},
+        "env_share": round(env_ms / (dt * 1e3), 4), "env_ms_per_step": round(env_ms / T, 3),
+        "rollout_storage_gb": round(ro.frames.numel() / 1e9, 2),
+    }
+    env.close()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -136,6 +176,9 @@ def main():
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=["headline", "ppo"], default="headline",
+                    help="headline: the env step (default); ppo: a PPO rollout feeding a Nature CNN (config 5)")
+    ap.add_argument("--ppo-steps", type=int, default=128, help="rollout length of --workload ppo")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -149,6 +192,9 @@ def main():
     from fast_mario_env_amd import HipVecEnv
     rom, rom_name = pick_rom()
     rom_sha = hashlib.sha1(rom).hexdigest()[:12]
+    if args.workload == "ppo":
+        run_ppo(args, rom, rom_name, rom_sha)
+        return
     n = args.envs
     log(f"creating {n} envs on {torch.cuda.get_device_name(0)} ({rom_name})")
     t0 = time.perf_counter()

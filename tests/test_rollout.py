@@ -1,0 +1,104 @@
+"""PPO rollout harness (config 5 of the build's workloads; the reference's ppo/train.py rollout and GAE,
+train.py:140-150): GAE against its recurrence written out element by element, the frame-deduplicated
+stack rebuild against explicit frame stacking, and on the GPU a rollout whose stored observations and
+actions are replayed through a second env."""
+import numpy as np
+import pytest
+import torch
+
+from fast_mario_env_amd.rollout import Rollout, gae, gae_reference
+
+
+def test_gae_matches_recurrence():
+    rng = np.random.default_rng(5)
+    T, n = 9, 6
+    rew = rng.normal(size=(T, n)).astype(np.float32)
+    val = rng.normal(size=(T, n)).astype(np.float32)
+    start = rng.random((T, n)) < 0.25
+    nv = rng.normal(size=n).astype(np.float32)
+    ns = rng.random(n) < 0.3
+    a, r = gae(torch.from_numpy(rew), torch.from_numpy(val), torch.from_numpy(start), torch.from_numpy(nv),
+               torch.from_numpy(ns), 0.99, 0.95)
+    ea, er = gae_reference(rew, val, start, nv, ns, 0.99, 0.95)
+    assert np.allclose(a.numpy(), ea, rtol=1e-5, atol=1e-5) and np.allclose(r.numpy(), er, rtol=1e-5, atol=1e-5)
+    # closed forms: no episode starts and lam = 1 -> discounted return minus value; lam = 0 -> one-step TD error
+    s0 = np.zeros((T, n), bool)
+    a1, _ = gae(torch.from_numpy(rew), torch.from_numpy(val), torch.from_numpy(s0), torch.from_numpy(nv),
+                torch.zeros(n, dtype=torch.bool), 0.9, 1.0)
+    disc = np.zeros((T, n)); g = nv.astype(np.float64)
+    for t in reversed(range(T)):
+        g = rew[t] + 0.9 * g; disc[t] = g
+    assert np.allclose(a1.numpy(), disc - val, rtol=1e-4, atol=1e-4)
+    a0, _ = gae(torch.from_numpy(rew), torch.from_numpy(val), torch.from_numpy(s0), torch.from_numpy(nv),
+                torch.zeros(n, dtype=torch.bool), 0.9, 0.0)
+    nxt = np.concatenate([val[1:], nv[None]], 0)
+    assert np.allclose(a0.numpy(), rew + 0.9 * nxt - val, rtol=1e-5, atol=1e-5)
+
+
+class _Stacker:
+    """Explicit frame stacking of k frames with resets to [0, ..., 0, frame]."""
+    def __init__(self, n, k):
+        self.s = np.zeros((n, k, 84, 84), np.uint8)
+
+    def push(self, frame, reset):
+        self.s[:, :-1] = np.where(reset[:, None, None, None], 0, self.s[:, 1:])
+        self.s[:, -1] = frame
+        return self.s.copy()
+
+
+def test_stack_rebuild_from_newest_frames():
+    rng = np.random.default_rng(7)
+    n, k, T = 5, 4, 11
+    st = _Stacker(n, k)
+    # history before the rollout, then the rollout's steps
+    for _ in range(3):
+        st.push(rng.integers(0, 255, (n, 84, 84), np.uint8), rng.random(n) < 0.3)
+    ro = Rollout.__new__(Rollout)
+    ro.torch, ro.k, ro.T = torch, k, T
+    ro.frames = torch.zeros(T, n, 84, 84, dtype=torch.uint8)
+    ro.start = torch.zeros(T, n, dtype=torch.bool)
+    stacks = []
+    for t in range(T):
+        f = rng.integers(0, 255, (n, 84, 84), np.uint8)
+        reset = rng.random(n) < 0.3
+        if t == 0:
+            reset[:] = False
+        s = st.push(f, reset)
+        if t == 0:
+            ro.first = torch.from_numpy(s.copy())
+        ro.frames[t] = torch.from_numpy(f)
+        ro.start[t] = torch.from_numpy(reset)
+        stacks.append(s)
+    for t in range(T):
+        assert np.array_equal(ro.obs(t).numpy(), stacks[t]), t
+
+
+@pytest.mark.gpu
+def test_rollout_replays_through_a_second_env():
+    from build_roms import rom_path
+    from fast_mario_env_amd import HipVecEnv
+    from fast_mario_env_amd.rollout import make_net
+    rom = open(rom_path("vanilla"), "rb").read()
+    kw = dict(seed=0, sticky=0.25, noop_max=30, max_steps=16, skip=4, frame_stack=4, maxpool=True, rom=rom)
+    n, T = 40, 24
+    env = HipVecEnv("1-1", n, **kw)
+    env.reset()
+    net = make_net(seed=0)
+    ro = Rollout(env, net, T=T, seed=3)
+    ro.collect()
+    assert ro.start[1:].any(), "the time limit should end some episodes inside the rollout"
+    twin = HipVecEnv("1-1", n, **kw)
+    twin.reset()
+    for t in range(T):
+        assert torch.equal(ro.obs(t), twin.obs), t
+        _, rew, term, trunc, _ = twin.step(ro.act[t])
+        assert torch.equal(rew, ro.rew[t]), t
+        nxt = ro.start[t + 1] if t + 1 < T else ro.next_start
+        assert torch.equal(term | trunc, nxt), t
+    # the stored values and log-probs are the policy's on the rebuilt observations (same batch, same weights)
+    lp_all = torch.log_softmax(net(ro.obs(T - 1))[0], -1)
+    assert torch.allclose(lp_all.gather(-1, ro.act[T - 1][:, None]).squeeze(-1), ro.logp[T - 1], atol=1e-3)
+    adv, ret = ro.advantages()
+    ea, er = gae_reference(*(x.cpu().numpy() for x in (ro.rew, ro.val, ro.start, ro.next_val, ro.next_start)))
+    assert np.allclose(adv.cpu().numpy(), ea, rtol=1e-4, atol=1e-4)
+    env.close(); twin.close()
