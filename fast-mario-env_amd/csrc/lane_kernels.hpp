@@ -83,41 +83,72 @@ __device__ __forceinline__ uint8_t area_pixel(const Image& g0, const Image& g1, 
     return round_sat(acc);
 }
 
-// INTER_AREA column dx of one image of a frame buffer (4-pixel words, word w of lane e at w np + e),
-// max-pooled with a second one if `pool`: out[dy * ostride] = output pixel (dy, dx) for dy = 0..83.
-// The float operations and their order are area_pixel's. A column's taps are at most 5 consecutive
-// source pixels (scale 256 / 84), so one source row needs two words per image.
-__device__ __forceinline__ void area_column(const uint32_t* g0, const uint32_t* g1, uint32_t np, uint32_t e,
-                                            bool pool, int dx, const AreaTables* T, uint8_t* out, size_t ostride) {
-    const int nx = T->xn[dx];
-    const int x0 = T->xs[dx * TAPS];
-    float w[5];
+// bytewise max of two words (in 16-bit lanes: 256 + a - b has bit 8 set exactly when a >= b)
+__device__ __forceinline__ uint32_t max_u8x4(uint32_t a, uint32_t b) {
+    const uint32_t a0 = a & 0x00ff00ffu, b0 = b & 0x00ff00ffu, a1 = (a >> 8) & 0x00ff00ffu, b1 = (b >> 8) & 0x00ff00ffu;
+    const uint32_t t0 = ((a0 | 0x01000100u) - b0) & 0x01000100u, t1 = ((a1 | 0x01000100u) - b1) & 0x01000100u;
+    const uint32_t k0 = t0 - (t0 >> 8), k1 = t1 - (t1 >> 8);
+    return ((a0 & k0) | (b0 & ~k0)) | (((a1 & k1) | (b1 & ~k1)) << 8);
+}
+__device__ __forceinline__ uint32_t pick4(const uint32_t (&m)[4], uint32_t i) {
+    return i == 0 ? m[0] : i == 1 ? m[1] : i == 2 ? m[2] : m[3];
+}
+
+// INTER_AREA output columns 4 chunk .. 4 chunk + 3 of one image of a frame buffer (4-pixel words, word w of
+// lane e at w np + e), max-pooled with a second one if `pool`: out[dy * row_stride + q * col_stride] =
+// output pixel (dy, 4 chunk + q). The float operations and their order are area_pixel's. The four
+// columns' taps (at most 4 consecutive source pixels each) lie in 4 consecutive words of a source row, so
+// a row is 4 word loads per image; a source row shared by two output rows is summed once.
+__device__ __forceinline__ void area_columns4(const uint32_t* g0, const uint32_t* g1, uint32_t np, uint32_t e,
+                                              bool pool, int chunk, const AreaTables* T, uint8_t* out,
+                                              size_t col_stride, size_t row_stride) {
+    const int c0 = 4 * chunk;
+    const uint32_t wl = (uint32_t)T->xs[c0 * TAPS] >> 2;
+    int nx[4];
+    uint32_t iq[4], sh[4];
+    float w[4][4];
 #pragma unroll
-    for (int k = 0; k < 5; k++) w[k] = T->xw[dx * TAPS + k];
-    const uint32_t sh = (uint32_t)(x0 & 3) * 8, wa = (uint32_t)x0 >> 2, wb = wa < 63 ? wa + 1 : 63;
+    for (int q = 0; q < 4; q++) {
+        const uint32_t rel = (uint32_t)T->xs[(c0 + q) * TAPS] - 4 * wl;
+        nx[q] = T->xn[c0 + q];
+        iq[q] = rel >> 2;
+        sh[q] = (rel & 3) * 8;
+#pragma unroll
+        for (int k = 0; k < 4; k++) w[q][k] = T->xw[(c0 + q) * TAPS + k];
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, rs[4] = {0.f, 0.f, 0.f, 0.f};
+    int last_sy = -1;
     for (int dy = 0; dy < 84; dy++) {
         const int ny = T->yn[dy];
-        float acc = 0.f;
         for (int j = 0; j < ny; j++) {
-            const uint32_t sy = (uint32_t)T->ys[dy * TAPS + j];
-            const size_t ia = (size_t)(sy * 64 + wa) * np + e, ib = (size_t)(sy * 64 + wb) * np + e;
-            const uint64_t v0 = ((uint64_t)g0[ia] | (uint64_t)g0[ib] << 32) >> sh;
-            uint64_t v1 = 0;
-            if (pool) v1 = ((uint64_t)g1[ia] | (uint64_t)g1[ib] << 32) >> sh;
-            float row = 0.f;
+            const int sy = T->ys[dy * TAPS + j];
+            if (sy != last_sy) {
+                uint32_t m[4];
 #pragma unroll
-            for (int k = 0; k < 5; k++) {
-                if (k < nx) {
-                    uint32_t s = (uint32_t)(v0 >> (8 * k)) & 0xffu;
-                    const uint32_t s1 = (uint32_t)(v1 >> (8 * k)) & 0xffu;
-                    if (pool && s1 > s) s = s1;
-                    row += (float)s * w[k];
+                for (int i = 0; i < 4; i++) {
+                    const size_t wi = (size_t)((uint32_t)sy * 64 + (wl + i < 63 ? wl + i : 63)) * np + e;
+                    m[i] = pool ? max_u8x4(g0[wi], g1[wi]) : g0[wi];
                 }
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint64_t win = ((uint64_t)pick4(m, iq[q] < 3 ? iq[q] + 1 : 3) << 32 | pick4(m, iq[q])) >> sh[q];
+                    float row = 0.f;
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        if (k < nx[q]) row += (float)(uint32_t)((win >> (8 * k)) & 0xffu) * w[q][k];
+                    rs[q] = row;
+                }
+                last_sy = sy;
             }
-            const float term = T->yw[dy * TAPS + j] * row;
-            acc = j == 0 ? term : acc + term;
+            const float yw = T->yw[dy * TAPS + j];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float term = yw * rs[q];
+                acc[q] = j == 0 ? term : acc[q] + term;
+            }
         }
-        out[(size_t)dy * ostride] = round_sat(acc);
+#pragma unroll
+        for (int q = 0; q < 4; q++) out[(size_t)dy * row_stride + (size_t)q * col_stride] = round_sat(acc[q]);
     }
 }
 

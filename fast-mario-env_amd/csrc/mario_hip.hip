@@ -3,7 +3,7 @@
 // One agent step of N envs is four kernels on the caller's stream:
 //   k_step          one lane per env: sticky draw, K frames of 6502 + catch-up PPU, reward/done/info,
 //                   hack frames, gray rendering of every frame into two alternating frame buffers
-//   k_obs           one thread per (env, output column): 2-frame max + INTER_AREA 256x240 -> 84x84
+//   k_obs           one thread per (env, 4 output columns): 2-frame max + INTER_AREA 256x240 -> 84x84
 //   k_reset         one lane per env: finished envs take a cached (level, no-op count) start state
 //   k_stack         LDS-transposed frame-stack shift, final_obs, reset observation
 #include <hip/hip_runtime.h>
@@ -135,24 +135,25 @@ struct ObsArgs {
 // New observation of every env: the boot observation right after a reset, else INTER_AREA of the last
 // frame, max-pooled with its partner frame (fastmario.cpp:377-386). E_POOLED bit 0: pool; bit 1: the
 // last frame is in frame buffer 1 (the episode ended at an agent frame of the other parity than K-1).
-// Threads: x = env (64 per block), y = output column (4 per block); the grid's x walks the 21 column
-// groups of one env group first, so the source words the groups share are still in the L2.
-__global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
+// Threads: x = env (64 per block), y = a chunk of 4 output columns (3 per block, 7 blocks per env group);
+// the grid's x walks the chunks of one env group first, so the source words they share are still in the L2.
+__global__ void __launch_bounds__(192) k_obs(ObsArgs A) {
     const uint32_t e = blockIdx.y * 64 + (threadIdx.x & 63);
-    const int dx = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (e >= (uint32_t)A.n || dx >= 84) return;
-    uint8_t* out = A.out + (size_t)dx * A.np + e;
-    const size_t ostride = (size_t)84 * A.np;
+    const int chunk = blockIdx.x * 3 + (threadIdx.x >> 6);
+    if (e >= (uint32_t)A.n || chunk >= 21) return;
+    uint8_t* out = A.out + (size_t)(4 * chunk) * A.np + e;
+    const size_t row_stride = (size_t)84 * A.np;
     if (A.ev[(size_t)E_SHOWS_BOOT * A.np + e]) {
-        const uint8_t* src = A.boot_obs + (size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + dx;
-        for (int dy = 0; dy < 84; dy++) out[(size_t)dy * ostride] = src[dy * 84];
+        const uint8_t* src = A.boot_obs + (size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + 4 * chunk;
+        for (int dy = 0; dy < 84; dy++)
+            for (int q = 0; q < 4; q++) out[(size_t)dy * row_stride + (size_t)q * A.np] = src[dy * 84 + q];
         return;
     }
     const uint32_t pw = A.ev[(size_t)E_POOLED * A.np + e];
     const uint32_t* g0 = (const uint32_t*)A.gray;
     const uint32_t* g1 = (const uint32_t*)(A.gray + (size_t)GRAY_PIX * A.np);
     if (pw & 2) { const uint32_t* t = g0; g0 = g1; g1 = t; }
-    area_column(g0, g1, A.np, e, (pw & 1) != 0, dx, A.T, out, ostride);
+    area_columns4(g0, g1, A.np, e, (pw & 1) != 0, chunk, A.T, out, A.np, row_stride);
 }
 
 struct StackArgs {
@@ -527,7 +528,7 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
     ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
-    hipLaunchKernelGGL(k_obs, dim3(84 / 4, h->np / 64), dim3(256), 0, s, oa);
+    hipLaunchKernelGGL(k_obs, dim3(7, h->np / 64), dim3(192), 0, s, oa);
     CK(hipGetLastError());
     if (mark(h, s, 2)) return -1;
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(0));
