@@ -926,14 +926,26 @@ struct Console {
     __device__ __forceinline__ bool instruction(int32_t j, int32_t tgt, bool pf, uint8_t op, uint8_t q1, uint8_t q2) {
         using namespace dec;
         if (!pf && ppu_calls < tgt) return false;
-        if (!pf) op = read(pc);
-        const uint32_t D = cart.dec[op];
-        const uint32_t xop0 = (D >> X_SH) & 15u;
         uint8_t b1 = q1, b2 = q2;
-        if (!pf && xop0 != X_JSR && xop0 != X_BRANCH) {   // JSR and branches fetch below, in their order
-            const uint32_t am0 = D & 15u;
-            if (am0 != M_NONE) b1 = read((uint16_t)(pc + 1));
-            if (am0 == M_ABS || am0 == M_ABSX || am0 == M_ABSY) b2 = read((uint16_t)(pc + 2));
+        uint32_t D;
+        if (!pf) {
+            // Opcode and operand bytes through the bus. Their loads are waited for inside this branch: a wait
+            // where the paths join would also wait for every store still in flight from earlier instructions.
+            uint32_t o = read(pc);
+            in_register(o);
+            op = (uint8_t)o;
+            D = cart.dec[op];
+            const uint32_t xop0 = (D >> X_SH) & 15u;
+            if (xop0 != X_JSR && xop0 != X_BRANCH) {   // JSR and branches fetch below, in their order
+                const uint32_t am0 = D & 15u;
+                uint32_t t1 = b1, t2 = b2;
+                if (am0 != M_NONE) t1 = read((uint16_t)(pc + 1));
+                if (am0 == M_ABS || am0 == M_ABSX || am0 == M_ABSY) t2 = read((uint16_t)(pc + 2));
+                in_register(t1); in_register(t2);
+                b1 = (uint8_t)t1; b2 = (uint8_t)t2;
+            }
+        } else {
+            D = cart.dec[op];
         }
         const uint32_t am = D & 15u, xop = (D >> X_SH) & 15u, dst = (D >> DST_SH) & 7u;
         const bool rd = (D & RD) != 0, wr = dst == D_MEM;
