@@ -147,6 +147,41 @@ __device__ inline void copy_console_wave(const Region& dst, const Region& src, u
         dst.sc[(size_t)w * dst.np + dst.idx] = src.sc[(size_t)w * src.np + src.idx];
 }
 
+// The memory rows of copy_console (not the register words), by one lane: the loads of a batch of 32 are
+// issued before its stores, so the lane keeps 32 accesses in flight instead of waiting for each one.
+__device__ inline void copy_rows_lane(const Region& dst, const Region& src) {
+    constexpr uint32_t B = 32, BYTE_ROWS = MEM_ROWS - 2048;   // the VRAM span aside
+    static_assert(BYTE_ROWS % B == 0 && ROW_VRAM % B == 0 && 512 % B == 0, "batches must not straddle the VRAM span");
+    for (uint32_t i0 = 0; i0 < BYTE_ROWS; i0 += B) {
+        const uint32_t r0 = i0 < (uint32_t)ROW_VRAM ? i0 : i0 + 2048;
+        uint8_t t[B];
+#pragma unroll
+        for (uint32_t b = 0; b < B; b++) t[b] = src.mem[(size_t)(r0 + b) * src.np + src.idx];
+#pragma unroll
+        for (uint32_t b = 0; b < B; b++) dst.mem[(size_t)(r0 + b) * dst.np + dst.idx] = t[b];
+    }
+    for (uint32_t w0 = 0; w0 < 512; w0 += B) {
+        uint32_t t[B];
+#pragma unroll
+        for (uint32_t b = 0; b < B; b++) t[b] = *(const uint32_t*)(src.mem + vram_word_offset(src.np, src.idx, w0 + b));
+#pragma unroll
+        for (uint32_t b = 0; b < B; b++) *(uint32_t*)(dst.mem + vram_word_offset(dst.np, dst.idx, w0 + b)) = t[b];
+    }
+}
+
+// Snapshot of a console between two frames into `dst` (a region of the same np, at the console's own
+// index): store() of the registers (and of the LDS copy of OAM into the console's rows), then its rows.
+__device__ inline void save_console(Console& c, const Region& live, const Region& dst) {
+    c.store(dst.sc, dst.idx);
+    copy_rows_lane(dst, live);
+}
+// The console as snapshotted: rows back, then load() of the registers (OAM to LDS, derived caches reset).
+// The instruction and bad-op counters are not part of the snapshot and keep counting.
+__device__ inline void restore_console(Console& c, const Region& live, const Region& src) {
+    copy_rows_lane(live, src);
+    c.load(src.sc, src.idx);
+}
+
 // One env's layer state in registers.
 struct EnvRegs {
     int64_t x_last, time_last;
@@ -165,7 +200,13 @@ struct Stepper {
     Pcg* rng;             // null: draws are counted, not taken (reset cache: action 0 == prev 0)
     uint8_t* gray0;       // frame buffer of frames K-1, K-3, ... of the agent step
     uint8_t* gray1;       // frame buffer of frames K-2, K-4, ...
+    Region live;          // the console's own rows and register words
+    uint8_t* snap_mem;    // two snapshot slots of live's layout: rows of slot s at snap_mem + s MEM_ROWS np,
+    uint32_t* snap_sc;    // register words at snap_sc + s S_COUNT np
 
+    __device__ __forceinline__ Region snap(int s) const {
+        return Region{snap_mem + (size_t)s * MEM_ROWS * live.np, snap_sc + (size_t)s * S_COUNT * live.np, live.np, live.idx};
+    }
     __device__ __forceinline__ bool busy() { return smb_busy(c) || smb_world_over(c); }
     // _skip_change_area before the _skip_occupied_states loop (fastmario.cpp:297-300)
     __device__ __forceinline__ void fix_change_area() {
@@ -194,73 +235,83 @@ struct Stepper {
     // with the hack frames of _skip_change_area / _skip_occupied_states (fastmario.cpp:297-308) after
     // every agent frame that did not end the episode.
     //
-    // When an observation is wanted, every agent frame (with its hack frames) is rendered, alternately
-    // into gray1 and gray0 so that frame K-1 lands in gray0 and K-2 in gray1. The reference renders only
-    // those two and, when the episode ends at an earlier frame `last`, restores its per-frame snapshots
-    // and re-emulates frame last-1 (with its hack frames, for the max-pool partner) and frame last with
-    // pixels on. Emulation is deterministic, so those re-emulated frames are exactly the frames already
-    // rendered here: the observation is taken from the two buffers (ev.slot_swap says which one holds
-    // `last`), and the counters add what the re-emulation would count. Written as a state machine
-    // around ONE console frame so that the emulator is inlined once.
+    // When an observation is wanted, frames K-1 and (max-pool) K-2 are rendered with their hack frames,
+    // K-1 into gray0 and K-2 into gray1. Before every frame that a re-emulation could start from, the
+    // console is snapshotted into slot (frame & 1). When the episode ends at a frame last < K-1, the
+    // snapshot of frame last-1 (max-pool, last >= 1) or of frame last is restored and those frames run
+    // again with pixels on, last-1 with its hack frames, as in fastmario.cpp:351-362; the re-emulated
+    // frames count like any other. Written as a state machine around ONE console frame so that the
+    // emulator is inlined once: a lane that re-emulates does so while the other lanes of its wave still
+    // run their remaining agent frames.
     __device__ __forceinline__ double agent_step(int act0, bool want_obs, bool* term) {
         const int K = cfg.skip;
         const bool mp = cfg.maxpool != 0;
         double total = 0.0;
-        bool done = false, hack = false;
+        bool done = false, hack = false, render = false;
         int i = 0, guard = 0;
-        bool render = false;
+        int rf = -1;                       // agent frame being re-emulated (-1: the first pass)
+        uint8_t b_prev = 0, b_cur = 0;     // buttons of agent frames i-1 and i
         uint8_t* slot = gray0;
-        // frames, bad ops and instructions of agent frames i (cur_*) and i - 1 (prev_*), hack frames included
-        uint32_t cur_f = 0, cur_b = 0, cur_n = 0, prev_f = 0, prev_b = 0, prev_n = 0, b0 = 0, n0 = 0;
         for (;;) {
             uint8_t buttons = 0;
-            if (!hack) {
+            if (hack) {
+                c.st(ROW_RAM + 0x7a0, 0);
+            } else if (rf < 0) {
                 int act = act0;
                 if (cfg.sticky != 0.0) {
                     if (rng) { if (rng->random() < cfg.sticky) act = ev.prev; }
                     else ev.draws++;
                 }
                 ev.prev = act;
-                render = want_obs;
+                b_prev = b_cur; b_cur = kButtons[act];
+                buttons = b_cur;
+                render = want_obs && (i == K - 1 || (mp && i == K - 2));
                 slot = ((K - 1 - i) & 1) ? gray1 : gray0;
-                buttons = kButtons[act];
-                cur_f = 0; b0 = c.bad_ops; n0 = c.instructions;
+                // re-emulations start at frame last-1 (max-pool, last >= 1) or last, for last < K-1
+                if (want_obs && i < K - 1 && (!mp || i == 0 || i <= K - 3)) save_console(c, live, snap(i & 1));
             } else {
-                c.st(ROW_RAM + 0x7a0, 0);
+                buttons = rf == i ? b_cur : b_prev;
+                render = true;
+                slot = ((K - 1 - rf) & 1) ? gray1 : gray0;
             }
             c.joy_buttons0 = buttons;
             c.render = render;
             c.gray = slot;
             c.frame();
             ev.frames++;
-            cur_f++;
             if (render) ev.shows_boot = false;
-            if (!hack) {
-                total += frame_reward(&done);
-                if (!done) { fix_change_area(); guard = 0; }
+            if (rf < 0) {
+                if (!hack) {
+                    total += frame_reward(&done);
+                    if (!done) { fix_change_area(); guard = 0; }
+                }
+                if (!done && busy()) {
+                    if (++guard <= HACK_FRAME_LIMIT) { hack = true; continue; }
+                    c.bad_ops |= ERR_HACK_LIMIT;
+                }
+                hack = false;
+                if (!done && i < K - 1) { i++; continue; }
+                // the first pass ended at agent frame i
+                if (!(want_obs && done && i < K - 1)) break;
+                rf = (mp && i >= 1) ? i - 1 : i;
+                restore_console(c, live, snap(rf & 1));
+            } else if (rf < i) {
+                // frame last-1 again, then its hack frames (it did not end the episode)
+                if (!hack) { fix_change_area(); guard = 0; }
+                if (busy()) {
+                    if (++guard <= HACK_FRAME_LIMIT) { hack = true; continue; }
+                    c.bad_ops |= ERR_HACK_LIMIT;
+                }
+                hack = false;
+                rf++;
+            } else {
+                break;
             }
-            if (!done && busy()) {
-                if (++guard <= HACK_FRAME_LIMIT) { hack = true; continue; }
-                c.bad_ops |= ERR_HACK_LIMIT;
-            }
-            hack = false;
-            // agent frame i (and its hack frames) is complete
-            cur_b = c.bad_ops - b0; cur_n = c.instructions - n0;
-            if (done || i == K - 1) break;
-            prev_f = cur_f; prev_b = cur_b; prev_n = cur_n;
-            i++;
         }
         const int last = i;
         if (want_obs) {
             ev.pooled = mp && last >= 1;
             ev.slot_swap = ((K - 1 - last) & 1) != 0;
-            if (done && last < K - 1) {
-                // the reference's re-emulation: frame last - 1 with its hack frames (max-pool), frame last
-                const bool two = mp && last >= 1;
-                ev.frames += 1 + (two ? prev_f : 0);
-                c.bad_ops += (cur_b & ~ERR_HACK_LIMIT) + (two ? (prev_b & ~ERR_HACK_LIMIT) : 0);
-                c.instructions += cur_n + (two ? prev_n : 0);
-            }
         }
         bool tm = done;
         int life = (int)ev.info.v[2];

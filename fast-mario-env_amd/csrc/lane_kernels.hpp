@@ -211,6 +211,7 @@ struct CacheArgs {
     const uint8_t* boot_mem; const uint32_t* boot_sc; const int64_t* x0; const int64_t* t0;
     uint8_t* mem; uint32_t* sc;          // cache consoles [row * ncp + c]
     uint8_t* gray;                       // 2 frame buffers of ncp lanes (4-pixel words)
+    uint8_t* snap_mem; uint32_t* snap_sc;  // 2 snapshot slots of the cache consoles' layout
     int64_t* cx; int64_t* ct; int32_t* clives; int32_t* cdraws; uint8_t* cboot;
     uint64_t* cframes; uint64_t* cinstr; uint32_t* cbad;
 };
@@ -223,6 +224,7 @@ struct StepArgs {
     uint8_t* mem; uint32_t* sc;
     uint32_t* ev;                 // env words [w * np + e]
     uint8_t* gray;                // 2 frame buffers of np lanes (4-pixel words)
+    uint8_t* snap_mem; uint32_t* snap_sc;   // 2 snapshot slots of the live layout (re-emulation)
     const int64_t* actions;
     float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
     const uint8_t* key_bank;      // CHR bank of each (level, ROM) key (E_LEVEL)
@@ -322,7 +324,8 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     EnvRegs ev{};
     ev.x_last = A.x0[lvl]; ev.time_last = A.t0[lvl];
     ev.prev = 0; ev.lives = -1; ev.shows_boot = true; ev.frames = 0; ev.draws = 0;
-    Stepper stp{c, ev, A.cfg, nullptr, A.gray + gray_lane_offset(ci), A.gray + (size_t)GRAY_PIX * A.ncp + gray_lane_offset(ci)};
+    Stepper stp{c, ev, A.cfg, nullptr, A.gray + gray_lane_offset(ci), A.gray + (size_t)GRAY_PIX * A.ncp + gray_lane_offset(ci),
+                live, A.snap_mem, A.snap_sc};
     for (int j = 0; j < k; j++) {
         bool term;
         stp.agent_step(0, j == k - 1, &term);
@@ -350,7 +353,8 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     rng.load(A.ev, A.np, e);
     int64_t a64 = A.actions[e];
     const int act = (a64 >= 0 && a64 < 7) ? (int)a64 : 0;
-    Stepper stp{c, ev, A.cfg, &rng, A.gray + gray_lane_offset(e), A.gray + (size_t)GRAY_PIX * A.np + gray_lane_offset(e)};
+    Stepper stp{c, ev, A.cfg, &rng, A.gray + gray_lane_offset(e), A.gray + (size_t)GRAY_PIX * A.np + gray_lane_offset(e),
+                Region{A.mem, A.sc, A.np, e}, A.snap_mem, A.snap_sc};
     bool tm;
     double r = stp.agent_step(act, true, &tm);
     ev.t++;

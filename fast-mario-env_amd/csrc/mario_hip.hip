@@ -311,12 +311,16 @@ struct MhEnv {
     AreaTables* T = nullptr;
     uint8_t *mem = nullptr, *gray = nullptr, *fresh = nullptr;
     uint32_t *sc = nullptr, *ev = nullptr;
+    uint8_t* snap_mem = nullptr;     // 2 snapshot slots of the live consoles (early-termination re-emulation)
+    uint32_t* snap_sc = nullptr;
     uint8_t *boot_mem = nullptr, *boot_gray = nullptr, *boot_obs = nullptr;
     uint32_t* boot_sc = nullptr;
     int64_t *x0 = nullptr, *t0 = nullptr;
     uint8_t *cmem = nullptr, *cgray = nullptr, *cobs = nullptr, *cboot = nullptr;
     uint8_t* key_bank = nullptr;     // CHR bank of each (level, ROM) key
     uint32_t *csc = nullptr;
+    uint8_t* csnap_mem = nullptr;    // 2 snapshot slots of the cache consoles
+    uint32_t* csnap_sc = nullptr;
     int64_t *cx = nullptr, *ct = nullptr;
     int32_t *clives = nullptr, *cdraws = nullptr;
     uint64_t *cframes = nullptr, *cinstr = nullptr;
@@ -423,6 +427,8 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     h->sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
     h->ev = B.alloc<uint32_t>((size_t)E_COUNT * h->np, good);
     h->gray = B.alloc<uint8_t>((size_t)2 * GRAY_PIX * h->np, good);
+    h->snap_mem = B.alloc<uint8_t>((size_t)2 * MEM_ROWS * h->np, good);
+    h->snap_sc = B.alloc<uint32_t>((size_t)2 * S_COUNT * h->np, good);
     h->fresh = B.alloc<uint8_t>((size_t)OBS_PIX * h->np, good);
     h->boot_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->nlp, good);
     h->boot_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->nlp, good);
@@ -432,6 +438,8 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     h->cmem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->ncp, good);
     h->csc = B.alloc<uint32_t>((size_t)S_COUNT * h->ncp, good);
     h->cgray = B.alloc<uint8_t>((size_t)2 * GRAY_PIX * h->ncp, good);
+    h->csnap_mem = B.alloc<uint8_t>((size_t)2 * MEM_ROWS * h->ncp, good);
+    h->csnap_sc = B.alloc<uint32_t>((size_t)2 * S_COUNT * h->ncp, good);
     h->cobs = B.alloc<uint8_t>((size_t)OBS_PIX * h->nc, good);
     h->cboot = B.alloc<uint8_t>(h->nc, good);
     h->cx = B.alloc<int64_t>(h->nc, good); h->ct = B.alloc<int64_t>(h->nc, good);
@@ -472,7 +480,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     SmallObsArgs so{h->boot_gray, h->nlp, nullptr, nullptr, 1, h->boot_obs, h->nl, h->T};
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nl), dim3(256), 0, 0, so);
     CacheArgs ca{h->R, h->cfg, h->key_bank, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
-                 h->cmem, h->csc, h->cgray, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
+                 h->cmem, h->csc, h->cgray, h->csnap_mem, h->csnap_sc, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
                  h->cframes, h->cinstr, h->cbad};
     hipLaunchKernelGGL(k_cache, emu_grid(h->nc), dim3(EMU_THREADS), 0, 0, ca);
     if (!ok(hipGetLastError(), "k_cache launch")) return fail();
@@ -522,7 +530,7 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     CK(hipSetDevice(h->device));
     hipStream_t s = (hipStream_t)stream;
     if (mark(h, s, 0)) return -1;
-    StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->ev, h->gray, d_actions,
+    StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->ev, h->gray, h->snap_mem, h->snap_sc, d_actions,
                 h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len, h->key_bank};
     hipLaunchKernelGGL(k_step, emu_grid(h->n), dim3(EMU_THREADS), 0, s, sa);
     CK(hipGetLastError());
@@ -617,7 +625,7 @@ int mh_num_levels(MhEnv* h) { return h ? h->nl : -1; }
 int64_t mh_state_bytes(void) { return (int64_t)MEM_ROWS + 4LL * S_COUNT; }
 int64_t mh_env_bytes(MhEnv* h) {
     if (!h) return -1;
-    int64_t per = MEM_ROWS + 4LL * S_COUNT + 4LL * E_COUNT + 2LL * GRAY_PIX + OBS_PIX;
+    int64_t per = 3LL * (MEM_ROWS + 4LL * S_COUNT) + 4LL * E_COUNT + 2LL * GRAY_PIX + OBS_PIX;
     return per * h->np / h->n;
 }
 
