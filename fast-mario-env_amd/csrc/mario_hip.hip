@@ -15,6 +15,7 @@
 
 #include "../../include/mario_hip.h"
 #include "lane_kernels.hpp"
+#include "replay.hpp"
 
 using namespace mh;
 
@@ -735,6 +736,45 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
         CK(hipMemcpy(d_T, &T, sizeof(T), hipMemcpyHostToDevice));
     }
     hipLaunchKernelGGL(k_resize_images, dim3((OBS_PIX + 255) / 256, n), dim3(256), 0, (hipStream_t)stream, d_src, d_dst, n, d_T);
+    CK(hipGetLastError());
+    return 0;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int mh_replay_add(uint8_t* frames, uint8_t* age, int16_t* act, float* rew, uint8_t* flags, int64_t* ptr,
+                  uint8_t* new_ep, int n_envs, int capacity, int frame_bytes, int k, const uint8_t* obs,
+                  const uint8_t* next_obs, const int64_t* action, const float* reward, const uint8_t* done,
+                  const uint8_t* truncated, void* stream) {
+    if (!frames || !age || !act || !rew || !flags || !ptr || !new_ep || !obs || !next_obs || !action || !reward ||
+        !done || !truncated || n_envs < 1 || capacity < 2 || k < 1 || frame_bytes < 16 || frame_bytes % 16) {
+        g_err = "invalid arguments"; return -1;
+    }
+    if (!aligned16(frames) || !aligned16(obs) || !aligned16(next_obs)) { g_err = "frame buffers must be 16-byte aligned"; return -1; }
+    ReplayAddArgs A{ReplayRing{frames, age, act, rew, flags, ptr, new_ep, n_envs, capacity, (uint32_t)frame_bytes},
+                    obs, next_obs, k, action, reward, done, truncated};
+    hipLaunchKernelGGL(k_replay_add, dim3(n_envs), dim3(256), 0, (hipStream_t)stream, A);
+    CK(hipGetLastError());
+    return 0;
+}
+
+int mh_replay_gather(const uint8_t* frames, const uint8_t* age, const int16_t* act, const float* rew,
+                     const uint8_t* flags, int n_envs, int capacity, int frame_bytes, int k, const int64_t* env,
+                     const int64_t* pos, int batch, int n_step, const float* gamma_pow, uint8_t* obs,
+                     uint8_t* next_obs, int64_t* action, float* reward, float* discount, float* terminal,
+                     int64_t* steps, int32_t* err, void* stream) {
+    if (!frames || !age || !act || !rew || !flags || !env || !pos || !gamma_pow || !obs || !next_obs || !action ||
+        !reward || !discount || !terminal || !steps || !err || n_envs < 1 || capacity < 2 || k < 1 ||
+        frame_bytes < 16 || frame_bytes % 16 || batch < 0 || n_step < 0) {
+        g_err = "invalid arguments"; return -1;
+    }
+    if (!aligned16(frames) || !aligned16(obs) || !aligned16(next_obs)) { g_err = "frame buffers must be 16-byte aligned"; return -1; }
+    if (batch == 0) return 0;
+    ReplayGatherArgs A{ReplayRing{(uint8_t*)frames, (uint8_t*)age, (int16_t*)act, (float*)rew, (uint8_t*)flags,
+                                  nullptr, nullptr, n_envs, capacity, (uint32_t)frame_bytes},
+                       k, n_step, batch, env, pos, gamma_pow, obs, next_obs, action, reward, discount, terminal,
+                       steps, err};
+    hipLaunchKernelGGL(k_replay_gather, dim3(batch, 2 * k), dim3(128), 0, (hipStream_t)stream, A);
     CK(hipGetLastError());
     return 0;
 }

@@ -67,6 +67,8 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).argtypes = [_P]
     L.mh_raw_destroy.argtypes = [_P]
     L.mh_resize.argtypes = [_P, _P, _i32, _P]
+    L.mh_replay_add.argtypes = [_P] * 7 + [_i32] * 4 + [_P] * 7
+    L.mh_replay_gather.argtypes = [_P] * 5 + [_i32] * 4 + [_P, _P, _i32, _i32] + [_P] * 10
     L.mh_timing.argtypes = [_P, _i32]
     L.mh_timing_read.argtypes = [_P, _P, _P]
     _lib = L

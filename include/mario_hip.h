@@ -126,6 +126,34 @@ void    mh_raw_destroy(MhRaw* h);
  * Replaces fm_resize_fast (fastmario.cpp:641-649). */
 int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
+/* ---- frame-deduplicating replay ring (device storage owned by the caller)
+ * The ring of FrameReplay (src/fast_mario_env/replay.py:43-60) for n_envs envs and `capacity` slots each,
+ * all device memory, slot s of env e at index e * capacity + s:
+ *   frames  u8  [n_envs][capacity][frame_bytes]   (16-byte aligned, frame_bytes a multiple of 16)
+ *   age     u8  [n_envs][capacity]   frames since the episode start, saturating at 255
+ *   act     i16 [n_envs][capacity]   rew f32 [n_envs][capacity]
+ *   flags   u8  [n_envs][capacity]   1 valid transition start, 2 done, 4 terminal (done and not truncated)
+ *   ptr     i64 [n_envs]             slots written so far
+ *   new_ep  u8  [n_envs]             the next add starts an episode (1 initially) */
+
+/* FrameReplay.add (replay.py:76-95): obs / next_obs are (n_envs, k, frame_bytes) stacks, of which only
+ * the newest frame is stored (obs's only when new_ep is set); action i64, reward f32, done and truncated
+ * u8, n_envs each. Updates ptr and new_ep on the device. */
+int mh_replay_add(uint8_t* frames, uint8_t* age, int16_t* act, float* rew, uint8_t* flags, int64_t* ptr,
+                  uint8_t* new_ep, int n_envs, int capacity, int frame_bytes, int k, const uint8_t* obs,
+                  const uint8_t* next_obs, const int64_t* action, const float* reward, const uint8_t* done,
+                  const uint8_t* truncated, void* stream);
+
+/* Batch assembly of FrameReplay.sample (replay.py:99-106, 131-145) for `batch` sampled (env, pos): the
+ * n-step return (gamma_pow[i] = float32(gamma ** i), i = 0..n_step), steps m, terminal, discount
+ * gamma_pow[m] * (1 - terminal), the action at pos, and the zero-padded (k, frame_bytes) stacks ending at
+ * pos (obs) and pos + m (next_obs). An (env, pos) outside the ring sets *err = 1 and yields zeros. */
+int mh_replay_gather(const uint8_t* frames, const uint8_t* age, const int16_t* act, const float* rew,
+                     const uint8_t* flags, int n_envs, int capacity, int frame_bytes, int k, const int64_t* env,
+                     const int64_t* pos, int batch, int n_step, const float* gamma_pow, uint8_t* obs,
+                     uint8_t* next_obs, int64_t* action, float* reward, float* discount, float* terminal,
+                     int64_t* steps, int32_t* err, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
