@@ -165,6 +165,82 @@ def run_ppo(args, rom, rom_name, rom_sha):
     print(json.dumps(out), flush=True)
 
 
+def run_replay(args, rom, rom_name, rom_sha):
+    """Replay workload (the GPU FrameReplay): the headline envs' transitions added to a 64-slot ring per env,
+    then batches of 4096 3-step transitions sampled. Kernel times come from HIP events on the stream the
+    kernels run on; the rooflines count the bytes each kernel must move."""
+    import torch
+
+    from fast_mario_env_amd import HipVecEnv
+    from fast_mario_env_amd.replay import FrameReplay
+    n, C, B, ns, reps = args.envs, 64, 4096, 3, 20
+    env = HipVecEnv("1-1", n, seed=0, sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4,
+                    maxpool=True, rom=rom, device="cuda:0")
+    rb = FrameReplay(C, n, 4, device="cuda:0", seed=0)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0)
+    obs = env.reset().clone()
+    add_ms, news = [], 0
+    log(f"replay: {n} envs, ring of {C} slots per env ({rb.nbytes() / 1e9:.1f} GB)")
+    for t in range(C + reps):                      # fill past one wrap of the ring, time the last `reps` adds
+        a = torch.randint(0, 7, (n,), generator=g, device="cuda:0")
+        o2, r, te, tr, _ = env.step(a)
+        d = te | tr
+        nxt = torch.where(d[:, None, None, None], env.final_obs, o2)
+        if t >= C:
+            news += int(rb._new_ep.sum())
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+        rb.add(obs, nxt, a, r, d, tr & ~te)
+        if t >= C:
+            e1.record()
+            add_ms.append((e0, e1))
+        obs = o2.clone()
+    torch.cuda.synchronize()
+    add_t = sum(x.elapsed_time(y) for x, y in add_ms) / reps
+    env.close()
+    rb.sample(B, ns, 0.99)                         # warm-up
+    torch.cuda.synchronize()
+    gat, draw_t = [], 0.0
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        d0 = time.perf_counter()
+        e, p = rb.draw(B, ns)
+        torch.cuda.synchronize()
+        draw_t += time.perf_counter() - d0
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rb.gather(e, p, ns, 0.99)
+        e1.record()
+        gat.append((e0, e1))
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    gat_t = sum(x.elapsed_time(y) for x, y in gat) / reps
+    rb.check_errors()
+    fb = 84 * 84
+    # add: the newest next_obs frame read and written per env, the obs frame too for envs starting an
+    # episode, and 16 B of slot metadata; gather: 2k frames read and written per sample plus its metadata
+    add_bytes = n * (2 * fb + 16) + (news / reps) * 2 * fb
+    gat_bytes = B * (2 * 4 * 2 * fb + ns * 6 + 2 + 40)
+    out = {
+        "metric": "replay: sampled 3-step transitions/sec (batch 4096) from a 64-slot-per-env ring at 32768 envs on 1 MI355X",
+        "value": round(B * reps / dt, 1), "unit": "transitions/s", "n_gpus": 1, "steps": reps, "warmup": C,
+        "ms_per_step": round(dt * 1e3 / reps, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic",
+        "config": {"workload": "replay: headline env transitions into FrameReplay, batch 4096, n_step 3", "envs": n,
+                   "capacity_per_env": C, "batch": B, "n_step": ns, "rom": rom_name, "rom_sha1": rom_sha},
+        "roofline": {"bound": "hbm", "kernel": "k_replay_gather", "achieved": round(gat_bytes / gat_t / 1e6, 1),
+                     "peak": 8000.0, "unit": "GB/s", "frac": round(gat_bytes / gat_t / 1e6 / 8000.0, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": int(gat_bytes)},
+        "add": {"kernel": "k_replay_add", "ms": round(add_t, 4), "achieved_GBps": round(add_bytes / add_t / 1e6, 1),
+                "frac": round(add_bytes / add_t / 1e6 / 8000.0, 4), "algorithmic_bytes_per_launch": int(add_bytes),
+                "transitions_per_s": round(n / add_t * 1e3, 1)},
+        "gather_ms": round(gat_t, 4), "draw_ms": round(draw_t * 1e3 / reps, 3),
+        "ring_gb": round(rb.nbytes() / 1e9, 2),
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,8 +252,9 @@ def main():
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["headline", "ppo"], default="headline",
-                    help="headline: the env step (default); ppo: a PPO rollout feeding a Nature CNN (config 5)")
+    ap.add_argument("--workload", choices=["headline", "ppo", "replay"], default="headline",
+                    help="headline: the env step (default); ppo: a PPO rollout feeding a Nature CNN (config 5); "
+                         "replay: env transitions into the GPU FrameReplay and sampled batches")
     ap.add_argument("--ppo-steps", type=int, default=128, help="rollout length of --workload ppo")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -194,6 +271,9 @@ def main():
     rom_sha = hashlib.sha1(rom).hexdigest()[:12]
     if args.workload == "ppo":
         run_ppo(args, rom, rom_name, rom_sha)
+        return
+    if args.workload == "replay":
+        run_replay(args, rom, rom_name, rom_sha)
         return
     n = args.envs
     log(f"creating {n} envs on {torch.cuda.get_device_name(0)} ({rom_name})")
