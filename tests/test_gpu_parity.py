@@ -88,6 +88,12 @@ CONFIGS = {
     "maxpool_sticky": dict(maxpool=True, sticky=0.25),
     "short_timelimit": dict(max_steps=60, noop_max=5),
     "headline": dict(sticky=0.25, noop_max=30, maxpool=True),
+    # frame-skip edges of the early-termination re-emulation: which frames are snapshotted depends on K and
+    # max-pool (K=1: none; K=2 max-pool: frame 0 only; K=3 without max-pool: frames 0 and 1; K=6: 0..3)
+    "skip1_stack2": dict(skip=1, frame_stack=2, noop_max=3),
+    "skip2_maxpool": dict(skip=2, maxpool=True, sticky=0.25, noop_max=3),
+    "skip3_short": dict(skip=3, sticky=0.25, max_steps=80),
+    "skip6_maxpool": dict(skip=6, maxpool=True, noop_max=4, sticky=0.5),
 }
 ACTION_P = [.05, .2, .25, .15, .25, .05, .05]
 
