@@ -238,19 +238,25 @@ struct Stepper {
     // When an observation is wanted, frames K-1 and (max-pool) K-2 are rendered with their hack frames,
     // K-1 into gray0 and K-2 into gray1. Before every frame that a re-emulation could start from, the
     // console is snapshotted into slot (frame & 1). When the episode ends at a frame last < K-1, the
-    // snapshot of frame last-1 (max-pool, last >= 1) or of frame last is restored and those frames run
-    // again with pixels on, last-1 with its hack frames, as in fastmario.cpp:351-362; the re-emulated
-    // frames count like any other. Written as a state machine around ONE console frame so that the
-    // emulator is inlined once: a lane that re-emulates does so while the other lanes of its wave still
-    // run their remaining agent frames.
+    // reference restores the snapshot of frame last-1 (max-pool, last >= 1) or of frame last and runs those
+    // frames again with pixels on, last-1 with its hack frames (fastmario.cpp:351-362); the re-emulated
+    // frames count like any other. Frames that were not rendered are re-emulated here the same way. Frame
+    // K-2 (max-pool) was rendered in the first pass, and running it again from the same state with the same
+    // buttons repeats it exactly: its state after the first pass is saved instead, only its partner K-3 runs
+    // again, the saved state is restored, and frame K-2 is counted a second time. No lane then runs more
+    // than K frames (plus hack frames) in a step, which would hold up its whole wave.
+    // Written as a state machine around ONE console frame so that the emulator is inlined once: a lane that
+    // re-emulates does so while the other lanes of its wave still run their remaining agent frames.
     __device__ __forceinline__ double agent_step(int act0, bool want_obs, bool* term) {
         const int K = cfg.skip;
         const bool mp = cfg.maxpool != 0;
         double total = 0.0;
         bool done = false, hack = false, render = false;
+        bool keep_last = false;            // the state after frame last is in slot last & 1
         int i = 0, guard = 0;
         int rf = -1;                       // agent frame being re-emulated (-1: the first pass)
         uint8_t b_prev = 0, b_cur = 0;     // buttons of agent frames i-1 and i
+        uint32_t n0 = 0, b0 = 0;           // instruction and bad-op counters at the start of agent frame i
         uint8_t* slot = gray0;
         for (;;) {
             uint8_t buttons = 0;
@@ -267,8 +273,10 @@ struct Stepper {
                 buttons = b_cur;
                 render = want_obs && (i == K - 1 || (mp && i == K - 2));
                 slot = ((K - 1 - i) & 1) ? gray1 : gray0;
-                // re-emulations start at frame last-1 (max-pool, last >= 1) or last, for last < K-1
-                if (want_obs && i < K - 1 && (!mp || i == 0 || i <= K - 3)) save_console(c, live, snap(i & 1));
+                n0 = c.instructions; b0 = c.bad_ops;
+                // re-emulations start at frame last-1 (max-pool, last >= 1) or last, for last < K-1, and
+                // never at K-2 (max-pool)
+                if (want_obs && i < K - 1 && (!mp || i <= K - 3)) save_console(c, live, snap(i & 1));
             } else {
                 buttons = rf == i ? b_cur : b_prev;
                 render = true;
@@ -293,7 +301,20 @@ struct Stepper {
                 if (!done && i < K - 1) { i++; continue; }
                 // the first pass ended at agent frame i
                 if (!(want_obs && done && i < K - 1)) break;
-                rf = (mp && i >= 1) ? i - 1 : i;
+                if (mp && i == K - 2) {
+                    // frame i was rendered: count its re-emulation (it ended the episode, so it had no hack
+                    // frames), and re-emulate its max-pool partner i-1 if there is one
+                    ev.frames++;
+                    const uint32_t dn = c.instructions - n0, db = (c.bad_ops - b0) & ~ERR_HACK_LIMIT;
+                    c.instructions += dn;
+                    c.bad_ops += db;
+                    if (i == 0) break;
+                    save_console(c, live, snap(i & 1));
+                    keep_last = true;
+                    rf = i - 1;
+                } else {
+                    rf = (mp && i >= 1) ? i - 1 : i;
+                }
                 restore_console(c, live, snap(rf & 1));
             } else if (rf < i) {
                 // frame last-1 again, then its hack frames (it did not end the episode)
@@ -303,6 +324,7 @@ struct Stepper {
                     c.bad_ops |= ERR_HACK_LIMIT;
                 }
                 hack = false;
+                if (keep_last) { restore_console(c, live, snap(i & 1)); break; }
                 rf++;
             } else {
                 break;
