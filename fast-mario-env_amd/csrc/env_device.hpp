@@ -246,7 +246,9 @@ struct Stepper {
     // again, the saved state is restored, and frame K-2 is counted a second time. No lane then runs more
     // than K frames (plus hack frames) in a step, which would hold up its whole wave.
     // Written as a state machine around ONE console frame so that the emulator is inlined once: a lane that
-    // re-emulates does so while the other lanes of its wave still run their remaining agent frames.
+    // re-emulates does so while the other lanes of its wave still run their remaining agent frames, and it
+    // waits (skipping the frame call) until the iterations of the wave's own rendered frames, K-2 and K-1,
+    // so that its rendered re-emulation does not turn an unrendered iteration of the wave into a rendered one.
     __device__ __forceinline__ double agent_step(int act0, bool want_obs, bool* term) {
         const int K = cfg.skip;
         const bool mp = cfg.maxpool != 0;
@@ -257,8 +259,11 @@ struct Stepper {
         int rf = -1;                       // agent frame being re-emulated (-1: the first pass)
         uint8_t b_prev = 0, b_cur = 0;     // buttons of agent frames i-1 and i
         uint32_t n0 = 0, b0 = 0;           // instruction and bad-op counters at the start of agent frame i
+        int it = 0, resume_at = 0;         // loop iterations so far; the iteration a re-emulation starts at
         uint8_t* slot = gray0;
         for (;;) {
+            if (rf >= 0 && it < resume_at) { it++; continue; }   // waiting for the wave's rendered frames
+            it++;
             uint8_t buttons = 0;
             if (hack) {
                 c.st(ROW_RAM + 0x7a0, 0);
@@ -315,6 +320,7 @@ struct Stepper {
                 } else {
                     rf = (mp && i >= 1) ? i - 1 : i;
                 }
+                resume_at = K - (keep_last ? 1 : i - rf + 1);   // K minus the frames to run again
                 restore_console(c, live, snap(rf & 1));
             } else if (rf < i) {
                 // frame last-1 again, then its hack frames (it did not end the episode)
