@@ -98,10 +98,12 @@ __device__ __forceinline__ uint32_t pick4(const uint32_t (&m)[4], uint32_t i) {
 // lane e at w np + e), max-pooled with a second one if `pool`: out[dy * row_stride + q * col_stride] =
 // output pixel (dy, 4 chunk + q). The float operations and their order are area_pixel's. The four
 // columns' taps (at most 4 consecutive source pixels each) lie in 4 consecutive words of a source row, so
-// a row is 4 word loads per image; a source row shared by two output rows is summed once.
+// a row is 4 word loads per image; a source row shared by two output rows is summed once. Output rows
+// dy0 .. dy1-1 only (a band; out still addresses row 0). The words of source row sy + 1 are loaded while
+// row sy is summed: the distinct source rows of consecutive output rows are consecutive.
 __device__ __forceinline__ void area_columns4(const uint32_t* g0, const uint32_t* g1, uint32_t np, uint32_t e,
                                               bool pool, int chunk, const AreaTables* T, uint8_t* out,
-                                              size_t col_stride, size_t row_stride) {
+                                              size_t col_stride, size_t row_stride, int dy0 = 0, int dy1 = 84) {
     const int c0 = 4 * chunk;
     const uint32_t wl = (uint32_t)T->xs[c0 * TAPS] >> 2;
     int nx[4];
@@ -118,17 +120,30 @@ __device__ __forceinline__ void area_columns4(const uint32_t* g0, const uint32_t
     }
     float acc[4] = {0.f, 0.f, 0.f, 0.f}, rs[4] = {0.f, 0.f, 0.f, 0.f};
     int last_sy = -1;
-    for (int dy = 0; dy < 84; dy++) {
+    // the source row's four words (max-pooled when pool) at row sy
+    auto row_words = [&](int sy, uint32_t* m) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const size_t wi = (size_t)((uint32_t)sy * 64 + (wl + i < 63 ? wl + i : 63)) * np + e;
+            m[i] = pool ? max_u8x4(g0[wi], g1[wi]) : g0[wi];
+        }
+    };
+    int pf_sy = T->ys[dy0 * TAPS];           // the row held in pm
+    uint32_t pm[4];
+    row_words(pf_sy, pm);
+    for (int dy = dy0; dy < dy1; dy++) {
         const int ny = T->yn[dy];
         for (int j = 0; j < ny; j++) {
             const int sy = T->ys[dy * TAPS + j];
             if (sy != last_sy) {
                 uint32_t m[4];
+                if (sy == pf_sy) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const size_t wi = (size_t)((uint32_t)sy * 64 + (wl + i < 63 ? wl + i : 63)) * np + e;
-                    m[i] = pool ? max_u8x4(g0[wi], g1[wi]) : g0[wi];
+                    for (int i = 0; i < 4; i++) m[i] = pm[i];
+                } else {
+                    row_words(sy, m);
                 }
+                if (sy + 1 < 240) { pf_sy = sy + 1; row_words(pf_sy, pm); }
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const uint64_t win = ((uint64_t)pick4(m, iq[q] < 3 ? iq[q] + 1 : 3) << 32 | pick4(m, iq[q])) >> sh[q];

@@ -3,7 +3,7 @@
 // One agent step of N envs is four kernels on the caller's stream:
 //   k_step          one lane per env: sticky draw, K frames of 6502 + catch-up PPU, reward/done/info,
 //                   hack frames, gray rendering of every frame into two alternating frame buffers
-//   k_obs           one thread per (env, 4 output columns): 2-frame max + INTER_AREA 256x240 -> 84x84
+//   k_obs           one thread per (env, 4 output columns, band of 21 output rows): 2-frame max + INTER_AREA
 //   k_reset         one lane per env: finished envs take a cached (level, no-op count) start state
 //   k_stack         LDS-transposed frame-stack shift, final_obs, reset observation
 #include <hip/hip_runtime.h>
@@ -138,15 +138,17 @@ struct ObsArgs {
 // last frame is in frame buffer 1 (the episode ended at an agent frame of the other parity than K-1).
 // Threads: x = env (64 per block), y = a chunk of 4 output columns (3 per block, 7 blocks per env group);
 // the grid's x walks the chunks of one env group first, so the source words they share are still in the L2.
+constexpr int OBS_BAND_ROWS = 21;   // output rows per k_obs workgroup: 4 bands, 4x the loads in flight
 __global__ void __launch_bounds__(192) k_obs(ObsArgs A) {
     const uint32_t e = blockIdx.y * 64 + (threadIdx.x & 63);
     const int chunk = blockIdx.x * 3 + (threadIdx.x >> 6);
     if (e >= (uint32_t)A.n || chunk >= 21) return;
     uint8_t* out = A.out + (size_t)(4 * chunk) * A.np + e;
     const size_t row_stride = (size_t)84 * A.np;
+    const int dy0 = OBS_BAND_ROWS * blockIdx.z, dy1 = dy0 + OBS_BAND_ROWS;   // this workgroup's output rows
     if (A.ev[(size_t)E_SHOWS_BOOT * A.np + e]) {
         const uint8_t* src = A.boot_obs + (size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + 4 * chunk;
-        for (int dy = 0; dy < 84; dy++)
+        for (int dy = dy0; dy < dy1; dy++)
             for (int q = 0; q < 4; q++) out[(size_t)dy * row_stride + (size_t)q * A.np] = src[dy * 84 + q];
         return;
     }
@@ -154,7 +156,7 @@ __global__ void __launch_bounds__(192) k_obs(ObsArgs A) {
     const uint32_t* g0 = (const uint32_t*)A.gray;
     const uint32_t* g1 = (const uint32_t*)(A.gray + (size_t)GRAY_PIX * A.np);
     if (pw & 2) { const uint32_t* t = g0; g0 = g1; g1 = t; }
-    area_columns4(g0, g1, A.np, e, (pw & 1) != 0, chunk, A.T, out, A.np, row_stride);
+    area_columns4(g0, g1, A.np, e, (pw & 1) != 0, chunk, A.T, out, A.np, row_stride, dy0, dy1);
 }
 
 struct StackArgs {
@@ -169,8 +171,8 @@ struct StackArgs {
 // frame; the fresh frame is read lane-interleaved and transposed through LDS.
 __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
     __shared__ uint32_t tile[64][65];
-    const uint32_t e0 = blockIdx.y * 64;
-    const int w0 = blockIdx.x * 64;             // word index within a frame (OBS_PIX / 4 = 1764 words)
+    const uint32_t e0 = blockIdx.x * 64;   // env groups vary fastest: neighbouring workgroups read adjacent fresh words
+    const int w0 = blockIdx.y * 64;        // word index within a frame (OBS_PIX / 4 = 1764 words)
     const int nw = OBS_PIX / 4;
     if (A.mode == 0) {
         for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
@@ -508,7 +510,7 @@ int mh_reset(MhEnv* h, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(1));
     CK(hipGetLastError());
-    hipLaunchKernelGGL(k_stack, dim3((OBS_PIX / 4 + 63) / 64, h->np / 64), dim3(256), 0, s, h->stack_args(1));
+    hipLaunchKernelGGL(k_stack, dim3(h->np / 64, (OBS_PIX / 4 + 63) / 64), dim3(256), 0, s, h->stack_args(1));
     CK(hipGetLastError());
     return 0;
 }
@@ -537,13 +539,13 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
     ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
-    hipLaunchKernelGGL(k_obs, dim3(7, h->np / 64), dim3(192), 0, s, oa);
+    hipLaunchKernelGGL(k_obs, dim3(7, h->np / 64, 84 / OBS_BAND_ROWS), dim3(192), 0, s, oa);
     CK(hipGetLastError());
     if (mark(h, s, 2)) return -1;
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(0));
     CK(hipGetLastError());
     if (mark(h, s, 3)) return -1;
-    hipLaunchKernelGGL(k_stack, dim3((OBS_PIX / 4 + 63) / 64, h->np / 64), dim3(256), 0, s, h->stack_args(0));
+    hipLaunchKernelGGL(k_stack, dim3(h->np / 64, (OBS_PIX / 4 + 63) / 64), dim3(256), 0, s, h->stack_args(0));
     CK(hipGetLastError());
     if (mark(h, s, 4)) return -1;
     if (h->timing) h->timed_steps++;
