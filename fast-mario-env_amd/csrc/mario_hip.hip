@@ -776,7 +776,7 @@ int mh_replay_gather(const uint8_t* frames, const uint8_t* age, const int16_t* a
                                   nullptr, nullptr, n_envs, capacity, (uint32_t)frame_bytes},
                        k, n_step, batch, env, pos, gamma_pow, obs, next_obs, action, reward, discount, terminal,
                        steps, err};
-    hipLaunchKernelGGL(k_replay_gather, dim3(batch, 2 * k), dim3(128), 0, (hipStream_t)stream, A);
+    hipLaunchKernelGGL(k_replay_gather, dim3(batch), dim3(REPLAY_GATHER_THREADS), 0, (hipStream_t)stream, A);
     CK(hipGetLastError());
     return 0;
 }

@@ -3,8 +3,7 @@
 //
 // Per env e a ring of C frame slots (E x C x FB bytes) with per-slot age (frames since the episode
 // start, saturating at 255), action (int16), reward (f32) and flags (1 valid start, 2 done, 4 terminal).
-// ptr[e] counts the slots ever written. Both kernels are HBM copies: one workgroup per env (add) or per
-// output frame (gather), 16-byte accesses.
+// ptr[e] counts the slots ever written. Both kernels are HBM copies in 16-byte accesses.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -103,28 +102,60 @@ __device__ __forceinline__ NStep n_step_return(const ReplayRing& R, const Replay
     return NStep{ret, term, m};
 }
 
-// Batch assembly (replay.py:99-106 and 143-145): workgroup (b, j) writes frame j of obs (j < k) or of
-// next_obs (j >= k) of sample b: the ring frame (q - off) mod C, or zeros where off exceeds the age of the
-// stack's newest slot (before the episode start). q = pos (obs) or pos + m (next_obs), off = k-1 .. 0.
-__global__ void __launch_bounds__(128) k_replay_gather(ReplayGatherArgs A) {
+// 16-byte word i of a sample's 2k output frames (obs stack, then next_obs stack): where it comes from in
+// the env's ring (frame (q - off) mod C, or zeros before the episode start) and where it goes.
+struct GatherView {
+    const uint4* ring;     // the env's ring, frame s at ring + s nv
+    uint4* obs; uint4* nxt;  // the sample's output stacks
+    uint32_t nv, total, k, C, qo, qn;   // words per frame, 2k nv, stack depth, ring size, newest slots
+    int age_o, age_n;      // ages of the newest slots
+    __device__ __forceinline__ uint4 load(uint32_t i) const {
+        const uint32_t ic = i < total ? i : 0u;                // past the end: an in-range word, not stored
+        const uint32_t f = ic / nv, o = ic - f * nv;
+        const bool second = f >= k;
+        const uint32_t jj = second ? f - k : f, off = k - 1u - jj, qs = second ? qn : qo;
+        const uint32_t slot = qs >= off ? qs - off : qs + C - off;   // (q - off) mod C, off < k <= C
+        const uint4 w = ring[(size_t)slot * nv + o];
+        return (int)off <= (second ? age_n : age_o) ? w : make_uint4(0, 0, 0, 0);
+    }
+    __device__ __forceinline__ void store(uint32_t i, uint4 w) const {
+        if (i >= total) return;
+        const uint32_t f = i / nv, o = i - f * nv;
+        if (f >= k) nxt[(size_t)(f - k) * nv + o] = w;
+        else obs[(size_t)f * nv + o] = w;
+    }
+};
+
+// Batch assembly (replay.py:99-106 and 143-145), one 256-thread workgroup per sample b: every thread
+// computes the sample's n-step return and the ages it needs (the same few addresses for all of them), then
+// the workgroup copies the 2k frames, obs stack (q = pos) then next_obs stack (q = pos + m): frame j is the
+// ring frame (q - off) mod C, off = k-1-j, or zeros where off exceeds the age of the stack's newest slot
+// (before the episode start). Eight 16-byte loads are in flight per thread.
+constexpr int REPLAY_GATHER_THREADS = 256;
+__global__ void __launch_bounds__(REPLAY_GATHER_THREADS) k_replay_gather(ReplayGatherArgs A) {
     const ReplayRing& R = A.R;
-    const int b = blockIdx.x, j = blockIdx.y;
-    if (b >= A.B || j >= 2 * A.k) return;
+    const int b = blockIdx.x;
+    if (b >= A.B) return;
     const int64_t e = A.env[b], p = A.pos[b];
     const bool bad = e < 0 || e >= R.E || p < 0;
     const NStep ns = bad ? NStep{0.0f, 0.0f, 0} : n_step_return(R, A, e, p);
-    const bool nxt = j >= A.k;
-    const int jj = nxt ? j - A.k : j, off = A.k - 1 - jj;
-    const int64_t q = p + (nxt ? ns.m : 0);
     const size_t fb = R.fb, row = bad ? 0 : (size_t)e * (size_t)R.C;
-    const bool keep = !bad && off <= (int)R.age[row + ring_slot(q, R.C)];
-    const uint4* src = (const uint4*)(R.frames + (row + ring_slot(q - off, R.C)) * fb);
-    uint4* dst = (uint4*)((nxt ? A.next_obs : A.obs) + ((size_t)b * A.k + jj) * fb);
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    for (uint32_t i = threadIdx.x; i < fb / 16; i += blockDim.x) dst[i] = keep ? src[i] : z;
-    if (j != 0 || threadIdx.x != 0) return;
+    const uint32_t C = (uint32_t)R.C;
+    const uint32_t qo = bad ? 0u : (uint32_t)ring_slot(p, R.C), qn = bad ? 0u : (uint32_t)ring_slot(p + ns.m, R.C);
+    const int age_o = bad ? -1 : (int)R.age[row + qo], age_n = bad ? -1 : (int)R.age[row + qn];
+    const uint32_t nv = (uint32_t)(fb / 16), total = 2u * (uint32_t)A.k * nv;
+    const GatherView G{(const uint4*)(R.frames + row * fb), (uint4*)A.obs + (size_t)b * A.k * nv,
+                       (uint4*)A.next_obs + (size_t)b * A.k * nv, nv, total, (uint32_t)A.k, C, qo, qn, age_o, age_n};
+    for (uint32_t i0 = threadIdx.x; i0 < total; i0 += 8 * REPLAY_GATHER_THREADS) {
+        constexpr uint32_t T = REPLAY_GATHER_THREADS;
+        const uint4 t0 = G.load(i0), t1 = G.load(i0 + T), t2 = G.load(i0 + 2 * T), t3 = G.load(i0 + 3 * T);
+        const uint4 t4 = G.load(i0 + 4 * T), t5 = G.load(i0 + 5 * T), t6 = G.load(i0 + 6 * T), t7 = G.load(i0 + 7 * T);
+        G.store(i0, t0); G.store(i0 + T, t1); G.store(i0 + 2 * T, t2); G.store(i0 + 3 * T, t3);
+        G.store(i0 + 4 * T, t4); G.store(i0 + 5 * T, t5); G.store(i0 + 6 * T, t6); G.store(i0 + 7 * T, t7);
+    }
+    if (threadIdx.x != 0) return;
     if (bad) *A.err = 1;                                  // every writer stores 1
-    A.action[b] = bad ? 0 : (int64_t)R.act[row + ring_slot(p, R.C)];
+    A.action[b] = bad ? 0 : (int64_t)R.act[row + qo];
     A.reward[b] = ns.R;
     A.steps[b] = ns.m;
     A.terminal[b] = ns.term;
