@@ -192,6 +192,7 @@ struct LaneCtx {
     const uint8_t* lut;
     uint32_t* sp;     // this lane's sprite line buffer (stride LDS_LANES words)
     uint32_t* gp;     // this lane's gray palette, tile row and OAM (stride LDS_LANES words)
+    uint8_t twin;     // which of the env's two twin lanes this is
 };
 
 // console e of the memory block `mem` (np consoles), on CHR bank `bank` of the staged cartridge
@@ -201,6 +202,7 @@ __device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* me
     c.cart = x.cart; c.cart.chr += bank * 0x2000u; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
     c.lds_bg = x.gp + LDS_GP_WORDS * LDS_LANES; c.bg_key = -1;
     c.lds_oam = x.gp + (LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES;
+    c.twin = x.twin;
     c.bad_ops = 0; c.instructions = 0;
     c.pend_line = -1; c.sp_line = -1; c.pal_dirty = true;
 }

@@ -40,15 +40,17 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
     __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
     __shared__ uint32_t s_gp[LDS_GP_REGION * LDS_LANES];
 
-// Env slot of this thread within its block (0 .. LDS_LANES-1), or -1 for a lane that carries no env.
+// Env slot of this thread within its block (0 .. LDS_LANES-1). Lanes l and l + 32 of a wave are twins:
+// they carry the same env, run its console in lockstep (identical state, identical loads and stores of
+// identical values) and share its LDS buffers; only the renderer gives them different work.
 __device__ __forceinline__ int lane_slot() {
-    const int lane = threadIdx.x & 63;
-    return lane < ENVS_PER_WAVE ? (int)(threadIdx.x >> 6) * ENVS_PER_WAVE + lane : -1;
+    return (int)(threadIdx.x >> 6) * ENVS_PER_WAVE + (int)(threadIdx.x & (ENVS_PER_WAVE - 1));
 }
+__device__ __forceinline__ uint8_t lane_twin() { return (uint8_t)((threadIdx.x / ENVS_PER_WAVE) & 1u); }
 
 __device__ __forceinline__ LaneCtx lane_ctx(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_lut,
                                             const uint32_t* s_dec, uint32_t* s_sp, uint32_t* s_gp, int slot) {
-    return LaneCtx{make_cart(R, s_rom, s_dec), s_lut, s_sp + slot, s_gp + slot};
+    return LaneCtx{make_cart(R, s_rom, s_dec), s_lut, s_sp + slot, s_gp + slot, lane_twin()};
 }
 
 constexpr int EMU_THREADS = 64 * WAVES_PER_BLOCK;
@@ -59,7 +61,6 @@ __global__ void __launch_bounds__(EMU_THREADS) k_boot(BootArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    if (slot < 0) return;
     const int l = (int)(blockIdx.x * LDS_LANES + slot);
     if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), l);
 }
@@ -68,7 +69,6 @@ __global__ void __launch_bounds__(EMU_THREADS) k_cache(CacheArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    if (slot < 0) return;
     const int ci = (int)(blockIdx.x * LDS_LANES + slot);
     if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), ci);
 }
@@ -77,7 +77,6 @@ __global__ void __launch_bounds__(EMU_THREADS) k_step(StepArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    if (slot < 0) return;
     const uint32_t e = (uint32_t)(blockIdx.x * LDS_LANES + slot);
     if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }
@@ -86,7 +85,6 @@ __global__ void __launch_bounds__(EMU_THREADS) k_raw(RawArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    if (slot < 0) return;
     const uint32_t e = (uint32_t)(blockIdx.x * LDS_LANES + slot);
     if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }

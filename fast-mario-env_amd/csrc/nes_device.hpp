@@ -18,10 +18,11 @@
 namespace mh {
 
 constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
-// Emulator launch shape: a 64-lane wave carries ENVS_PER_WAVE envs (its other lanes idle) and a block holds
-// WAVES_PER_BLOCK waves sharing one LDS copy of the cartridge. 32768 envs in full waves are 512 waves, which
-// leave half of the 1024 SIMDs of the chip empty; half-full waves put a wave on every SIMD and halve the lanes
-// whose divergent paths one wave has to walk.
+// Emulator launch shape: a 64-lane wave carries ENVS_PER_WAVE envs, each on two twin lanes (l and l + 32),
+// and a block holds WAVES_PER_BLOCK waves sharing one LDS copy of the cartridge. 32768 envs in full waves
+// are 512 waves, which leave half of the 1024 SIMDs of the chip empty; half-full waves put a wave on every
+// SIMD and halve the lanes whose divergent paths one wave has to walk. The twins run the same console in
+// lockstep, which costs the wave nothing, and split the renderer's pixel groups between them.
 constexpr int ENVS_PER_WAVE = 32;
 constexpr int WAVES_PER_BLOCK = 4;
 constexpr int LDS_LANES = ENVS_PER_WAVE * WAVES_PER_BLOCK;  // env slots sharing one block's per-lane LDS buffers
@@ -198,6 +199,8 @@ struct Console {
     uint8_t* gray;           // GRAY slot + 4 e: pixels 4i..4i+3 in the 32-bit word at gray + 4 i np
     const uint8_t* lut;      // palette value -> gray (LDS, 256 entries)
     bool render;
+    uint8_t twin;            // 0 or 1: which of the env's two lanes this is (both run the console; the
+                             // renderer splits the 8-pixel groups between them)
     // ---- CPU
     uint16_t pc;
     uint8_t sp, a, x, y, p, zero_skip;
@@ -738,24 +741,31 @@ struct Console {
         // pixel bb of a group takes the second tile's attribute when f + bb >= 8: bytes bb >= 8 - f
         const uint64_t second = f ? (~0ull << (8 * (8 - f))) : 0ull;
         const uint32_t tsel0 = (uint32_t)second & 0x04040404u, tsel1 = (uint32_t)(second >> 32) & 0x04040404u;
-        // Software pipeline over the groups: group g needs tiles g and g + 1 (a, b). Iteration g fetches
-        // the planes of tile g + 2, the index of tile g + 3 and the sprite bytes of group g + 1, which
-        // are used one iteration later, so no LDS round trip sits between two groups. The fetches are
-        // unconditional (indices clamped to the buffers; a layer that is off masks its values
-        // afterwards), so every iteration issues the same LDS operations.
+        // The two twin lanes of the env split the groups: this lane draws the groups whose parity is its
+        // twin index (a fixed owner per group, so a group cut by a catch-up boundary is finished by the
+        // lane that started it). Software pipeline over this lane's groups: group g needs tiles g and
+        // g + 1 (a, b). Iteration g fetches the planes of tiles g + 2 and g + 3, the indices of tiles
+        // g + 4 and g + 5 and the sprite bytes of group g + 2, which are used one iteration later, so no
+        // LDS round trip sits between two groups. The fetches are unconditional (indices clamped to the
+        // buffers; a layer that is off masks its values afterwards), so every iteration issues the same
+        // LDS operations.
+        auto tile_of = [&](int k) { return bg_tile_of(k < 32 ? k : 32, bc0, bcy); };
+        int g = g0 + ((g0 ^ (int)twin) & 1);
         uint32_t alo, ahi, agt, blo, bhi, bgt;
-        bg_planes(bg_tile_of(g0, bc0, bcy), fy, bgpal, alo, ahi, agt);
-        bg_planes(bg_tile_of(g0 + 1, bc0, bcy), fy, bgpal, blo, bhi, bgt);
-        uint32_t nxt = bg_tile_of(g0 + 2 < 32 ? g0 + 2 : 32, bc0, bcy);
+        bg_planes(tile_of(g), fy, bgpal, alo, ahi, agt);
+        bg_planes(tile_of(g + 1), fy, bgpal, blo, bhi, bgt);
+        uint32_t nxa = tile_of(g + 2), nxb = tile_of(g + 3);
         if (!show_bg) { alo = ahi = blo = bhi = 0; agt = bgt = ubg; }
-        uint32_t s0 = lds_sp[(2 * g0) * LDS_LANES], s1 = lds_sp[(2 * g0 + 1) * LDS_LANES];   // the group's sprite bytes
+        const int ws0 = 2 * g < 62 ? 2 * g : 62;
+        uint32_t s0 = lds_sp[ws0 * LDS_LANES], s1 = lds_sp[(ws0 + 1) * LDS_LANES];   // the group's sprite bytes
         if (!spr) s0 = s1 = 0;
-        uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g0) * np;   // word of pixels 8g .. 8g+3
-        for (int g = g0; g < g1; g++) {
-            uint32_t clo, chi, cgt;
-            bg_planes(nxt, fy, bgpal, clo, chi, cgt);
-            const uint32_t nn = bg_tile_of(g + 3 < 32 ? g + 3 : 32, bc0, bcy);
-            const int ws = 2 * g + 2 < 62 ? 2 * g + 2 : 62;
+        uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g) * np;   // word of pixels 8g .. 8g+3
+        for (; g < g1; g += 2) {
+            uint32_t clo, chi, cgt, dlo, dhi, dgt;
+            bg_planes(nxa, fy, bgpal, clo, chi, cgt);
+            bg_planes(nxb, fy, bgpal, dlo, dhi, dgt);
+            const uint32_t na = tile_of(g + 4), nb = tile_of(g + 5);
+            const int ws = 2 * g + 4 < 62 ? 2 * g + 4 : 62;
             const uint32_t t0 = lds_sp[ws * LDS_LANES], t1 = lds_sp[(ws + 1) * LDS_LANES];
             // pixel 8g + bb is bit 15 - bb of the window after the fine-scroll shift; reversed: bit 16 + bb
             const uint32_t rlo = __builtin_bitreverse32(((alo << 8) | blo) << f);
@@ -800,10 +810,10 @@ struct Console {
                     }
                 }
             }
-            wp += 2 * np;
-            alo = blo; ahi = bhi; agt = bgt;
-            blo = show_bg ? clo : 0u; bhi = show_bg ? chi : 0u; bgt = show_bg ? cgt : ubg;
-            nxt = nn; s0 = spr ? t0 : 0u; s1 = spr ? t1 : 0u;
+            wp += 4 * np;
+            alo = show_bg ? clo : 0u; ahi = show_bg ? chi : 0u; agt = show_bg ? cgt : ubg;
+            blo = show_bg ? dlo : 0u; bhi = show_bg ? dhi : 0u; bgt = show_bg ? dgt : ubg;
+            nxa = na; nxb = nb; s0 = spr ? t0 : 0u; s1 = spr ? t1 : 0u;
         }
     }
 
