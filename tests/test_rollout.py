@@ -102,3 +102,29 @@ def test_rollout_replays_through_a_second_env():
     ea, er = gae_reference(*(x.cpu().numpy() for x in (ro.rew, ro.val, ro.start, ro.next_val, ro.next_start)))
     assert np.allclose(adv.cpu().numpy(), ea, rtol=1e-4, atol=1e-4)
     env.close(); twin.close()
+
+
+@pytest.mark.gpu
+def test_policy_input_path_matches_float_scaling():
+    # the GPU forward scales the uint8 observation straight into bf16 channels-last; it must give exactly what
+    # the plain float32 scaling under bf16 autocast gives (plain PyTorch, NCHW)
+    import torch.nn.functional as F
+
+    from fast_mario_env_amd.rollout import make_net
+    net = make_net(seed=1)
+    obs = torch.randint(0, 256, (96, 4, 84, 84), dtype=torch.uint8, device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(5))
+    with torch.no_grad():
+        logits, value = net(obs)
+        logits2, value2 = net(obs[:64])          # a second batch shape gets its own buffer
+        x = obs.float().mul_(1.0 / 255.0)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            for c in net.convs:
+                x = F.relu(F.conv2d(x, c.weight.contiguous(), c.bias, c.stride))
+            h = F.relu(net.fc(x.flatten(1)))
+        h = h.float()
+        ref_logits, ref_value = net.pi(h), net.vf(h).squeeze(-1)
+    # bf16 convolutions: the two layouts may pick different kernels, so compare at bf16 resolution
+    assert torch.allclose(logits, ref_logits, rtol=2e-2, atol=2e-3)
+    assert torch.allclose(value, ref_value, rtol=2e-2, atol=2e-3)
+    assert torch.allclose(logits[:64], logits2, rtol=2e-2, atol=2e-3)
