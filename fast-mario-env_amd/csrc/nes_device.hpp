@@ -636,14 +636,31 @@ struct Console {
             }
             const uint8_t lo = vbus_read(ad), hi = vbus_read((uint16_t)(ad + 8));
             const uint32_t tag = 0x80u | ((attr & 3u) << 2) | (attr & 0x20 ? 0u : 0x40u);
-            const int xe = sx + 8 < 256 ? sx + 8 : 256;
-            for (int px = sx; px < xe; px++) {
-                int xs = px - sx;
-                if (!(attr & 0x40)) xs ^= 7;
-                const uint32_t c = ((lo >> xs) & 1u) | (((hi >> xs) & 1u) << 1);
-                uint32_t* wp = &lds_sp[(px >> 2) * LDS_LANES];
-                const int sh = 8 * (px & 3);
-                if (c && !((*wp >> sh) & 0xffu)) *wp |= (c | tag) << sh;
+            // The sprite's 8 pixels as 8 bytes (pixel sx + j in byte j: pattern | tag, or 0 where transparent),
+            // merged into the (at most 3) line words they cover: a byte takes the sprite only where no
+            // earlier listed sprite is opaque (a written byte always has bit 7 set). Pixels past x = 255 fall
+            // in words past the line and are dropped.
+            const uint32_t rlo = (attr & 0x40) ? (uint32_t)lo : __builtin_bitreverse32((uint32_t)lo) >> 24;
+            const uint32_t rhi = (attr & 0x40) ? (uint32_t)hi : __builtin_bitreverse32((uint32_t)hi) >> 24;
+            uint32_t cw[2];
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const uint32_t pat = (__umul24((rlo >> (4 * q)) & 0xfu, 0x204081u) & 0x01010101u) |
+                                     ((__umul24((rhi >> (4 * q)) & 0xfu, 0x204081u) & 0x01010101u) << 1);
+                const uint32_t nz = (pat + 0x7f7f7f7fu) & 0x80808080u;
+                cw[q] = (pat | tag * 0x01010101u) & (nz | (nz - (nz >> 7)));
+            }
+            const uint64_t span = ((uint64_t)cw[1] << 32 | cw[0]) ;
+            const int w0 = sx >> 2, sh = 8 * (sx & 3);
+            const uint64_t lo64 = span << sh;
+            const uint32_t cv[3] = {(uint32_t)lo64, (uint32_t)(lo64 >> 32), sh ? (uint32_t)(span >> (64 - sh)) : 0u};
+#pragma unroll
+            for (int i = 0; i < 3; i++) {
+                if (w0 + i < LDS_SP_WORDS) {
+                    uint32_t* wp = &lds_sp[(w0 + i) * LDS_LANES];
+                    const uint32_t old = *wp, occ = old & 0x80808080u;
+                    *wp = old | (cv[i] & ~(occ | (occ - (occ >> 7))));
+                }
             }
         }
         sp_line = py;
