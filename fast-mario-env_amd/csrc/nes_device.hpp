@@ -30,7 +30,8 @@ constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite lin
 constexpr int LDS_BG_WORDS = 20;                   // words per lane: two name-table rows (64 tiles) + their attributes
 constexpr int LDS_BG_ATTR = 64;                    // byte offset of the attribute bytes in the tile row
 constexpr int LDS_OAM_WORDS = 64;                  // words per lane: OAM (sprite i = word i: y, tile, attr, x)
-constexpr int LDS_GP_REGION = LDS_GP_WORDS + LDS_BG_WORDS + LDS_OAM_WORDS;   // palette, tile row, OAM
+constexpr int LDS_XCHG_WORDS = 2;                 // words per env slot: the twins' halves of the sprite-range mask
+constexpr int LDS_GP_REGION = LDS_GP_WORDS + LDS_BG_WORDS + LDS_OAM_WORDS + LDS_XCHG_WORDS;   // palette, tile row, OAM, exchange
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
 // Render lines per frame slice (a power of two). A wave runs its lanes' CPUs to the end of a group of
 // this many lines and then catches their PPUs up together; a wave iteration costs the slowest lane's
@@ -501,12 +502,19 @@ struct Console {
         // in-range sprites as a 64-bit mask (bit i: pend_line - y_i in [0, h)), from index oam_addr / 4 on;
         // the list is its first (at most 8) set bits, entries past the count keep their old values
         const uint32_t h = long_spr ? 16u : 8u;
-        uint32_t mlo = 0, mhi = 0;
+        // The env's twin lanes each test one half of OAM (twin t: sprites 32 t .. 32 t + 31) into exchange word
+        // t of the env, then both read both words. The wave barrier is a convergence point: every lane active
+        // here has stored its word before any lane loads (a wave's LDS accesses complete in order).
+        uint32_t half = 0;
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            mlo |= ((uint32_t)(pend_line - (int)(oam_sprite(i) & 0xffu)) < h ? 1u : 0u) << i;
-            mhi |= ((uint32_t)(pend_line - (int)(oam_sprite(32 + i) & 0xffu)) < h ? 1u : 0u) << i;
-        }
+        for (int i = 0; i < 32; i++)
+            half |= ((uint32_t)(pend_line - (int)(oam_sprite(32 * twin + i) & 0xffu)) < h ? 1u : 0u) << i;
+        uint32_t* const xw = lds_oam + LDS_OAM_WORDS * LDS_LANES;
+        xw[twin * LDS_LANES] = half;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        uint32_t mlo = xw[0], mhi = xw[LDS_LANES];
         const int i0 = oam_addr >> 2;
         if (i0 < 32) mlo &= ~0u << i0;
         else { mlo = 0; mhi &= ~0u << (i0 - 32); }
