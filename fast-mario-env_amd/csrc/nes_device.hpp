@@ -766,47 +766,43 @@ struct Console {
         // pixel bb of a group takes the second tile's attribute when f + bb >= 8: bytes bb >= 8 - f
         const uint64_t second = f ? (~0ull << (8 * (8 - f))) : 0ull;
         const uint32_t tsel0 = (uint32_t)second & 0x04040404u, tsel1 = (uint32_t)(second >> 32) & 0x04040404u;
-        // The two twin lanes of the env split the groups: this lane draws the groups whose parity is its
-        // twin index (a fixed owner per group, so a group cut by a catch-up boundary is finished by the
-        // lane that started it). Software pipeline over this lane's groups: group g needs tiles g and
-        // g + 1 (a, b). Iteration g fetches the planes of tiles g + 2 and g + 3, the indices of tiles
-        // g + 4 and g + 5 and the sprite bytes of group g + 2, which are used one iteration later, so no
-        // LDS round trip sits between two groups. The fetches are unconditional (indices clamped to the
-        // buffers; a layer that is off masks its values afterwards), so every iteration issues the same
-        // LDS operations.
+        // The two twin lanes of the env split the groups in pairs: this lane draws groups 4m + 2 twin and
+        // 4m + 2 twin + 1 (a fixed owner per group, so a group cut by a catch-up boundary is finished by the
+        // lane that started it). One iteration draws one pair (p, p + 1) from tiles p, p + 1 and p + 2, and
+        // fetches the planes of the next pair's three tiles, the indices of the pair after it and the next
+        // pair's sprite bytes, which are used one iteration later, so no LDS round trip sits between two
+        // pairs. The fetches are unconditional (indices clamped to the buffers; a layer that is off masks
+        // its values afterwards), so every iteration issues the same LDS operations. A group of a pair that
+        // lies outside [x0, x1) gets an empty pixel mask and is not written.
         auto tile_of = [&](int k) { return bg_tile_of(k < 32 ? k : 32, bc0, bcy); };
-        int g = g0 + ((g0 ^ (int)twin) & 1);
-        uint32_t alo, ahi, agt, blo, bhi, bgt;
-        bg_planes(tile_of(g), fy, bgpal, alo, ahi, agt);
-        bg_planes(tile_of(g + 1), fy, bgpal, blo, bhi, bgt);
-        uint32_t nxa = tile_of(g + 2), nxb = tile_of(g + 3);
-        if (!show_bg) { alo = ahi = blo = bhi = 0; agt = bgt = ubg; }
-        const int ws0 = 2 * g < 62 ? 2 * g : 62;
-        uint32_t s0 = lds_sp[ws0 * LDS_LANES], s1 = lds_sp[(ws0 + 1) * LDS_LANES];   // the group's sprite bytes
-        if (!spr) s0 = s1 = 0;
-        uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * g) * np;   // word of pixels 8g .. 8g+3
-        for (; g < g1; g += 2) {
-            uint32_t clo, chi, cgt, dlo, dhi, dgt;
-            bg_planes(nxa, fy, bgpal, clo, chi, cgt);
-            bg_planes(nxb, fy, bgpal, dlo, dhi, dgt);
-            const uint32_t na = tile_of(g + 4), nb = tile_of(g + 5);
-            const int ws = 2 * g + 4 < 62 ? 2 * g + 4 : 62;
-            const uint32_t t0 = lds_sp[ws * LDS_LANES], t1 = lds_sp[(ws + 1) * LDS_LANES];
+        int pg = (g0 & ~3) + 2 * (int)twin;
+        if (pg + 1 < g0) pg += 4;
+        uint32_t alo, ahi, agt, blo, bhi, bgt, clo, chi, cgt;
+        bg_planes(tile_of(pg), fy, bgpal, alo, ahi, agt);
+        bg_planes(tile_of(pg + 1), fy, bgpal, blo, bhi, bgt);
+        bg_planes(tile_of(pg + 2), fy, bgpal, clo, chi, cgt);
+        uint32_t nxa = tile_of(pg + 4), nxb = tile_of(pg + 5), nxc = tile_of(pg + 6);
+        if (!show_bg) { alo = ahi = blo = bhi = clo = chi = 0; agt = bgt = cgt = ubg; }
+        const int ws0 = 2 * pg < 60 ? 2 * pg : 60;
+        uint32_t s0 = lds_sp[ws0 * LDS_LANES], s1 = lds_sp[(ws0 + 1) * LDS_LANES];   // the pair's sprite bytes
+        uint32_t s2 = lds_sp[(ws0 + 2) * LDS_LANES], s3 = lds_sp[(ws0 + 3) * LDS_LANES];
+        if (!spr) s0 = s1 = s2 = s3 = 0;
+        uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * pg) * np;   // word of pixels 8pg .. 8pg+3
+        // the two words of the group drawn from tiles (lo0, hi0, gt0) and (lo1, hi1, gt1) with sprite bytes ca, cb
+        auto group_words = [&](uint32_t lo0, uint32_t hi0, uint32_t gt0, uint32_t lo1, uint32_t hi1, uint32_t gt1,
+                               uint32_t ca, uint32_t cb, uint32_t keep_bg, uint32_t keep_sp, uint32_t (&out)[2]) {
             // pixel 8g + bb is bit 15 - bb of the window after the fine-scroll shift; reversed: bit 16 + bb
-            const uint32_t rlo = __builtin_bitreverse32(((alo << 8) | blo) << f);
-            const uint32_t rhi = __builtin_bitreverse32(((ahi << 8) | bhi) << f);
-            const uint32_t keep_bg = (g == 0 && hide_edge_bg) ? 0u : ~0u;     // pixels 0-7 may hide either layer
-            const uint32_t keep_sp = (g == 0 && hide_edge_spr) ? 0u : ~0u;
-            uint32_t out[2];
+            const uint32_t rlo = __builtin_bitreverse32(((lo0 << 8) | lo1) << f);
+            const uint32_t rhi = __builtin_bitreverse32(((hi0 << 8) | hi1) << f);
 #pragma unroll
             for (int q = 0; q < 2; q++) {
                 // background pattern of the four pixels, one per byte (0..3)
                 const uint32_t nlo = (rlo >> (16 + 4 * q)) & 0xfu, nhi = (rhi >> (16 + 4 * q)) & 0xfu;
                 const uint32_t bgp = (((__umul24(nlo, 0x204081u) & 0x01010101u) |
                                        ((__umul24(nhi, 0x204081u) & 0x01010101u) << 1))) & keep_bg;
-                uint32_t word = byte_perm(bgt, agt, bgp | (q ? tsel1 : tsel0));
+                uint32_t word = byte_perm(gt1, gt0, bgp | (q ? tsel1 : tsel0));
                 if (any_spr) {
-                    const uint32_t c = q ? s1 : s0;
+                    const uint32_t c = q ? cb : ca;
                     const uint32_t opaque = (bgp + 0x7f7f7f7fu) & 0x80808080u;       // background pattern != 0
                     const uint32_t take = c & (~opaque | (c << 1)) & 0x80808080u & keep_sp;
                     const uint32_t tmask = take | (take - (take >> 7));
@@ -818,27 +814,47 @@ struct Console {
                 }
                 out[q] = word;
             }
-            const int xg = 8 * g;
-            // streaming stores: the frame buffers are read by the next kernel only, so they should not
-            // evict the console state from the L2
-            if (xg >= x0 && xg + 8 <= x1) { __builtin_nontemporal_store(out[0], wp); __builtin_nontemporal_store(out[1], wp + np); }
+        };
+        // the group's two words at w (pixels xg .. xg + 7): streaming stores when all 8 pixels are in [x0, x1)
+        // (the frame buffers are read by the next kernel only, so they should not evict the console state from
+        // the L2), else a read-modify-write of the pixels in [x0, x1)
+        auto store_group = [&](int xg, uint32_t* w, const uint32_t (&out)[2]) {
+            if (xg >= x0 && xg + 8 <= x1) { __builtin_nontemporal_store(out[0], w); __builtin_nontemporal_store(out[1], w + np); }
             else {
-                // a partial group: only the pixels in [x0, x1)
 #pragma unroll
                 for (int q = 0; q < 2; q++) {
                     const int xq = xg + 4 * q;
                     const int lo = x0 > xq ? x0 - xq : 0, hi = x1 < xq + 4 ? x1 - xq : 4;
                     if (lo < hi) {
                         const uint32_t in = (uint32_t)((((1ull << (8 * hi)) - 1) >> (8 * lo)) << (8 * lo));
-                        uint32_t* w = wp + q * np;
-                        *w = (*w & ~in) | (out[q] & in);
+                        uint32_t* wq = w + q * np;
+                        *wq = (*wq & ~in) | (out[q] & in);
                     }
                 }
             }
-            wp += 4 * np;
-            alo = show_bg ? clo : 0u; ahi = show_bg ? chi : 0u; agt = show_bg ? cgt : ubg;
-            blo = show_bg ? dlo : 0u; bhi = show_bg ? dhi : 0u; bgt = show_bg ? dgt : ubg;
-            nxa = na; nxb = nb; s0 = spr ? t0 : 0u; s1 = spr ? t1 : 0u;
+        };
+        for (; pg < g1; pg += 4) {
+            uint32_t dlo, dhi, dgt, elo, ehi, egt, flo, fhi, fgt;
+            bg_planes(nxa, fy, bgpal, dlo, dhi, dgt);
+            bg_planes(nxb, fy, bgpal, elo, ehi, egt);
+            bg_planes(nxc, fy, bgpal, flo, fhi, fgt);
+            const uint32_t na = tile_of(pg + 8), nb = tile_of(pg + 9), nc = tile_of(pg + 10);
+            const int ws = 2 * pg + 8 < 60 ? 2 * pg + 8 : 60;
+            const uint32_t t0 = lds_sp[ws * LDS_LANES], t1 = lds_sp[(ws + 1) * LDS_LANES];
+            const uint32_t t2 = lds_sp[(ws + 2) * LDS_LANES], t3 = lds_sp[(ws + 3) * LDS_LANES];
+            uint32_t out0[2], out1[2];
+            // pixels 0-7 may hide either layer
+            group_words(alo, ahi, agt, blo, bhi, bgt, s0, s1, (pg == 0 && hide_edge_bg) ? 0u : ~0u,
+                        (pg == 0 && hide_edge_spr) ? 0u : ~0u, out0);
+            group_words(blo, bhi, bgt, clo, chi, cgt, s2, s3, ~0u, ~0u, out1);
+            store_group(8 * pg, wp, out0);
+            store_group(8 * pg + 8, wp + 2 * np, out1);
+            wp += 8 * np;
+            alo = show_bg ? dlo : 0u; ahi = show_bg ? dhi : 0u; agt = show_bg ? dgt : ubg;
+            blo = show_bg ? elo : 0u; bhi = show_bg ? ehi : 0u; bgt = show_bg ? egt : ubg;
+            clo = show_bg ? flo : 0u; chi = show_bg ? fhi : 0u; cgt = show_bg ? fgt : ubg;
+            nxa = na; nxb = nb; nxc = nc;
+            s0 = spr ? t0 : 0u; s1 = spr ? t1 : 0u; s2 = spr ? t2 : 0u; s3 = spr ? t3 : 0u;
         }
     }
 
