@@ -1221,14 +1221,18 @@ struct Console {
             bool act = !parked;
             if (act && (j >= end || tgt > slice)) { parked = true; act = false; }
             if (act && tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; act = false; }
-            // PRG bytes at pc for the fast paths; the idle check reads 0xff past 0xffff
+            // PRG bytes pc .. pc + 6 for the fast paths, from three aligned LDS words and two byte-aligns (the
+            // words past the last PRG word are the staged CHR bank's first ones: in bounds, and the bytes taken
+            // from them are not used); the idle check reads 0xff past 0xffff
             const bool in_prg = pc >= 0x8000;
-            uint8_t op0 = 0, q1 = 0xff, q2 = 0xff;
-            if (in_prg) {
-                op0 = prg(pc);
-                if (pc != 0xffff) q1 = prg((uint16_t)(pc + 1));
-                if (pc < 0xfffe) q2 = prg((uint16_t)(pc + 2));
-            }
+            const uint32_t pa = pc & 0x7fffu;
+            const uint32_t* pw = (const uint32_t*)cart.prg + (pa >> 2);
+            const uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[2];
+            const uint32_t b0 = __builtin_amdgcn_alignbyte(w1, w0, pa & 3u);   // bytes pc .. pc + 3
+            const uint32_t b4 = __builtin_amdgcn_alignbyte(w2, w1, pa & 3u);   // bytes pc + 4 .. pc + 7
+            const uint8_t op0 = in_prg ? (uint8_t)b0 : (uint8_t)0;
+            const uint8_t q1 = in_prg && pc != 0xffff ? (uint8_t)(b0 >> 8) : (uint8_t)0xff;
+            const uint8_t q2 = in_prg && pc < 0xfffe ? (uint8_t)(b0 >> 16) : (uint8_t)0xff;
             if (act && in_prg && op0 == 0x4c && (uint16_t)(q1 | q2 << 8) == pc) {
                 const int32_t lim_end = end - j, lim_nmi = nmi_thresh - tgt;
                 const int32_t k1 = lim_end > 0 ? (lim_end + 2) / 3 : 0;
@@ -1236,9 +1240,9 @@ struct Console {
                 const int32_t k = k1 < k2 ? k1 : k2;
                 if (k > 1) { exec_at = j + 3 * (k - 1); zero_skip = 0; act = false; }
             }
-            if (act && in_prg && op0 == 0xad && q1 == 0x02 && q2 == 0x20 && pc <= 0xfff8 && prg(pc + 3) == 0x29 &&
-                prg(pc + 4) == 0x40 && prg(pc + 6) == 0xf9) {
-                const uint8_t br = prg(pc + 5);
+            // LDA $2002 / AND #$40 / BEQ|BNE back to the LDA: bytes AD 02 20 29 40 (F0|D0) F9
+            if (act && in_prg && pc <= 0xfff8 && b0 == 0x292002adu && (b4 & 0x00ff00ffu) == 0x00f90040u) {
+                const uint8_t br = (uint8_t)(b4 >> 8);
                 if (br == 0xf0 || br == 0xd0) {
                     if (ppu_calls < tgt) { want = tgt; act = false; }   // the sync of the LDA $2002 at j
                     else if (poll_skip(j, end, br == 0xf0)) act = false;
