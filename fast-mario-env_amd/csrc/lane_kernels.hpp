@@ -102,8 +102,8 @@ __device__ __forceinline__ uint32_t pick4(const uint32_t (&m)[4], uint32_t i) {
 // dy0 .. dy1-1 only (a band; out still addresses row 0). The words of source row sy + 1 are loaded while
 // row sy is summed: the distinct source rows of consecutive output rows are consecutive.
 __device__ __forceinline__ void area_columns4(const uint32_t* g0, const uint32_t* g1, uint32_t np, uint32_t e,
-                                              bool pool, int chunk, const AreaTables* T, uint8_t* out,
-                                              size_t col_stride, size_t row_stride, int dy0 = 0, int dy1 = 84) {
+                                              bool pool, int chunk, const AreaTables* T, uint32_t* out,
+                                              size_t row_stride, int dy0 = 0, int dy1 = 84) {
     const int c0 = 4 * chunk;
     const uint32_t wl = (uint32_t)T->xs[c0 * TAPS] >> 2;
     int nx[4];
@@ -162,8 +162,9 @@ __device__ __forceinline__ void area_columns4(const uint32_t* g0, const uint32_t
                 acc[q] = j == 0 ? term : acc[q] + term;
             }
         }
-#pragma unroll
-        for (int q = 0; q < 4; q++) out[(size_t)dy * row_stride + (size_t)q * col_stride] = round_sat(acc[q]);
+        // the four output pixels of the row as one word (pixel 4 chunk + q in byte q)
+        out[(size_t)dy * row_stride] = (uint32_t)round_sat(acc[0]) | (uint32_t)round_sat(acc[1]) << 8 |
+                                       (uint32_t)round_sat(acc[2]) << 16 | (uint32_t)round_sat(acc[3]) << 24;
     }
 }
 

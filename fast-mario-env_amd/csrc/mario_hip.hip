@@ -128,7 +128,7 @@ struct ObsArgs {
     const uint32_t* ev;
     const uint8_t* gray;          // 2 frame buffers of np lanes (4-pixel words)
     const uint8_t* boot_obs;      // [level * OBS_PIX + o]
-    uint8_t* out;                 // [o * np + e]
+    uint8_t* out;                 // word w (pixels 4w .. 4w+3) of env e at 32-bit word [w * np + e]
     const AreaTables* T;
 };
 // New observation of every env: the boot observation right after a reset, else INTER_AREA of the last
@@ -141,26 +141,27 @@ __global__ void __launch_bounds__(192) k_obs(ObsArgs A) {
     const uint32_t e = blockIdx.y * 64 + (threadIdx.x & 63);
     const int chunk = blockIdx.x * 3 + (threadIdx.x >> 6);
     if (e >= (uint32_t)A.n || chunk >= 21) return;
-    uint8_t* out = A.out + (size_t)(4 * chunk) * A.np + e;
-    const size_t row_stride = (size_t)84 * A.np;
+    uint32_t* out = (uint32_t*)A.out + (size_t)chunk * A.np + e;   // word (row, chunk): pixels 4 chunk .. + 3
+    const size_t row_stride = (size_t)21 * A.np;
     const int dy0 = OBS_BAND_ROWS * blockIdx.z, dy1 = dy0 + OBS_BAND_ROWS;   // this workgroup's output rows
     if (A.ev[(size_t)E_SHOWS_BOOT * A.np + e]) {
         const uint8_t* src = A.boot_obs + (size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + 4 * chunk;
         for (int dy = dy0; dy < dy1; dy++)
-            for (int q = 0; q < 4; q++) out[(size_t)dy * row_stride + (size_t)q * A.np] = src[dy * 84 + q];
+            out[(size_t)dy * row_stride] = (uint32_t)src[dy * 84] | (uint32_t)src[dy * 84 + 1] << 8 |
+                                           (uint32_t)src[dy * 84 + 2] << 16 | (uint32_t)src[dy * 84 + 3] << 24;
         return;
     }
     const uint32_t pw = A.ev[(size_t)E_POOLED * A.np + e];
     const uint32_t* g0 = (const uint32_t*)A.gray;
     const uint32_t* g1 = (const uint32_t*)(A.gray + (size_t)GRAY_PIX * A.np);
     if (pw & 2) { const uint32_t* t = g0; g0 = g1; g1 = t; }
-    area_columns4(g0, g1, A.np, e, (pw & 1) != 0, chunk, A.T, out, A.np, row_stride, dy0, dy1);
+    area_columns4(g0, g1, A.np, e, (pw & 1) != 0, chunk, A.T, out, row_stride, dy0, dy1);
 }
 
 struct StackArgs {
     int n; uint32_t np; int K;
     uint8_t* obs; uint8_t* fin;   // [e][K][OBS_PIX]
-    const uint8_t* fresh;         // [o * np + e]
+    const uint8_t* fresh;         // word w (pixels 4w .. 4w+3) of env e at 32-bit word [w * np + e]
     const uint32_t* ev;
     const uint8_t* cobs;          // [ci * OBS_PIX + o]
     int mode;                     // 0 step, 1 reset
@@ -177,9 +178,7 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
             const int wl = idx >> 6, j = idx & 63;
             const uint32_t e = e0 + j;
             uint32_t val = 0;
-            if (w0 + wl < nw && e < (uint32_t)A.n)
-                for (int b = 0; b < 4; b++)
-                    val |= (uint32_t)A.fresh[(size_t)(4 * (w0 + wl) + b) * A.np + e] << (8 * b);
+            if (w0 + wl < nw && e < (uint32_t)A.n) val = ((const uint32_t*)A.fresh)[(size_t)(w0 + wl) * A.np + e];
             tile[wl][j] = val;
         }
     }
