@@ -12,12 +12,19 @@ enum EnvWord : int {
     E_EPRET_LO, E_EPRET_HI, E_SHOWS_BOOT, E_POOLED, E_LEVEL, E_FRAMES_LO, E_FRAMES_HI,
     E_BAD, E_INSTR_LO, E_INSTR_HI,
     E_RNG_S0, E_RNG_S1, E_RNG_S2, E_RNG_S3, E_RNG_I0, E_RNG_I1, E_RNG_I2, E_RNG_I3,   // little-endian u32 limbs
-    E_RNG_HAS32, E_RNG_HALF, E_DONE, E_RESET_IDX, E_COUNT
+    E_RNG_HAS32, E_RNG_HALF, E_DONE, E_RESET_IDX,
+    E_FF_LO, E_FF_HI,                                  // poll-loop instructions fast-forwarded (in E_INSTR too)
+    E_REEMU_ONE, E_REEMU_PAIR, E_REEMU_K2,             // early-termination re-emulations by kind (REEMU_*)
+    E_COUNT
 };
 
 constexpr int MAX_SKIP = 16;
+// Kinds of early-termination re-emulation (an agent step whose episode ended at frame last < K-1), by the
+// reference's branches (fastmario.cpp:351-362): ONE re-runs frame last alone, PAIR re-runs its max-pool
+// partner last-1 too; K2 marks an end at frame K-2 under max-pool, where frame last was rendered in the
+// first pass and only the partner runs again.
+enum : uint32_t { REEMU_ONE = 1u, REEMU_PAIR = 2u, REEMU_K2 = 4u };
 constexpr int HACK_FRAME_LIMIT = 20000;   // guard against a game stuck in a busy state (the reference loops forever)
-constexpr uint32_t ERR_HACK_LIMIT = 1u << 24;
 
 __device__ __constant__ static const uint8_t kButtons[8] = {0x00, 0x80, 0x81, 0x82, 0x83, 0x01, 0x40, 0x00};
 
@@ -190,6 +197,7 @@ struct EnvRegs {
     bool shows_boot, pooled, slot_swap;   // slot_swap: the last frame is in frame buffer 1
     uint64_t frames;
     uint32_t draws;     // sticky draws taken (counted by the reset-cache builder)
+    uint32_t reemu;     // REEMU_* bits of the last agent step
     Info info;
 };
 
@@ -258,7 +266,7 @@ struct Stepper {
         int i = 0, guard = 0;
         int rf = -1;                       // agent frame being re-emulated (-1: the first pass)
         uint8_t b_prev = 0, b_cur = 0;     // buttons of agent frames i-1 and i
-        uint32_t n0 = 0, b0 = 0;           // instruction and bad-op counters at the start of agent frame i
+        uint32_t n0 = 0, b0 = 0, f0 = 0;   // instruction, bad-op and fast-forward counters at the start of agent frame i
         int it = 0, resume_at = 0;         // loop iterations so far; the iteration a re-emulation starts at
         uint8_t* slot = gray0;
         for (;;) {
@@ -278,7 +286,7 @@ struct Stepper {
                 buttons = b_cur;
                 render = want_obs && (i == K - 1 || (mp && i == K - 2));
                 slot = ((K - 1 - i) & 1) ? gray1 : gray0;
-                n0 = c.instructions; b0 = c.bad_ops;
+                n0 = c.instructions; b0 = c.bad_ops; f0 = c.ff_instructions;
                 // re-emulations start at frame last-1 (max-pool, last >= 1) or last, for last < K-1, and
                 // never at K-2 (max-pool)
                 if (want_obs && i < K - 1 && (!mp || i <= K - 3)) save_console(c, live, snap(i & 1));
@@ -310,9 +318,10 @@ struct Stepper {
                     // frame i was rendered: count its re-emulation (it ended the episode, so it had no hack
                     // frames), and re-emulate its max-pool partner i-1 if there is one
                     ev.frames++;
-                    const uint32_t dn = c.instructions - n0, db = (c.bad_ops - b0) & ~ERR_HACK_LIMIT;
+                    const uint32_t dn = c.instructions - n0, db = (c.bad_ops - b0) & ~ERR_FLAGS;
                     c.instructions += dn;
                     c.bad_ops += db;
+                    c.ff_instructions += c.ff_instructions - f0;
                     if (i == 0) break;
                     save_console(c, live, snap(i & 1));
                     keep_last = true;
@@ -337,6 +346,9 @@ struct Stepper {
             }
         }
         const int last = i;
+        ev.reemu = (want_obs && done && last < K - 1)
+                       ? ((mp && last >= 1) ? REEMU_PAIR : REEMU_ONE) | ((mp && last == K - 2) ? REEMU_K2 : 0u)
+                       : 0u;
         if (want_obs) {
             ev.pooled = mp && last >= 1;
             ev.slot_swap = ((K - 1 - last) & 1) != 0;

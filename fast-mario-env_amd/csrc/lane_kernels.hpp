@@ -204,7 +204,7 @@ __device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* me
     c.lds_bg = x.gp + LDS_GP_WORDS * LDS_LANES; c.bg_key = -1;
     c.lds_oam = x.gp + (LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES;
     c.twin = x.twin;
-    c.bad_ops = 0; c.instructions = 0;
+    c.bad_ops = 0; c.instructions = 0; c.ff_instructions = 0;
     c.pend_line = -1; c.sp_line = -1; c.pal_dirty = true;
 }
 
@@ -231,7 +231,7 @@ struct CacheArgs {
     uint8_t* gray;                       // 2 frame buffers of ncp lanes (4-pixel words)
     uint8_t* snap_mem; uint32_t* snap_sc;  // 2 snapshot slots of the cache consoles' layout
     int64_t* cx; int64_t* ct; int32_t* clives; int32_t* cdraws; uint8_t* cboot;
-    uint64_t* cframes; uint64_t* cinstr; uint32_t* cbad;
+    uint64_t* cframes; uint64_t* cinstr; uint64_t* cff; uint32_t* cbad;
 };
 
 struct StepArgs {
@@ -255,7 +255,7 @@ struct ResetArgs {
     uint8_t* mem; uint32_t* sc; uint32_t* ev;
     const uint8_t* cmem; const uint32_t* csc;
     const int64_t* cx; const int64_t* ct; const int32_t* clives; const int32_t* cdraws; const uint8_t* cboot;
-    const uint64_t* cframes; const uint64_t* cinstr; const uint32_t* cbad;
+    const uint64_t* cframes; const uint64_t* cinstr; const uint64_t* cff; const uint32_t* cbad;
     int all;
 };
 
@@ -266,7 +266,7 @@ struct RawArgs {
     uint8_t* screen;             // [pix * np + e], palette values
     const uint8_t* buttons;      // n
     int render;
-    uint32_t* bad; uint32_t* instr;
+    uint32_t* bad; uint32_t* instr; uint32_t* ff;
     int power_on;
 };
 
@@ -357,7 +357,7 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     c.store(A.sc, ci);
     A.cx[ci] = ev.x_last; A.ct[ci] = ev.time_last; A.clives[ci] = ev.lives;
     A.cdraws[ci] = (int32_t)ev.draws; A.cboot[ci] = ev.shows_boot;
-    A.cframes[ci] = ev.frames; A.cinstr[ci] = c.instructions; A.cbad[ci] = c.bad_ops;
+    A.cframes[ci] = ev.frames; A.cinstr[ci] = c.instructions; A.cff[ci] = c.ff_instructions; A.cbad[ci] = c.bad_ops;
 }
 
 // One agent step of env e (fastmario.cpp:403-411 + 336-374).
@@ -390,7 +390,10 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     A.ev[(size_t)E_DONE * A.np + e] = done;
     add_counter(A.ev, A.np, e, E_FRAMES_LO, ev.frames);
     add_counter(A.ev, A.np, e, E_INSTR_LO, c.instructions);
+    add_counter(A.ev, A.np, e, E_FF_LO, c.ff_instructions);
     A.ev[(size_t)E_BAD * A.np + e] += c.bad_ops;
+    for (int k = 0; k < 3; k++)
+        if ((ev.reemu >> k) & 1u) A.ev[(size_t)(E_REEMU_ONE + k) * A.np + e] += 1;
 }
 
 // Auto-reset (fastmario.cpp:389-401): k = integers(noop_max + 1) from the env's stream, the draws of
@@ -417,6 +420,7 @@ __device__ inline int reset_lane(const ResetArgs& A, uint32_t e) {
     // the no-op steps count as emulated work, as on the reference CPU path
     add_counter(E, A.np, e, E_FRAMES_LO, A.cframes[ci]);
     add_counter(E, A.np, e, E_INSTR_LO, A.cinstr[ci]);
+    add_counter(E, A.np, e, E_FF_LO, A.cff[ci]);
     E[E_BAD * np + e] += A.cbad[ci];
     return ci;
 }
@@ -437,6 +441,7 @@ __device__ inline void raw_lane(const RawArgs& A, const LaneCtx& x, uint32_t e) 
     c.store(A.sc, e);
     A.bad[e] += c.bad_ops;
     A.instr[e] += c.instructions;
+    A.ff[e] += c.ff_instructions;
 }
 
 // Canonical state dump of console e (layout in include/mario_hip.h).

@@ -10,6 +10,8 @@
 
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -323,7 +325,7 @@ struct MhEnv {
     uint32_t* csnap_sc = nullptr;
     int64_t *cx = nullptr, *ct = nullptr;
     int32_t *clives = nullptr, *cdraws = nullptr;
-    uint64_t *cframes = nullptr, *cinstr = nullptr;
+    uint64_t *cframes = nullptr, *cinstr = nullptr, *cff = nullptr;
     uint32_t* cbad = nullptr;
     uint8_t *obs = nullptr, *fin = nullptr, *term = nullptr, *trunc = nullptr;
     float* rew = nullptr;
@@ -337,7 +339,7 @@ struct MhEnv {
 
     ResetArgs reset_args(int all) const {
         return ResetArgs{n, np, cfg, nk, ncp, mem, sc, ev, cmem, csc, cx, ct, clives, cdraws, cboot,
-                         cframes, cinstr, cbad, all};
+                         cframes, cinstr, cff, cbad, all};
     }
     StackArgs stack_args(int mode) const { return StackArgs{n, np, K, obs, fin, fresh, ev, cobs, mode}; }
 };
@@ -348,7 +350,7 @@ struct MhRaw {
     DevBufs B;
     RomArgs R{};
     uint8_t *mem = nullptr, *screen = nullptr, *bk_mem = nullptr;
-    uint32_t *sc = nullptr, *bk_sc = nullptr, *bad = nullptr, *instr = nullptr;
+    uint32_t *sc = nullptr, *bk_sc = nullptr, *bad = nullptr, *instr = nullptr, *ff = nullptr;
 };
 
 extern "C" {
@@ -445,6 +447,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     h->cx = B.alloc<int64_t>(h->nc, good); h->ct = B.alloc<int64_t>(h->nc, good);
     h->clives = B.alloc<int32_t>(h->nc, good); h->cdraws = B.alloc<int32_t>(h->nc, good);
     h->cframes = B.alloc<uint64_t>(h->nc, good); h->cinstr = B.alloc<uint64_t>(h->nc, good);
+    h->cff = B.alloc<uint64_t>(h->nc, good);
     h->cbad = B.alloc<uint32_t>(h->nc, good);
     uint32_t* d_err = B.alloc<uint32_t>(1, good);
     if (!good) return fail();
@@ -481,7 +484,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nl), dim3(256), 0, 0, so);
     CacheArgs ca{h->R, h->cfg, h->key_bank, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
                  h->cmem, h->csc, h->cgray, h->csnap_mem, h->csnap_sc, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
-                 h->cframes, h->cinstr, h->cbad};
+                 h->cframes, h->cinstr, h->cff, h->cbad};
     hipLaunchKernelGGL(k_cache, emu_grid(h->nc), dim3(EMU_THREADS), 0, 0, ca);
     if (!ok(hipGetLastError(), "k_cache launch")) return fail();
     SmallObsArgs co{h->cgray, h->ncp, h->cboot, h->boot_obs, h->nk, h->cobs, h->nc, h->T};
@@ -493,9 +496,34 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     return h;
 }
 
+// A buffer the kernels may write: device memory of the env's GPU or pinned host memory, aligned to `align`.
+static bool kernel_writable(const MhEnv* h, const void* p, uintptr_t align, const char* name) {
+    if (((uintptr_t)p & (align - 1)) != 0) {
+        g_err = std::string(name) + ": not aligned to " + std::to_string(align) + " bytes";
+        return false;
+    }
+    hipPointerAttribute_t at;
+    const hipError_t e = hipPointerGetAttributes(&at, p);
+    (void)hipGetLastError();   // a refused host pointer must not surface as the error of a later launch
+    const bool dev = e == hipSuccess && at.type == hipMemoryTypeDevice && at.device == h->device;
+    const bool pinned = e == hipSuccess && (at.type == hipMemoryTypeHost || at.type == hipMemoryTypeManaged);
+    if (!dev && !pinned) {
+        g_err = std::string(name) + ": neither device memory of GPU " + std::to_string(h->device) +
+                " nor pinned host memory (pageable host memory cannot be written by the kernels)";
+        return false;
+    }
+    return true;
+}
+
 int mh_set_buffers(MhEnv* h, uint8_t* obs, uint8_t* fin, float* rew, uint8_t* term, uint8_t* trunc,
                    int32_t* info, double* ep_ret, int32_t* ep_len) {
     if (!h || !obs || !fin || !rew || !term || !trunc || !info || !ep_ret || !ep_len) { g_err = "null buffer"; return -1; }
+    if (!ok(hipSetDevice(h->device), "hipSetDevice")) return -1;
+    if (!kernel_writable(h, obs, 4, "obs") || !kernel_writable(h, fin, 4, "final_obs") ||
+        !kernel_writable(h, rew, 4, "rew") || !kernel_writable(h, term, 1, "term") ||
+        !kernel_writable(h, trunc, 1, "trunc") || !kernel_writable(h, info, 4, "info") ||
+        !kernel_writable(h, ep_ret, 8, "ep_ret") || !kernel_writable(h, ep_len, 4, "ep_len"))
+        return -1;
     h->obs = obs; h->fin = fin; h->rew = rew; h->term = term; h->trunc = trunc; h->info = info;
     h->ep_ret = ep_ret; h->ep_len = ep_len;
     return 0;
@@ -602,6 +630,13 @@ static int64_t sum_words(const MhEnv* h, int lo_word, bool wide) {
 int64_t mh_frames(MhEnv* h) { return h ? sum_words(h, E_FRAMES_LO, true) : -1; }
 int64_t mh_bad_ops(MhEnv* h) { return h ? sum_words(h, E_BAD, false) : -1; }
 int64_t mh_instructions(MhEnv* h) { return h ? sum_words(h, E_INSTR_LO, true) : -1; }
+int64_t mh_ff_instructions(MhEnv* h) { return h ? sum_words(h, E_FF_LO, true) : -1; }
+int mh_reemulations(MhEnv* h, int64_t* out) {
+    if (!h || !out) { g_err = "null handle or buffer"; return -1; }
+    for (int k = 0; k < 3; k++)
+        if ((out[k] = sum_words(h, E_REEMU_ONE + k, false)) < 0) { g_err = "counter read failed"; return -1; }
+    return 0;
+}
 
 int mh_env_ram(MhEnv* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
@@ -656,6 +691,7 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     h->screen = B.alloc<uint8_t>((size_t)GRAY_PIX * h->np, good);
     h->bad = B.alloc<uint32_t>(h->np, good);
     h->instr = B.alloc<uint32_t>(h->np, good);
+    h->ff = B.alloc<uint32_t>(h->np, good);
     if (!good) { delete h; return nullptr; }
     uint8_t ident[256];
     for (int i = 0; i < 256; i++) ident[i] = (uint8_t)i;
@@ -664,14 +700,14 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     h->R.rom = d_rom; h->R.lut = d_lut; h->R.n_chr = 1;
     h->R.nt_bits = 0;
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
-    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, 1};
+    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, h->ff, 1};
     hipLaunchKernelGGL(k_raw, emu_grid(h->n), dim3(EMU_THREADS), 0, 0, ra);
     if (!ok(hipDeviceSynchronize(), "raw power-on")) { delete h; return nullptr; }
     return h;
 }
 int mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream) {
     if (!h || !d_buttons) return -1;
-    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, d_buttons, render, h->bad, h->instr, 0};
+    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, d_buttons, render, h->bad, h->instr, h->ff, 0};
     hipLaunchKernelGGL(k_raw, emu_grid(h->n), dim3(EMU_THREADS), 0, (hipStream_t)stream, ra);
     CK(hipGetLastError());
     return 0;
@@ -725,6 +761,7 @@ static int64_t raw_sum(MhRaw* h, uint32_t* d) {
 }
 int64_t mh_raw_bad_ops(MhRaw* h) { return h ? raw_sum(h, h->bad) : -1; }
 int64_t mh_raw_instructions(MhRaw* h) { return h ? raw_sum(h, h->instr) : -1; }
+int64_t mh_raw_ff_instructions(MhRaw* h) { return h ? raw_sum(h, h->ff) : -1; }
 void mh_raw_destroy(MhRaw* h) {
     if (!h) return;
     (void)hipSetDevice(h->device);
@@ -732,14 +769,27 @@ void mh_raw_destroy(MhRaw* h) {
     delete h;
 }
 
+// mh_resize's tables: one copy per device, allocated on the device's first call and kept until the process ends.
+static std::mutex g_tables_mu;
+static std::map<int, AreaTables*> g_tables;
+
 int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
-    if (!d_src || !d_dst || n < 1) { g_err = "invalid arguments"; return -1; }
-    static AreaTables* d_T = nullptr;
-    if (!d_T) {
-        AreaTables T;
-        area_tables(&T);
-        CK(hipMalloc(&d_T, sizeof(T)));
-        CK(hipMemcpy(d_T, &T, sizeof(T), hipMemcpyHostToDevice));
+    if (!d_src || !d_dst || n < 1 || n > MH_RESIZE_MAX_IMAGES) { g_err = "invalid arguments (n must be 1..65535)"; return -1; }
+    int dev = 0;
+    CK(hipGetDevice(&dev));
+    AreaTables* d_T = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_tables_mu);
+        auto it = g_tables.find(dev);
+        if (it == g_tables.end()) {
+            AreaTables T;
+            area_tables(&T);
+            CK(hipMalloc(&d_T, sizeof(T)));
+            if (!ok(hipMemcpy(d_T, &T, sizeof(T), hipMemcpyHostToDevice), "upload tables")) { (void)hipFree(d_T); return -1; }
+            g_tables[dev] = d_T;
+        } else {
+            d_T = it->second;
+        }
     }
     hipLaunchKernelGGL(k_resize_images, dim3((OBS_PIX + 255) / 256, n), dim3(256), 0, (hipStream_t)stream, d_src, d_dst, n, d_T);
     CK(hipGetLastError());

@@ -47,6 +47,11 @@ __device__ __forceinline__ size_t vram_word_offset(uint32_t np, uint32_t e, uint
     return (size_t)ROW_VRAM * np + ((size_t)w * np + e) * 4;
 }
 enum : uint8_t { FN = 0x01, FV = 0x02, FONE = 0x04, FB = 0x08, FD = 0x10, FI = 0x20, FZ = 0x40, FC = 0x80 };
+// Error flags or-ed into a console's bad-op counter (every parity check requires a zero count):
+// ERR_HACK_LIMIT  the env layer's busy-state loop hit its frame limit;
+// ERR_TWIN        a sprite evaluation ran on one twin lane without the other, so the sprite-range half it
+//                 read from its partner's exchange word was stale.
+constexpr uint32_t ERR_HACK_LIMIT = 1u << 24, ERR_TWIN = 1u << 25, ERR_FLAGS = ERR_HACK_LIMIT | ERR_TWIN;
 enum : uint8_t { ST_PRE = 0, ST_RENDER = 1, ST_POST = 2, ST_VBLANK = 3 };
 
 // Scalar words of one console, interleaved as SC[w * NP + e].
@@ -220,7 +225,8 @@ struct Console {
     int32_t pcyc, scanline;
     uint16_t v, t, inc;
     // ---- counters
-    uint32_t bad_ops, instructions;
+    uint32_t bad_ops, instructions;          // instructions: retired, poll-loop fast-forwards included
+    uint32_t ff_instructions;                // of those, the ones poll_skip fast-forwarded without executing
     // ---- derived state (not part of the machine state)
     int32_t pend_line;       // scanline of a sprite evaluation not yet materialized (-1: the list is current)
     int32_t sp_line;         // scanline the LDS sprite line buffer holds (-1: invalid)
@@ -505,6 +511,7 @@ struct Console {
         // The env's twin lanes each test one half of OAM (twin t: sprites 32 t .. 32 t + 31) into exchange word
         // t of the env, then both read both words. The wave barrier is a convergence point: every lane active
         // here has stored its word before any lane loads (a wave's LDS accesses complete in order).
+        if (!((__ballot(1) >> (__lane_id() ^ 32u)) & 1ull)) bad_ops |= ERR_TWIN;   // the partner must be here
         uint32_t half = 0;
 #pragma unroll
         for (int i = 0; i < 32; i++)
@@ -1165,6 +1172,7 @@ struct Console {
         exec_at = j + k * c;
         zero_skip = 0;
         instructions += 3 * (uint32_t)k;
+        ff_instructions += 3 * (uint32_t)k;
         return true;
     }
 

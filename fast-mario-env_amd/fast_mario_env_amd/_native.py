@@ -47,7 +47,7 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).argtypes = [_P, _P]
     L.mh_step_async.argtypes = [_P, _P, _P]
     L.mh_destroy.argtypes = [_P]
-    for f in ("mh_frames", "mh_bad_ops", "mh_instructions", "mh_env_bytes"):
+    for f in ("mh_frames", "mh_bad_ops", "mh_instructions", "mh_ff_instructions", "mh_env_bytes"):
         getattr(L, f).restype = _i64
         getattr(L, f).argtypes = [_P]
     for f in ("mh_env_ram", "mh_env_canon", "mh_level_canon", "mh_level_obs"):
@@ -62,11 +62,12 @@ def lib() -> ctypes.CDLL:
     L.mh_raw_screen_rgb.argtypes = [_P, _P, _P, _P]
     for f in ("mh_raw_backup", "mh_raw_restore"):
         getattr(L, f).argtypes = [_P, _P]
-    for f in ("mh_raw_bad_ops", "mh_raw_instructions"):
+    for f in ("mh_raw_bad_ops", "mh_raw_instructions", "mh_raw_ff_instructions"):
         getattr(L, f).restype = _i64
         getattr(L, f).argtypes = [_P]
     L.mh_raw_destroy.argtypes = [_P]
     L.mh_resize.argtypes = [_P, _P, _i32, _P]
+    L.mh_reemulations.argtypes = [_P, _P]
     L.mh_replay_add.argtypes = [_P] * 7 + [_i32] * 4 + [_P] * 7
     L.mh_replay_gather.argtypes = [_P] * 5 + [_i32] * 4 + [_P, _P, _i32, _i32] + [_P] * 10
     L.mh_timing.argtypes = [_P, _i32]

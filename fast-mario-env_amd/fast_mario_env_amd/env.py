@@ -15,6 +15,7 @@ final_obs. Every step runs as gfx950 kernels (libmario_hip.so) on torch's curren
 """
 from __future__ import annotations
 
+import csv
 import json
 import os
 import time
@@ -83,23 +84,45 @@ def _stream(torch, dev):
 
 
 class MonitorCSV:
-    """SB3 VecMonitor-compatible monitor.monitor.csv writer (columns r,l,t,x_pos,flag_get); env.py:93-110."""
+    """Episode log in the monitor.csv format that Stable-Baselines3's VecMonitor / load_results read: a
+    ``#``-prefixed JSON line with the start time, a header, then one row per finished episode with the return,
+    length, wall time since the start and the final x_pos / flag_get (the columns of the reference's
+    env.py:93-110).
 
-    def __init__(self, path: str):
-        if not path.endswith(".monitor.csv"):
-            path = os.path.join(path, "monitor.monitor.csv") if os.path.isdir(path) else path + ".monitor.csv"
-        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
-        self.f = open(path, "w")
-        self.f.write("#%s\n" % json.dumps({"t_start": time.time(), "env_id": "None"}))
-        self.f.write("r,l,t,x_pos,flag_get\n")
-        self.f.flush()
+    `path` may name the file itself (ending in ``.monitor.csv``), an existing directory (the file is then
+    ``monitor.monitor.csv`` inside it), or a prefix to which ``.monitor.csv`` is appended."""
 
-    def write(self, e: dict):
-        self.f.write(f"{e['r']},{e['l']},{e['t']},{e['x_pos']},{e['flag_get']}\n")
-        self.f.flush()
+    COLUMNS = ("r", "l", "t", "x_pos", "flag_get")
+    SUFFIX = ".monitor.csv"
+
+    @classmethod
+    def resolve(cls, path) -> str:
+        path = os.fspath(path)
+        if path.endswith(cls.SUFFIX):
+            return path
+        if os.path.isdir(path):
+            return os.path.join(path, "monitor" + cls.SUFFIX)
+        return path + cls.SUFFIX
+
+    def __init__(self, path):
+        self.path = self.resolve(path)
+        parent = os.path.dirname(os.path.abspath(self.path))
+        os.makedirs(parent, exist_ok=True)
+        self._fh = open(self.path, "w", newline="")
+        meta = {"t_start": time.time(), "env_id": "None"}
+        self._fh.write("#" + json.dumps(meta) + "\n")
+        self._rows = csv.writer(self._fh, lineterminator="\n")
+        self._rows.writerow(self.COLUMNS)
+        self._fh.flush()
+
+    def write(self, episode: dict):
+        """Append one finished episode (a dict with the COLUMNS keys) and flush it to disk."""
+        self._rows.writerow([episode[c] for c in self.COLUMNS])
+        self._fh.flush()
 
     def close(self):
-        self.f.close()
+        if not self._fh.closed:
+            self._fh.close()
 
 
 class HipVecEnv:
@@ -241,7 +264,21 @@ class HipVecEnv:
         return int(lib().mh_bad_ops(self.h))
 
     def instructions(self) -> int:
+        """6502 instructions retired so far (poll-loop fast-forwards included, as the reference counts them)."""
         return int(lib().mh_instructions(self.h))
+
+    def ff_instructions(self) -> int:
+        """Of instructions(), those the exact sprite-0 poll-loop fast-forward retired without executing."""
+        return int(lib().mh_ff_instructions(self.h))
+
+    REEMU_KINDS = ("one", "pair", "k2")
+
+    def reemulations(self) -> dict:
+        """Early-termination re-emulations so far: 'one' (frame last re-run alone), 'pair' (its max-pool
+        partner re-run too), and 'k2' (of both, the episode ends at frame K-2 under max-pool)."""
+        out = np.zeros(3, np.int64)
+        check(lib().mh_reemulations(self.h, out.ctypes.data), "mh_reemulations")
+        return dict(zip(self.REEMU_KINDS, out.tolist()))
 
     def bytes_per_env(self) -> int:
         return int(lib().mh_env_bytes(self.h))
@@ -301,10 +338,50 @@ class FastVecEnv:
         self._closed = False
 
     def set_buffers(self, obs, fin, rew, term, trunc, info, ep_ret, ep_len):
-        """Point the outputs at other device buffers (torch tensors on the env's device, or raw device
-        addresses); info is int32 (N, 10) and ep_len int32 here. The caller keeps them alive."""
-        addr = [x if isinstance(x, int) else _ptr(x) for x in (obs, fin, rew, term, trunc, info, ep_ret, ep_len)]
+        """Have every step write its outputs into caller-owned buffers (env.py:183-188 of the reference).
+
+        * numpy arrays (the reference's form): obs / fin (N, k, 84, 84) uint8, rew (N,) float32, term / trunc
+          (N,) uint8 or bool, info (N, 10) int64 (int32 accepted), ep_ret (N,) float64, ep_len (N,) int64 (int32
+          accepted). reset() and step_wait() copy the results into them; fin / ep_ret / ep_len rows change only
+          for envs whose episode ended, as in the reference.
+        * torch tensors on the env's GPU or raw device addresses: the kernels write them directly (info and
+          ep_len int32). The library refuses pageable host memory, memory of another GPU and misaligned
+          buffers; step_wait() keeps returning copies of the env's own buffers, so read yours.
+        The caller keeps the buffers alive."""
+        bufs = (obs, fin, rew, term, trunc, info, ep_ret, ep_len)
+        if all(isinstance(b, np.ndarray) for b in bufs):
+            n, k = self.n, self.k
+            want = (((n, k, OBS_HW, OBS_HW), (np.uint8,)), ((n, k, OBS_HW, OBS_HW), (np.uint8,)),
+                    ((n,), (np.float32,)), ((n,), (np.uint8, np.bool_)), ((n,), (np.uint8, np.bool_)),
+                    ((n, len(INFO_FIELDS)), (np.int64, np.int32)), ((n,), (np.float64,)), ((n,), (np.int64, np.int32)))
+            names = ("obs", "fin", "rew", "term", "trunc", "info", "ep_ret", "ep_len")
+            for b, (shape, dts), nm in zip(bufs, want, names):
+                if b.shape != shape or b.dtype.type not in dts:
+                    raise ValueError(f"set_buffers: {nm} must be {shape} of {[d.__name__ for d in dts]}, "
+                                     f"got {b.shape} {b.dtype}")
+            self._host_bufs = dict(zip(names, bufs))
+            return
+        if any(isinstance(b, np.ndarray) for b in bufs):
+            raise ValueError("set_buffers: pass all eight buffers as numpy arrays or all as device buffers")
+        addr = [x if isinstance(x, int) else _ptr(x) for x in bufs]
         check(lib().mh_set_buffers(self.venv.h, *addr), "mh_set_buffers")
+        self._host_bufs = None
+
+    def _fill_host(self, obs, rew=None, term=None, trunc=None, info=None, done=None, fin=None, epr=None, epl=None):
+        hb = getattr(self, "_host_bufs", None)
+        if not hb:
+            return
+        hb["obs"][...] = obs
+        if rew is None:
+            return
+        hb["rew"][...] = rew
+        hb["term"][...] = term
+        hb["trunc"][...] = trunc
+        hb["info"][...] = info
+        if done is not None and done.size:
+            hb["fin"][done] = fin
+            hb["ep_ret"][done] = epr[done]
+            hb["ep_len"][done] = epl[done]
 
     @property
     def frames(self) -> int:
@@ -318,6 +395,7 @@ class FastVecEnv:
 
     def reset(self):
         obs = self.venv.reset().cpu().numpy()
+        self._fill_host(obs)
         return obs.copy() if self.copy_obs else obs
 
     def step_async(self, actions):
@@ -333,11 +411,13 @@ class FastVecEnv:
         term = v.term.cpu().numpy().astype(bool)
         trunc = v.trunc.cpu().numpy().astype(bool)
         rew = v.rew.cpu().numpy().copy()
-        inf = v.info_t.cpu().numpy().astype(np.int64).tolist()
+        info_arr = v.info_t.cpu().numpy().astype(np.int64)
+        inf = info_arr.tolist()
         done = np.flatnonzero(term | trunc)
         fin = v.final_obs[done].cpu().numpy() if done.size else None
         epr = v.ep_ret.cpu().numpy() if done.size else None
         epl = v.ep_len.cpu().numpy() if done.size else None
+        self._fill_host(obs, rew, term, trunc, info_arr, done, fin, epr, epl)
         infos = []
         for i in range(self.n):
             r = inf[i]
@@ -450,6 +530,9 @@ class HipRawNES:
 
     def instructions(self) -> int:
         return int(lib().mh_raw_instructions(self.h))
+
+    def ff_instructions(self) -> int:
+        return int(lib().mh_raw_ff_instructions(self.h))
 
     def __del__(self):
         h, self.h = getattr(self, "h", None), None

@@ -56,10 +56,13 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
                       const int* levels, const uint8_t* lut, int skip, int max_steps, double sticky, int noop_max,
                       int maxpool, int frame_stack, const uint64_t* rng, int device);
 
-/* Output buffers (device pointers, caller-owned). Replaces fm_set_buffers (fastmario.cpp:603-609).
+/* Output buffers (caller-owned). Replaces fm_set_buffers (fastmario.cpp:603-609).
  *   obs, fin  n * frame_stack * 84 * 84 u8 (stacked observations; final stack of finished episodes)
  *   rew       n f32;  term, trunc  n u8 (0/1);  info  n * 10 i32
- *   ep_ret    n f64;  ep_len  n i32 (written only for envs whose episode ended this step) */
+ *   ep_ret    n f64;  ep_len  n i32 (written only for envs whose episode ended this step)
+ * Each must be device memory of the env's GPU (or pinned / managed host memory) and aligned to its element
+ * size, obs and fin to 4 bytes (the frame stack is written in 32-bit words). Pageable host memory, memory
+ * of another GPU and misaligned buffers are refused (-1), where the reference's CPU path takes host arrays. */
 int mh_set_buffers(MhEnv* h, uint8_t* obs, uint8_t* fin, float* rew, uint8_t* term, uint8_t* trunc,
                    int32_t* info, double* ep_ret, int32_t* ep_len);
 
@@ -90,6 +93,13 @@ int mh_timing_read(MhEnv* h, double* ms, int64_t* steps);
 int64_t mh_frames(MhEnv* h);
 int64_t mh_bad_ops(MhEnv* h);
 int64_t mh_instructions(MhEnv* h);
+/* Of mh_instructions, those the exact sprite-0 poll-loop fast-forward retired without executing them (the
+ * reference executes each; its FM_PROF counter prof_cpu_instr, nes_core.hpp:1195, counts both kinds). */
+int64_t mh_ff_instructions(MhEnv* h);
+/* Early-termination re-emulations so far, by kind (synchronizing): out[0] an episode end at frame
+ * last < K-1 re-ran frame last alone, out[1] it re-ran the max-pool partner last-1 as well (the two
+ * branches of fastmario.cpp:351-362), out[2] of all of these, the ends at frame K-2 under max-pool. */
+int mh_reemulations(MhEnv* h, int64_t* out);
 
 /* RAM of every env into d_out (n * 2048 u8, device). Replaces fm_env_ram (fastmario.cpp:630). */
 int mh_env_ram(MhEnv* h, uint8_t* d_out, void* stream);
@@ -119,11 +129,14 @@ int     mh_raw_backup(MhRaw* h, void* stream);
 int     mh_raw_restore(MhRaw* h, void* stream);
 int64_t mh_raw_bad_ops(MhRaw* h);
 int64_t mh_raw_instructions(MhRaw* h);
+int64_t mh_raw_ff_instructions(MhRaw* h);   /* of those, poll-loop fast-forwards (see mh_ff_instructions) */
 void    mh_raw_destroy(MhRaw* h);
 
 /* ---- helpers */
-/* 240x256 gray images -> 84x84 INTER_AREA on the device (n images, device pointers).
- * Replaces fm_resize_fast (fastmario.cpp:641-649). */
+/* 240x256 gray images -> 84x84 INTER_AREA on the device (n images, device pointers, n <= 65535).
+ * Replaces fm_resize_fast (fastmario.cpp:641-649). The first call on a device allocates that device's
+ * filter tables (kept until the process ends). */
+#define MH_RESIZE_MAX_IMAGES 65535
 int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
 /* ---- frame-deduplicating replay ring (device storage owned by the caller)

@@ -807,6 +807,9 @@ struct Env {
     std::vector<uint8_t> g, g_prev;
     Info info{};
     int64_t frames = 0;
+    int reemu_kind = -1;             // branch of the last agent step's early termination (-1: none)
+    bool reemu_k2 = false;           // ... and it ended at frame K-2 under max-pool
+    int64_t reemu[3] = {0, 0, 0};    // env steps (not reset no-ops) by kind: re-ran last alone, with last-1, K-2 ends
 
     void restore() { con.m = lvl->boot; x_last = lvl->x0; time_last = lvl->time0; shows_boot = true; }
     void nes_frame(uint8_t buttons, bool render) {
@@ -862,7 +865,10 @@ struct Env {
             if (done) break;
         }
         int last = done ? i : K - 1;
+        reemu_kind = -1;
         if (want_obs && done && last < K - 1) {
+            reemu_kind = (mp && last >= 1) ? 1 : 0;
+            reemu_k2 = mp && last == K - 2;
             if (mp && last >= 1) {
                 con.m = snaps[last - 1];
                 nes_frame(kButtons[acts[last - 1]], true);
@@ -908,6 +914,7 @@ struct Env {
     void step(int a, uint8_t* out, float* rew, bool* term, bool* trunc) {   // fastmario.cpp:403-411
         bool tm;
         double r = agent_step(a, true, &tm);
+        if (reemu_kind >= 0) { reemu[reemu_kind]++; reemu[2] += reemu_k2; }
         t++;
         *trunc = t >= cfg->max_steps;
         ep_ret += r; ep_len++;
@@ -1072,6 +1079,10 @@ void or_step(void* h, const int64_t* actions) {
 int64_t or_frames(void* h) { int64_t f = 0; for (auto& e : ((Vec*)h)->envs) f += e.frames; return f; }
 int64_t or_bad_ops(void* h) { int64_t f = 0; for (auto& e : ((Vec*)h)->envs) f += e.con.bad_ops; return f; }
 int64_t or_instructions(void* h) { int64_t f = 0; for (auto& e : ((Vec*)h)->envs) f += e.con.instructions; return f; }
+void or_reemulations(void* h, int64_t* out) {
+    out[0] = out[1] = out[2] = 0;
+    for (auto& e : ((Vec*)h)->envs) for (int k = 0; k < 3; k++) out[k] += e.reemu[k];
+}
 void or_env_ram(void* h, int i, uint8_t* out) { memcpy(out, ((Vec*)h)->envs[i].con.m.ram, 0x800); }
 void or_env_canon(void* h, int i, uint8_t* out) { canon(((Vec*)h)->envs[i].con.m, out); }
 void or_env_gray(void* h, int i, uint8_t* out) { memcpy(out, ((Vec*)h)->envs[i].g.data(), kGray); }

@@ -57,6 +57,10 @@ void    or_step(void* h, const int64_t* actions);
 int64_t or_frames(void* h);
 int64_t or_bad_ops(void* h);
 int64_t or_instructions(void* h);
+/* Early-termination re-emulations of env steps (reset no-op steps excluded), by the branch of
+ * fastmario.cpp:351-362: out[0] frame last re-run alone, out[1] with its max-pool partner last-1,
+ * out[2] of both, the episode ends at frame K-2 under max-pool. */
+void    or_reemulations(void* h, int64_t* out);
 void    or_env_ram(void* h, int i, uint8_t* out);
 void    or_env_canon(void* h, int i, uint8_t* out);
 void    or_env_gray(void* h, int i, uint8_t* out);      /* 240*256 gray buffer of env i */

@@ -15,6 +15,8 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libfastmario_ref.so")
+# the same reference sources built with their own -DFM_PROF counters (nes_core.hpp:23-26)
+REF_PROF_SO = os.path.join(ROOT, "oracle", "_ref", "libfastmario_ref_prof.so")
 CANON_BYTES = 4464
 GRAY = 240 * 256
 OBS = 84 * 84
@@ -30,6 +32,10 @@ def _ptr(a: np.ndarray):
 
 def have_ref() -> bool:
     return os.path.isfile(REF_SO)
+
+
+def have_ref_prof() -> bool:
+    return os.path.isfile(REF_PROF_SO)
 
 
 def oracle() -> ctypes.CDLL:
@@ -53,6 +59,7 @@ def oracle() -> ctypes.CDLL:
         for f in ("or_env_ram", "or_env_canon", "or_env_gray", "or_level_canon", "or_level_obs"):
             getattr(L, f).argtypes = [_P, _i32, _P]
         L.or_palette.argtypes = [_P]
+        L.or_reemulations.argtypes = [_P, _P]
         L.or_pcg_run.argtypes = [_P, _P, _i32, _P, _P]
         L.or_resize.argtypes = [_P, _P]
         L.or_area_tab.restype = _i32
@@ -61,9 +68,10 @@ def oracle() -> ctypes.CDLL:
     return _libs["or"]
 
 
-def reference() -> ctypes.CDLL:
-    if "ref" not in _libs:
-        L = ctypes.CDLL(REF_SO)
+def reference(prof: bool = False) -> ctypes.CDLL:
+    key = "ref_prof" if prof else "ref"
+    if key not in _libs:
+        L = ctypes.CDLL(REF_PROF_SO if prof else REF_SO)
         L.fm_create.restype = _P
         L.fm_create.argtypes = [_P, _i64, _i32, _P, _P, _i32, _i32, _dbl, _i32, _i32, _i32, _P, _i32]
         L.fm_set_buffers.argtypes = [_P] * 9
@@ -84,8 +92,15 @@ def reference() -> ctypes.CDLL:
         L.fm_raw_backup.argtypes = L.fm_raw_restore.argtypes = L.fm_raw_destroy.argtypes = [_P]
         L.fm_raw_bad_ops.restype = _i64
         L.fm_raw_bad_ops.argtypes = [_P]
-        _libs["ref"] = L
-    return _libs["ref"]
+        _libs[key] = L
+    return _libs[key]
+
+
+def prof_counter(name: str = "prof_cpu_instr") -> ctypes.c_uint64:
+    """A uint64 FM_PROF counter of the profiling reference build (a C++ inline variable fm::<name>),
+    readable and writable in place."""
+    mangled = f"_ZN2fm{len(name)}{name}E"
+    return ctypes.c_uint64.in_dll(reference(prof=True), mangled)
 
 
 # ---------------------------------------------------------------- raw consoles
@@ -133,8 +148,8 @@ class OracleRaw(_RawBase):
 
 
 class RefRaw(_RawBase):
-    def __init__(self, rom):
-        L = self.L = reference()
+    def __init__(self, rom, prof=False):
+        L = self.L = reference(prof)
         self._create, self._ram, self._screen = L.fm_raw_create, L.fm_raw_ram, L.fm_raw_screen
         super().__init__(rom)
 
@@ -248,6 +263,11 @@ class OracleVec(_VecBase):
     def instructions(self):
         return int(self.L.or_instructions(self.h))
 
+    def reemulations(self):
+        out = np.zeros(3, np.int64)
+        self.L.or_reemulations(self.h, _ptr(out))
+        return dict(zip(("one", "pair", "k2"), out.tolist()))
+
     def close(self):
         if getattr(self, "h", None):
             self.L.or_destroy(self.h)
@@ -257,9 +277,9 @@ class OracleVec(_VecBase):
 
 
 class RefVec(_VecBase):
-    def __init__(self, rom, levels, n, n_threads=0, **kw):
+    def __init__(self, rom, levels, n, n_threads=0, prof=False, **kw):
         super().__init__(rom, levels, n, **kw)
-        L = self.L = reference()
+        L = self.L = reference(prof)
         self.h = L.fm_create(_ptr(self._rom), len(self._rom), n, _ptr(self._lv), _ptr(self._lut), *self.args,
                              _ptr(self._rng), int(n_threads))
         if not self.h:

@@ -1,0 +1,160 @@
+"""The FastVecEnv surface on the GPU (the reference's tests/test_api.py:54-98, ported): shapes and dtypes, the
+zero-padded reset stack, list-of-dict infos with episode / final_obs / TimeLimit.truncated at the time
+limit, env_offset equivalence, determinism, the monitor CSV rows, and set_buffers in both of its forms.
+The CPU oracle is the checker for every value."""
+import csv
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from build_roms import rom_path
+from cpu_libs import OracleVec
+
+pytestmark = pytest.mark.gpu
+
+MINI = open(rom_path("vanilla"), "rb").read()
+
+
+def _levels(names):
+    from fast_mario_env_amd import decode_level
+    return [decode_level(x) for x in names]
+
+
+def test_shapes_infos_and_time_limit(tmp_path):
+    """test_api.py:54-71: (3, 4, 84, 84) uint8 obs, zero-padded reset stack, float32 / bool outputs, the info
+    keys, and at max_steps=20 every env truncated with episode l == 20, final_obs (4, 84, 84) and
+    TimeLimit.truncated; here also every value against the oracle and the monitor CSV rows."""
+    import fast_mario_env_amd as fme
+    mon = tmp_path / "run"
+    v = fme.FastVecEnv("1-1", 3, seed=0, max_steps=20, n_threads=2, rom=MINI, monitor_path=str(mon))
+    ref = OracleVec(MINI, _levels(["1-1"] * 3), 3, seed=0, max_steps=20)
+    obs = v.reset()
+    assert obs.shape == (3, 4, 84, 84) and obs.dtype == np.uint8
+    assert (obs[:, :3] == 0).all() and obs[:, 3].any()
+    assert np.array_equal(obs, ref.reset())
+    ended, episodes = 0, []
+    for t in range(25):
+        obs, r, te, tr, infos = v.step(np.full(3, 1))
+        o1, r1, te1, tr1, i1 = ref.step(np.full(3, 1))
+        assert r.dtype == np.float32 and te.dtype == bool and tr.dtype == bool and len(infos) == 3
+        assert np.array_equal(obs, o1) and np.array_equal(r, r1) and np.array_equal(te, te1) and np.array_equal(tr, tr1)
+        for i in range(3):
+            assert set(fme.INFO_KEYS) <= set(infos[i])
+            assert [infos[i][k] for k in fme.INFO_KEYS] == [int(x) for x in i1[i, :7]], (t, i)
+            assert isinstance(infos[i]["flag_get"], bool)
+        for i in np.flatnonzero(te | tr):
+            ended += 1
+            ep = infos[i]["episode"]
+            assert infos[i]["final_obs"].shape == (4, 84, 84)
+            assert np.array_equal(infos[i]["final_obs"], ref.fin[i])
+            assert ep["l"] == 20 and infos[i]["TimeLimit.truncated"]
+            assert ep["r"] == round(float(ref.ep_ret[i]), 6)
+            assert ep["x_pos"] == infos[i]["x_pos"] and ep["flag_get"] == infos[i]["flag_get"]
+            episodes.append(ep)
+        for i in np.flatnonzero(~(te | tr)):
+            assert "episode" not in infos[i] and "final_obs" not in infos[i]
+    assert ended == 3
+    assert v.bad_ops() == 0 and v.frames == ref.frames() > 0
+    v.close()
+    path = fme.MonitorCSV.resolve(str(mon))
+    lines = open(path).read().splitlines()
+    assert lines[0].startswith("#{") and '"t_start"' in lines[0]
+    rows = list(csv.DictReader(lines[1:]))
+    assert len(rows) == len(episodes) == 3
+    for row, ep in zip(rows, episodes):
+        assert float(row["r"]) == ep["r"] and int(row["l"]) == ep["l"] and int(row["x_pos"]) == ep["x_pos"]
+        assert row["flag_get"] == str(ep["flag_get"]) and float(row["t"]) >= 0
+
+
+def test_env_offset_matches_single_env():
+    """test_api.py:89-98: envs 2..3 of a 4-env instance equal a 2-env instance with env_offset=2."""
+    import fast_mario_env_amd as fme
+    acts = np.random.default_rng(1).integers(0, 7, (40, 4))
+    a = fme.FastVecEnv("1-1", 4, seed=2, sticky=0.25, noop_max=10, rom=MINI)
+    b = fme.FastVecEnv("1-1", 2, seed=2, sticky=0.25, noop_max=10, env_offset=2, rom=MINI)
+    oa, ob = a.reset(), b.reset()
+    assert np.array_equal(oa[2:], ob)
+    for x in acts:
+        ra, rb = a.step(x), b.step(x[2:])
+        assert np.array_equal(ra[0][2:], rb[0]) and np.array_equal(ra[1][2:], rb[1])
+    a.close(); b.close()
+
+
+def test_determinism():
+    """test_api.py:74-86: the same seed gives the same trajectory (n_threads sizes the reference's pool and
+    changes nothing here either)."""
+    import fast_mario_env_amd as fme
+    acts = np.random.default_rng(0).integers(0, 7, (60, 4))
+    outs = []
+    for threads in (0, 3):
+        v = fme.FastVecEnv(["1-1", "1-2", "4-1", "8-4"], 4, seed=5, sticky=0.25, noop_max=10, n_threads=threads,
+                           rom=MINI)
+        o = [v.reset()]
+        for x in acts:
+            o.append(v.step(x)[0])
+        outs.append(np.stack(o))
+        v.close()
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_set_buffers_numpy_like_the_reference():
+    """set_buffers with numpy arrays and the reference's int64 info / ep_len: reset and step write into them."""
+    import fast_mario_env_amd as fme
+    n, kw = 4, dict(seed=3, sticky=0.25, noop_max=5, max_steps=12)
+    v = fme.FastVecEnv(["1-1", "4-1", "1-2", "8-4"], n, rom=MINI, **kw)
+    ref = OracleVec(MINI, _levels(["1-1", "4-1", "1-2", "8-4"]), n, **kw)
+    bufs = (np.zeros((n, 4, 84, 84), np.uint8), np.zeros((n, 4, 84, 84), np.uint8), np.zeros(n, np.float32),
+            np.zeros(n, np.uint8), np.zeros(n, np.uint8), np.zeros((n, 10), np.int64), np.zeros(n, np.float64),
+            np.zeros(n, np.int64))
+    v.set_buffers(*bufs)
+    v.reset()
+    assert np.array_equal(bufs[0], ref.reset())
+    rng = np.random.default_rng(2)
+    ends = 0
+    for _ in range(30):
+        a = rng.integers(0, 7, n)
+        v.step(a)
+        ref.step(a)
+        for mine, theirs in zip(bufs, (ref.obs, ref.fin, ref.rew, ref.term, ref.trunc, ref.info, ref.ep_ret, ref.ep_len)):
+            assert np.array_equal(mine, theirs)
+        ends += int((ref.term | ref.trunc).sum())
+    assert ends > 0
+    with pytest.raises(ValueError, match="info"):
+        v.set_buffers(*bufs[:5], np.zeros((n, 10), np.float32), *bufs[6:])
+    v.close()
+
+
+def test_set_buffers_device_and_refusals():
+    """Device buffers are written in place by the kernels; pageable host memory and misaligned buffers are
+    refused with a message instead of being written by the GPU."""
+    import fast_mario_env_amd as fme
+    n = 2
+    v = fme.FastVecEnv("1-1", n, seed=1, rom=MINI)
+    z = lambda *s, dt: torch.zeros(*s, dtype=dt, device="cuda")  # noqa: E731
+    dev = [z(n, 4, 84, 84, dt=torch.uint8), z(n, 4, 84, 84, dt=torch.uint8), z(n, dt=torch.float32),
+           z(n, dt=torch.uint8), z(n, dt=torch.uint8), z(n, 10, dt=torch.int32), z(n, dt=torch.float64),
+           z(n, dt=torch.int32)]
+    v.set_buffers(*dev)
+    v.reset()
+    torch.cuda.synchronize()
+    assert dev[0][:, 3].any() and not dev[0][:, :3].any()
+    v.step(np.array([1, 2]))
+    torch.cuda.synchronize()
+    ref = OracleVec(MINI, _levels(["1-1"] * n), n, seed=1)
+    ref.reset()
+    ref.step(np.array([1, 2]))
+    assert np.array_equal(dev[0].cpu().numpy(), ref.obs) and np.array_equal(dev[5].cpu().numpy(), ref.info)
+    host = np.zeros((n, 4, 84, 84), np.uint8)                       # pageable host memory as a raw address
+    addrs = [host.ctypes.data] + [int(t.data_ptr()) for t in dev[1:]]
+    with pytest.raises(RuntimeError, match="pageable"):
+        v.set_buffers(*addrs)
+    addrs = [int(dev[0].data_ptr()) + 1] + [int(t.data_ptr()) for t in dev[1:]]
+    with pytest.raises(RuntimeError, match="aligned"):
+        v.set_buffers(*addrs)
+    # the refusals left no stale error behind: the env still steps
+    v.set_buffers(*dev)
+    v.step(np.array([0, 0]))
+    torch.cuda.synchronize()
+    v.close()

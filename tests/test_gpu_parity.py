@@ -96,6 +96,14 @@ CONFIGS = {
     "skip6_maxpool": dict(skip=6, maxpool=True, noop_max=4, sticky=0.5),
 }
 ACTION_P = [.05, .2, .25, .15, .25, .05, .05]
+# Early-termination re-emulation kinds each configuration must exercise in _env_run (counted on the GPU and
+# by the oracle, which must agree): "one" re-runs the last frame alone, "pair" its max-pool partner too, "k2"
+# ends at frame K-2 under max-pool. K = 1 has no early termination; K = 2 has no pair.
+EXPECT_REEMU = {
+    "default": ("one",), "sticky_noop": ("one",), "maxpool_sticky": ("one", "pair", "k2"),
+    "short_timelimit": ("one",), "headline": ("one", "pair"), "skip1_stack2": (),
+    "skip2_maxpool": ("one", "k2"), "skip3_short": ("one",), "skip6_maxpool": ("one", "pair", "k2"),
+}
 
 
 def _levels(names):
@@ -186,5 +194,41 @@ def _env_run(names, config, steps):
     assert gpu.frames == cpu.frames()
     assert gpu.bad_ops() == 0 and cpu.bad_ops() == 0
     assert gpu.instructions() == cpu.instructions()
+    assert 0 <= gpu.ff_instructions() < gpu.instructions()
+    re_gpu, re_cpu = gpu.reemulations(), cpu.reemulations()
+    assert re_gpu == re_cpu, (re_gpu, re_cpu)
+    if steps >= 150:
+        for kind in EXPECT_REEMU.get(config, ()):
+            assert re_cpu[kind] > 0, (config, kind, re_cpu)
+        if CONFIGS[config].get("skip") == 1:
+            assert sum(re_cpu.values()) == 0
     if config == "short_timelimit":
         assert eps > 0
+
+
+def test_config1_golden_trace_on_gpu():
+    """The CPU golden-trace workload (32 envs of 1-1, seed 0, no sticky / no-op / max-pool, actions from
+    default_rng(0)) through the HIP path, against the digests the reference C++ wrote for all 1,000 steps
+    (obs, reward, terminated, truncated, int64 info and every env's RAM) and the full arrays kept at steps
+    0, 1, 10, 100 and 999."""
+    import json
+
+    import torch
+
+    import make_golden as G
+    from fast_mario_env_amd import HipVecEnv
+    g = json.load(open(G.GOLDEN))["config1"]
+    keep = np.load(G.CONFIG1)
+    n = 32
+    env = HipVecEnv("1-1", n, seed=0, rom=MINI)
+    assert G.digest(env.reset().cpu().numpy()) == g["trace"][0]
+    for t, a in enumerate(G.config1_actions()):
+        obs, rew, term, trunc, _ = env.step(torch.from_numpy(np.asarray(a, np.int64)).cuda())
+        obs, rew, term, trunc = (x.cpu().numpy() for x in (obs, rew, term, trunc))
+        info = env.info_t.cpu().numpy().astype(np.int64)
+        ram = env.ram().cpu().numpy()
+        assert G.digest(obs, rew, term, trunc, info, ram) == g["trace"][t + 1], t
+        if t in G.CONFIG1_KEEP:
+            assert np.array_equal(obs, keep[f"obs_{t}"]) and np.array_equal(ram, keep[f"ram_{t}"]), t
+            assert np.array_equal(info, keep[f"info_{t}"]) and np.array_equal(rew, keep[f"rew_{t}"]), t
+    assert env.frames == g["frames"] and env.bad_ops() == g["bad_ops"] == 0

@@ -1,0 +1,188 @@
+"""GPU parity at the benchmark workloads' real sizes.
+
+The small parity tests fit in one workgroup (128 env slots). These run many: 4,096 envs (32 workgroups) with
+the headline wrappers, 4,096 raw consoles, and the 65,536-env divergence-stress instance (512 workgroups; its
+second frame buffer starts 4.03e9 bytes in and ends past 2^33). Every env's outputs are recorded on the
+device; a sample of envs (a fixed stride, the last env, and envs whose episodes ended, which take the reset,
+final_obs and re-emulation paths) is then replayed by one-env CPU oracles on the sampled env's own PCG64
+stream (env_offset = its index, as the reference's env_offset equivalence allows, env.py:155-156), bit for
+bit. Every env is also checked against size-independent properties: the frame-stack shift and reset stack of
+k_stack, final_obs, and zero bad ops.
+"""
+import numpy as np
+import pytest
+import torch
+
+from build_roms import MODES, rom_path
+from cpu_libs import OracleRaw, OracleVec
+
+pytestmark = pytest.mark.gpu
+
+ROMS = {m: open(rom_path(m), "rb").read() for m in MODES}
+HEADLINE = dict(sticky=0.25, noop_max=30, skip=4, maxpool=True, frame_stack=4, max_steps=2000)
+STRESS = dict(sticky=0.25, noop_max=30, skip=4, maxpool=False, frame_stack=4, max_steps=2000)
+
+
+def _levels(names):
+    from fast_mario_env_amd import decode_level
+    return [decode_level(x) for x in names]
+
+
+def _first_diff(a, b):
+    d = np.flatnonzero(np.asarray(a).reshape(-1) != np.asarray(b).reshape(-1))
+    return d[:8].tolist()
+
+
+def _record(env, actions):
+    """Reset, then step every row of `actions` (T, N) on the device; every output kept on the device."""
+    rec = {"obs0": env.reset().clone(), "canon0": env.canon()}
+    keys = ("obs", "rew", "term", "trunc", "info", "ram", "fin", "ep_ret", "ep_len")
+    for k in keys:
+        rec[k] = []
+    for a in actions:
+        obs, rew, term, trunc, _ = env.step(a)
+        done = term | trunc
+        rec["obs"].append(obs.clone())
+        rec["rew"].append(rew.clone())
+        rec["term"].append(term.clone())
+        rec["trunc"].append(trunc.clone())
+        rec["info"].append(env.info_t.clone())
+        rec["ram"].append(env.ram())
+        # final_obs / episode stats are valid only where the episode ended: keep those rows as a dense copy
+        rec["fin"].append(torch.where(done[:, None, None, None], env.final_obs, 0))
+        rec["ep_ret"].append(torch.where(done, env.ep_ret, 0))
+        rec["ep_len"].append(torch.where(done, env.ep_len, 0))
+    torch.cuda.synchronize()
+    return rec
+
+
+def _check_stack_invariants(rec):
+    """k_stack on every env: the stack shifts by one frame, a finished episode's final_obs is the shifted stack
+    plus the last frame, and its new stack is [0, ..., 0, reset frame]."""
+    prev = rec["obs0"]
+    for t, obs in enumerate(rec["obs"]):
+        done = rec["term"][t] | rec["trunc"][t]
+        live = ~done
+        assert torch.equal(obs[live][:, :-1], prev[live][:, 1:]), (t, "stack shift")
+        if done.any():
+            fin = rec["fin"][t][done]
+            assert torch.equal(fin[:, :-1], prev[done][:, 1:]), (t, "final_obs shift")
+            assert not obs[done][:, :-1].any(), (t, "reset stack")
+        prev = obs
+
+
+def _sample(n, stride, rec, extra):
+    done_any = torch.stack([a | b for a, b in zip(rec["term"], rec["trunc"])]).any(0).cpu().numpy()
+    picks = set(range(0, n, stride)) | {n - 1}
+    done_idx = np.flatnonzero(done_any)
+    picks |= set(done_idx[np.linspace(0, len(done_idx) - 1, min(extra, len(done_idx))).astype(int)].tolist()) \
+        if len(done_idx) else set()
+    return sorted(picks), int(done_any.sum())
+
+
+def _replay_samples(rec, samples, names, modes, kw, seed, actions):
+    acts = actions.cpu().numpy()
+    host = {k: [x[samples].cpu().numpy() for x in rec[k]] for k in
+            ("obs", "rew", "term", "trunc", "info", "ram", "fin", "ep_ret", "ep_len")}
+    obs0 = rec["obs0"][samples].cpu().numpy()
+    canon0 = rec["canon0"][samples].cpu().numpy()
+    eps = 0
+    for j, i in enumerate(samples):
+        cpu = OracleVec(ROMS[modes[i]], _levels([names[i]]), 1, seed=seed, env_offset=i, **kw)
+        assert np.array_equal(cpu.reset()[0], obs0[j]), (i, "reset obs")
+        assert np.array_equal(cpu.canon(0), canon0[j]), (i, "reset state", _first_diff(cpu.canon(0), canon0[j]))
+        for t in range(len(acts)):
+            o, r, te, tr, inf = cpu.step(acts[t, i:i + 1])
+            assert r[0] == host["rew"][t][j] and te[0] == host["term"][t][j] and tr[0] == host["trunc"][t][j], \
+                (t, i, "reward/done", r[0], host["rew"][t][j])
+            assert np.array_equal(inf[0], host["info"][t][j]), (t, i, "info", inf[0], host["info"][t][j])
+            assert np.array_equal(cpu.ram(0), host["ram"][t][j]), (t, i, "ram", _first_diff(cpu.ram(0), host["ram"][t][j]))
+            assert np.array_equal(o[0], host["obs"][t][j]), (t, i, "obs", _first_diff(o[0], host["obs"][t][j]))
+            if te[0] or tr[0]:
+                eps += 1
+                assert np.array_equal(cpu.fin[0], host["fin"][t][j]), (t, i, "final_obs")
+                assert cpu.ep_ret[0] == host["ep_ret"][t][j] and cpu.ep_len[0] == host["ep_len"][t][j], (t, i, "episode")
+        assert cpu.bad_ops() == 0
+        cpu.close()
+    return eps
+
+
+def _run(names, modes, kw, seed, actions, stride, extra):
+    from fast_mario_env_amd import HipVecEnv
+    n = len(names)
+    rom = {m: ROMS[m] for m in set(modes)}
+    env = HipVecEnv(names, n, seed=seed, rom=rom, rom_mode=modes, device="cuda:0", **kw)
+    print(f"scale run: {n} envs, {len(actions)} steps", flush=True)
+    rec = _record(env, actions)
+    _check_stack_invariants(rec)
+    assert env.bad_ops() == 0
+    samples, n_done = _sample(n, stride, rec, extra)
+    print(f"  {n_done} envs ended an episode; replaying {len(samples)} sampled envs on the CPU", flush=True)
+    eps = _replay_samples(rec, samples, names, modes, kw, seed, actions)
+    re = env.reemulations()
+    env.close()
+    return n_done, eps, re
+
+
+def test_headline_4096_envs_mixed_levels():
+    """Headline wrappers (sticky 0.25, no-op 30, skip 4, max-pool) at 4,096 envs: 32 workgroups, levels mixed."""
+    from fast_mario_env_amd import ALL_LEVELS
+    n, T = 4096, 50
+    lv = np.random.default_rng(11).integers(0, 32, n)
+    names = [ALL_LEVELS[k] for k in lv]
+    g = torch.Generator(device="cuda:0").manual_seed(5)
+    actions = torch.randint(0, 7, (T, n), generator=g, device="cuda:0")
+    n_done, eps, re = _run(names, ["vanilla"] * n, HEADLINE, 0, actions, stride=61, extra=24)
+    assert n_done > 0 and eps > 0
+    assert re["one"] > 0 and re["pair"] > 0 and re["k2"] > 0, re
+
+
+def test_divergence_stress_65536_envs():
+    """The divergence-stress instance at its full size: 65,536 envs, levels drawn from default_rng(7) over the 32
+    world-stage pairs, rom_mode cycled over the four variants per env, sticky 0.25, no-op 30, skip 4, no
+    max-pool; per env, action 2 (right + A) with p = 0.5, else uniform over 0..6."""
+    from fast_mario_env_amd import ALL_LEVELS
+    n, T = 65536, 8
+    lv = np.random.default_rng(7).integers(0, 32, n)
+    names = [ALL_LEVELS[k] for k in lv]
+    modes = [MODES[i % 4] for i in range(n)]
+    rng = np.random.default_rng(3)
+    acts = np.where(rng.random((T, n)) < 0.5, 2, rng.integers(0, 7, (T, n)))
+    actions = torch.from_numpy(acts).to("cuda:0")
+    n_done, eps, re = _run(names, modes, STRESS, 0, actions, stride=1021, extra=24)
+    assert n_done > 0 and eps > 0
+    assert re["one"] > 0, re
+
+
+def test_raw_4096_consoles():
+    """Raw consoles at 4,096 (the raw-emulator workload's size): a Start/none prologue that enters 1-1, then
+    SIMPLE_MOVEMENT buttons drawn per console and frame from default_rng(1), every frame rendered. Sampled
+    consoles against one CPU console each: RAM, palette screen, RGB24 screen and the whole machine state."""
+    from fast_mario_env_amd import HipRawNES, palette_rgb
+    n, prologue, frames = 4096, 40, 40
+    buttons_tab = np.array([0x00, 0x80, 0x81, 0x82, 0x83, 0x01, 0x40], np.uint8)
+    rng = np.random.default_rng(1)
+    sched = [np.full(n, 8 if f % 2 == 0 else 0, np.uint8) for f in range(prologue)]
+    sched += [buttons_tab[rng.integers(0, 7, n)] for _ in range(frames)]
+    gpu = HipRawNES(ROMS["vanilla"], n)
+    samples = sorted(set(range(0, n, 61)) | {n - 1})
+    cpu = {i: OracleRaw(ROMS["vanilla"]) for i in samples}
+    pal = palette_rgb()
+    idx = torch.tensor(samples, device="cuda:0")
+    for f, b in enumerate(sched):
+        gpu.frame(torch.from_numpy(b), True)
+        for i, c in cpu.items():
+            c.frame(int(b[i]), True)
+        ram = gpu.ram[idx].cpu().numpy()
+        scr = gpu.screen[idx].cpu().numpy()
+        canon = gpu.canon()[idx].cpu().numpy()
+        rgb = gpu.screen_rgb[idx].cpu().numpy() if f % 10 == 9 else None
+        for j, i in enumerate(samples):
+            c = cpu[i]
+            assert np.array_equal(ram[j], c.ram), (f, i, "ram", _first_diff(ram[j], c.ram))
+            assert np.array_equal(scr[j], c.screen), (f, i, "screen", _first_diff(scr[j], c.screen))
+            assert np.array_equal(canon[j], c.canon()), (f, i, "state", _first_diff(canon[j], c.canon()))
+            if rgb is not None:
+                assert np.array_equal(rgb[j], pal[c.screen & 63]), (f, i, "rgb screen")
+    assert gpu.bad_ops() == 0
+    assert sum(c.instructions() for c in cpu.values()) > 0

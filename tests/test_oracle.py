@@ -20,11 +20,12 @@ import alu_rom
 import fuzz
 import make_golden as G
 from build_roms import MODES, build, rom_path
-from cpu_libs import OracleRaw, OracleVec, RefRaw, RefVec, gray_lut, have_ref, oracle
+from cpu_libs import OracleRaw, OracleVec, RefRaw, RefVec, gray_lut, have_ref, have_ref_prof, oracle, prof_counter
 
 GOLD = json.load(open(G.GOLDEN))
 MINI = open(rom_path("vanilla"), "rb").read()
 requires_ref = pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built (no reference tree)")
+requires_ref_prof = pytest.mark.skipif(not have_ref_prof(), reason="oracle/_ref prof build absent (no reference tree)")
 
 
 def _levels(names):
@@ -127,6 +128,40 @@ def test_env_offset_and_threads_vs_reference():
     for x in acts:
         assert np.array_equal(full.step(x)[0][2:], part.step(x[2:])[0])
         assert np.array_equal(full.obs, thr.step(x)[0])
+
+
+# ---------------------------------------------------------------- the instruction counter
+@requires_ref_prof
+@pytest.mark.parametrize("case", ["mini_smb", "program_1", "program_4", "random_2"])
+def test_raw_instruction_count_vs_reference_prof(case):
+    """The oracle's retired-instruction count equals the reference's own FM_PROF counter prof_cpu_instr
+    (nes_core.hpp:1195), which counts every executed instruction and no idle-skipped JMP * iteration."""
+    rom = G.raw_rom(case)
+    sched = G.raw_schedule(7, scaled(120))
+    ref = RefRaw(rom, prof=True)
+    ctr = prof_counter()
+    ctr.value = 0
+    con = OracleRaw(rom)
+    G.run_raw(ref, sched)
+    G.run_raw(con, sched)
+    assert con.instructions() == ctr.value > 0
+
+
+@requires_ref_prof
+@pytest.mark.parametrize("kw", [dict(sticky=0.25, noop_max=30, maxpool=True), dict(skip=3, max_steps=40)])
+def test_env_instruction_count_vs_reference_prof(kw):
+    """Same for the env path from reset on (no-op starts, hack frames and early-termination re-emulations
+    included), with the reference stepping inline (n_threads=0) so the global counter is not raced."""
+    names = ["1-1", "4-1", "8-4", "1-2"]
+    ctr = prof_counter()
+    ref = RefVec(MINI, _levels(names), 4, n_threads=0, prof=True, seed=3, **kw)
+    ctr.value = 0                              # level boot happened in the constructor: not counted
+    con = OracleVec(MINI, _levels(names), 4, seed=3, **kw)
+    ref.reset(); con.reset()
+    for a in G.env_actions(4, scaled(80), seed=4):
+        ref.step(a); con.step(a)
+    assert con.instructions() == ctr.value > 0
+    assert con.frames() == ref.frames()
 
 
 # ---------------------------------------------------------------- numpy PCG64
