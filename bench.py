@@ -1,19 +1,28 @@
 #!/usr/bin/env python
-"""Headline benchmark: batched Super Mario Bros agent steps on one MI355X (the full wrapper stack at 32768 envs).
+"""Benchmarks of batched Super Mario Bros stepping on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--envs N] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--workload headline|stress|raw|ppo|replay] [--gpus 1]
 
-Workload: N = 32768 envs on level 1-1, sticky 0.25, no-op starts up to 30, skip 4, 2-frame max-pool,
-gray + INTER_AREA 84x84, frame stack 4, time limit 2000, auto-reset, seed 0 (env i: PCG64 stream i);
-actions uniform in {0..6}, pre-generated on the device from torch.Generator seed 0. The ROM is the
-real one when the reference's lookup finds it, else this repository's synthetic NROM stand-in
-(tests/golden/roms/mini_smb_vanilla.nes); the JSON line names which.
+headline (default; the metric's configuration): 32,768 envs of 1-1, sticky 0.25, no-op starts up to 30,
+    skip 4, 2-frame max-pool, gray + INTER_AREA 84x84, frame stack 4, time limit 2000, auto-reset, seed 0
+    (env i: PCG64 stream i); actions uniform in {0..6} from torch.Generator seed 0 on the device.
+stress: the divergence-stress configuration: 65,536 envs, level of env i drawn from default_rng(7) over the
+    32 world-stage pairs, rom_mode cycled over the four variants per env, sticky 0.25, no-op 30, skip 4, no
+    max-pool; per env and step, action 2 (right + A) with p = 0.5, else uniform (torch.Generator seed 0).
+raw: the raw-emulator configuration: 4,096 consoles, skip 1, no wrappers, every frame rendered and delivered
+    as an RGB24 screen plus the 2 KB RAM; a Start/none prologue enters 1-1, then SIMPLE_MOVEMENT buttons
+    drawn per console and frame from default_rng(1); K timed frames.
+ppo / replay: the PPO rollout feeding a Nature CNN, and the GPU FrameReplay.
 
-One step = mh_step_async (k_step, k_obs, k_reset, k_stack) on torch's current stream;
-inputs are resident in HBM. K steps are timed between two device synchronizations after W warm-up
-steps. Stage times come from HIP events recorded on the same stream. The reference C++ FastVecEnv
-(oracle/_ref, the checker build of the reference) is timed on the host cores on a bounded sample of
-the same workload and reported beside the GPU number.
+The ROM is the real one when the reference's lookup finds it, else this repository's synthetic NROM stand-in
+(tests/golden/roms/mini_smb_*.nes); the JSON line names which. One step is one mh_step_async (k_step, k_obs,
+k_reset, k_stack) or, for raw, one frame and its outputs, on torch's current stream with inputs resident in
+HBM. Before the W warm-up steps, --preroll untimed steps carry the envs past their first episodes so that the
+timed window has episode ends, resets and early-termination re-emulations in it (the first steps after a
+reset are the cheapest ones). K steps are timed between two device synchronizations; per-kernel times come
+from HIP events recorded on the launch stream. The reference C++ (oracle/_ref, the checker build of the
+reference) is timed on the host cores on a bounded sample of the same workload and reported beside the GPU
+number.
 """
 from __future__ import annotations
 
@@ -39,21 +48,22 @@ ENV_WORD_BYTES = 4 * 30
 K_STEP_BYTES = 2 * STATE_BYTES + 2 * ENV_WORD_BYTES + 8 + 4 + 1 + 1 + 40
 K_STEP_DONE_BYTES = 12
 OBS = 84 * 84
+SIMPLE_BUTTONS = (0x00, 0x80, 0x81, 0x82, 0x83, 0x01, 0x40)
 
 
 def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def pick_rom():
+def pick_rom(mode="vanilla"):
+    """(bytes, description) of the ROM for a rom_mode: the real one if found, else the synthetic stand-in."""
     from fast_mario_env_amd import RomNotFoundError, load_rom
     try:
-        data = load_rom()
-        return data, "super-mario-bros.nes (real ROM)"
+        return load_rom(rom_mode=mode), f"{mode}: real ROM"
     except (RomNotFoundError, ValueError):
         from build_roms import rom_path
-        path = rom_path("vanilla")
-        return open(path, "rb").read(), "mini_smb_vanilla.nes (synthetic NROM stand-in; no SMB ROM on this machine)"
+        path = rom_path(mode)
+        return open(path, "rb").read(), f"{mode}: {os.path.basename(path)} (synthetic NROM stand-in; no SMB ROM here)"
 
 
 def profile_values(name, workload_key):
@@ -78,41 +88,38 @@ def traffic_from_profiles(workload_key):
         return None
 
 
-def valu_issue_from_profiles(workload_key):
-    """k_step's VALU issue fraction from the committed rocprofv3 SQ-counter summary, if one exists."""
+def valu_roofline(workload_key):
+    """k_step's VALU-issue roofline from the committed rocprofv3 SQ-counter summary of this workload: the
+    binding one for an interpreter (HBM is ~0.01 of peak). Counters cannot be read inside this run; the
+    summary names the command, the steady-state window it measured and the kernel build it measured."""
+    v = profile_values("k_step_sq_counters_headline.md", workload_key)
     try:
-        return float(profile_values("k_step_sq_counters_headline.md", workload_key)["valu_issue_fraction"])
+        frac = float(v["valu_issue_fraction"])
     except (KeyError, ValueError):
         return None
+    out = {"bound": "valu_issue", "kernel": "k_step", "frac": frac,
+           "unit": "VALU wave-instructions x 4 cycles / (1024 SIMDs x cycles)",
+           "source": "profiles/k_step_sq_counters_headline.md"}
+    for k in ("window", "active_lane_fraction", "occupancy_waves_per_simd", "lds_bank_conflict_per_lds_instr",
+              "kernel_source_sha1"):
+        if k in v:
+            out[k] = v[k]
+    return out
 
 
-def cpu_baseline(rom, seconds):
-    """The reference C++ thread pool (oracle/_ref) on the host cores, headline settings, bounded sample."""
-    import numpy as np
+def kernel_source_sha1():
+    """sha1 of the HIP sources the library is built from (names the kernel build a profile measured)."""
+    h = hashlib.sha1()
+    d = os.path.join(ROOT, "fast-mario-env_amd", "csrc")
+    for f in sorted(os.listdir(d)):
+        if f.endswith((".hip", ".hpp")):
+            h.update(open(os.path.join(d, f), "rb").read())
+    return h.hexdigest()[:12]
 
-    from cpu_libs import OracleVec, RefVec, have_ref
-    from fast_mario_env_amd import decode_level
-    cores = os.cpu_count() or 1
-    n = max(256, 32 * cores)
-    kw = dict(seed=0, sticky=0.25, noop_max=30, skip=4, maxpool=True, frame_stack=4, max_steps=2000)
-    lv = [decode_level("1-1")] * n
-    if have_ref():
-        env, kind, threads = RefVec(rom, lv, n, n_threads=cores, **kw), "reference", cores
-    else:
-        n = 64
-        env, kind, threads = OracleVec(rom, [decode_level("1-1")] * n, n, **kw), "port", 1
-    env.reset()
-    rng = np.random.default_rng(0)
-    for _ in range(3):
-        env.step(rng.integers(0, 7, n))
-    steps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        env.step(rng.integers(0, 7, n))
-        steps += 1
-    dt = time.perf_counter() - t0
-    env.close()
+
+def host_info():
     try:
-        load1 = os.getloadavg()[0]
+        load1 = round(os.getloadavg()[0], 2)
     except OSError:
         load1 = None
     model = ""
@@ -120,19 +127,124 @@ def cpu_baseline(rom, seconds):
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except (OSError, StopIteration):
         pass
+    return model, load1
+
+
+def host_threads():
+    """Worker threads for the CPU baselines: the host's cores, capped by OMP_NUM_THREADS where it is set (the
+    GPU boxes set it to their CPU share, whatever os.cpu_count() shows)."""
+    cores = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(cores, int(cap))) if cap.isdigit() else cores
+
+
+def mem_available_gb():
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) / 2**20
+    except OSError:
+        pass
+    return 0.0
+
+
+def _timed_cpu_steps(envs_actions, seconds, min_steps=1):
+    """Steps every (env, action-fn) pair once per step until `seconds` passed (at least min_steps)."""
+    steps, t0 = 0, time.perf_counter()
+    while steps < min_steps or time.perf_counter() - t0 < seconds:
+        for env, act in envs_actions:
+            env.step(act(env.n))
+        steps += 1
+    return steps, time.perf_counter() - t0
+
+
+def cpu_baseline_env(rom_by_mode, kw, levels, modes, seconds, n_req, action_fn, what):
+    """The reference C++ thread pool (oracle/_ref) on the host cores: one FastVecEnv per rom_mode (the reference
+    takes one rom_mode per instance), envs split by their mode, stepped one after the other each step."""
+    import numpy as np
+
+    from cpu_libs import OracleVec, RefVec, have_ref
+    from fast_mario_env_amd import decode_level
+    cores = host_threads()
+    n, why = n_req, ""
+    need_gb = 0.4 * n / 1024                   # ~0.36 MB per env (state, snapshots, frames, stacks)
+    if mem_available_gb() < need_gb + 4:
+        n = max(1024, 8 * cores)
+        why = f"; {n_req} envs would need ~{need_gb:.0f} GB of host RAM, {mem_available_gb():.0f} GB available"
+    by_mode = {}
+    for i in range(n):
+        by_mode.setdefault(modes[i], []).append(i)
+    t_build = time.perf_counter()
+    if have_ref():
+        kind, threads = "reference", cores
+        envs = [RefVec(rom_by_mode[m], [decode_level(levels[i]) for i in idx], len(idx), n_threads=cores, **kw)
+                for m, idx in by_mode.items()]
+    else:
+        kind, threads, n = "port", 1, 64
+        envs = [OracleVec(rom_by_mode[modes[0]], [decode_level(levels[0])] * n, n, **kw)]
+    for e in envs:
+        e.reset()
+    build_s = time.perf_counter() - t_build
+    pairs = [(e, action_fn) for e in envs]
+    _timed_cpu_steps(pairs, 0.0, min_steps=3)
+    steps, dt = _timed_cpu_steps(pairs, seconds)
+    for e in envs:
+        e.close()
+    model, load1 = host_info()
     return {"value": round(n * steps / dt, 1), "unit": "agent-steps/s", "cores": threads, "kind": kind,
-            "sample": f"{n} envs x {steps} timed steps after 3 warm-up steps ({dt:.1f} s), level 1-1, headline "
-                      f"wrapper settings; {model}; load1 {load1}"}
+            "sample": f"{n} envs ({what}) x {steps} timed steps after 3 warm-up steps ({dt:.1f} s; construction "
+                      f"+ reset {build_s:.1f} s), {len(envs)} instance(s) by rom_mode; {model}; load1 {load1}{why}"}
 
 
-def run_ppo(args, rom, rom_name, rom_sha):
+def cpu_baseline_raw(rom, n, prologue, seconds):
+    """The reference's raw console (fm_raw_*, oracle/_ref): n consoles split over one Python thread per host
+    core (ctypes releases the GIL during each frame call), the same prologue, then random SIMPLE_MOVEMENT
+    frames, every frame rendered (palette screen + RAM in place; no RGB24 conversion)."""
+    import concurrent.futures as cf
+
+    import numpy as np
+
+    from cpu_libs import OracleRaw, RefRaw, have_ref
+    cores = host_threads()
+    kind = "reference" if have_ref() else "port"
+    mk = RefRaw if have_ref() else OracleRaw
+    if kind == "port":
+        n, cores = 64, 1
+    cons = [mk(rom) for _ in range(n)]
+    parts = [cons[t::cores] for t in range(cores)]
+    rng = np.random.default_rng(1)
+
+    def run(part, buttons):
+        for c, b in zip(part, buttons):
+            c.frame(int(b), True)
+
+    with cf.ThreadPoolExecutor(cores) as pool:
+        for f in range(prologue):
+            b = np.full(n, 8 if f % 2 == 0 else 0, np.uint8)
+            list(pool.map(run, parts, [b[t::cores] for t in range(cores)]))
+        frames, t0 = 0, time.perf_counter()
+        tab = np.array(SIMPLE_BUTTONS, np.uint8)
+        while frames < 1 or time.perf_counter() - t0 < seconds:
+            b = tab[rng.integers(0, 7, n)]
+            list(pool.map(run, parts, [b[t::cores] for t in range(cores)]))
+            frames += 1
+        dt = time.perf_counter() - t0
+    model, load1 = host_info()
+    return {"value": round(n * frames / dt, 1), "unit": "env-frames/s", "cores": cores, "kind": kind,
+            "sample": f"{n} consoles x {frames} timed frames after the {prologue}-frame prologue ({dt:.1f} s), "
+                      f"{cores} threads; {model}; load1 {load1}"}
+
+
+def run_ppo(args):
     """PPO rollout workload (config 5): the headline envs feeding a random-init bf16 Nature CNN, Gumbel-max
     actions from seed 3, 128-step rollouts with frame-deduplicated storage and GAE (0.99, 0.95)."""
     import torch
 
     from fast_mario_env_amd import HipVecEnv
     from fast_mario_env_amd.rollout import Rollout, make_net
-    n, T = args.envs, args.ppo_steps
+    rom, rom_name = pick_rom()
+    rom_sha = hashlib.sha1(rom).hexdigest()[:12]
+    n, T = args.envs or 32768, args.ppo_steps
     env = HipVecEnv("1-1", n, seed=0, sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4,
                     maxpool=True, rom=rom, device="cuda:0")
     env.reset()
@@ -165,7 +277,7 @@ def run_ppo(args, rom, rom_name, rom_sha):
     print(json.dumps(out), flush=True)
 
 
-def run_replay(args, rom, rom_name, rom_sha):
+def run_replay(args):
     """Replay workload (the GPU FrameReplay): the headline envs' transitions added to a 64-slot ring per env,
     then batches of 4096 3-step transitions sampled. Kernel times come from HIP events on the stream the
     kernels run on; the rooflines count the bytes each kernel must move."""
@@ -173,7 +285,9 @@ def run_replay(args, rom, rom_name, rom_sha):
 
     from fast_mario_env_amd import HipVecEnv
     from fast_mario_env_amd.replay import FrameReplay
-    n, C, B, ns, reps = args.envs, 64, 4096, 3, 20
+    rom, rom_name = pick_rom()
+    rom_sha = hashlib.sha1(rom).hexdigest()[:12]
+    n, C, B, ns, reps = args.envs or 32768, 64, 4096, 3, 20
     env = HipVecEnv("1-1", n, seed=0, sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4,
                     maxpool=True, rom=rom, device="cuda:0")
     rb = FrameReplay(C, n, 4, device="cuda:0", seed=0)
@@ -241,77 +355,37 @@ def run_replay(args, rom, rom_name, rom_sha):
     print(json.dumps(out), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--envs", type=int, default=32768)
-    ap.add_argument("--probe-copy-mib", type=int, default=0,
-                    help="before the steps, copy a buffer of this many MiB once (a kernel of known traffic "
-                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["headline", "ppo", "replay"], default="headline",
-                    help="headline: the env step (default); ppo: a PPO rollout feeding a Nature CNN (config 5); "
-                         "replay: env transitions into the GPU FrameReplay and sampled batches")
-    ap.add_argument("--ppo-steps", type=int, default=128, help="rollout length of --workload ppo")
-    args = ap.parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU only: every GPU box in this build has one GPU and the env step "
-              f"needs no collectives (envs shard by env_offset with zero exchange). Got --gpus {args.gpus}, "
-              f"WORLD_SIZE {world}.", file=sys.stderr)
-        sys.exit(2)
-
+def step_loop(env, args, next_actions, timed_actions):
+    """--preroll untimed steps (fresh actions from next_actions()), W warm-up and K timed steps over the rows of
+    timed_actions (pre-generated on the device). Returns the measurements of the K timed steps."""
     import torch
-
-    from fast_mario_env_amd import HipVecEnv
-    rom, rom_name = pick_rom()
-    rom_sha = hashlib.sha1(rom).hexdigest()[:12]
-    if args.workload == "ppo":
-        run_ppo(args, rom, rom_name, rom_sha)
-        return
-    if args.workload == "replay":
-        run_replay(args, rom, rom_name, rom_sha)
-        return
-    n = args.envs
-    log(f"creating {n} envs on {torch.cuda.get_device_name(0)} ({rom_name})")
+    n = env.n
+    done_acc = torch.zeros(n, dtype=torch.int32, device=env.dev)   # episodes ended per env (no per-step allocation)
+    done_tmp = torch.zeros(n, dtype=torch.bool, device=env.dev)
     t0 = time.perf_counter()
-    env = HipVecEnv("1-1", n, seed=0, sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4,
-                    maxpool=True, rom=rom, device="cuda:0")
-    env.reset()
+    for i in range(args.preroll):
+        env.step(next_actions())
+        if (i + 1) % 100 == 0:
+            torch.cuda.synchronize()
+            log(f"preroll {i + 1}/{args.preroll}")
     torch.cuda.synchronize()
-    log(f"boot + reset cache + reset: {time.perf_counter() - t0:.1f} s")
-    gen = torch.Generator(device="cuda:0")
-    gen.manual_seed(0)
-    acts = torch.randint(0, 7, (args.warmup + args.steps, n), generator=gen, device="cuda:0", dtype=torch.int64)
-    done_acc = torch.zeros(n, dtype=torch.int32, device="cuda:0")     # episodes ended per env (no per-step allocation)
-    done_tmp = torch.zeros(n, dtype=torch.bool, device="cuda:0")
-    if args.probe_copy_mib:
-        src = torch.ones(args.probe_copy_mib << 20, dtype=torch.uint8, device="cuda:0")
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"copy probe: {args.probe_copy_mib} MiB device-to-device")
-        del src, dst
+    log(f"{args.preroll} preroll steps: {time.perf_counter() - t0:.1f} s")
     for i in range(args.warmup):
-        _, _, term, trunc, _ = env.step(acts[i])
+        _, _, term, trunc, _ = env.step(timed_actions[i])
         # the timed loop's own bookkeeping ops run here first: torch loads a kernel's code on its first
         # use, ~0.1 s that would otherwise land inside the timed steps
         torch.logical_or(term, trunc, out=done_tmp)
         done_acc.add_(done_tmp)
     done_acc.zero_()
     torch.cuda.synchronize()
-    log(f"{args.warmup} warm-up steps done")
-    f0, i0 = env.frames, env.instructions()
+    f0, i0, ff0 = env.frames, env.instructions(), env.ff_instructions()
+    re0 = env.reemulations()
     env.timing(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    # progress lines need a device sync, which idles the GPU between steps: long runs only
-    every = args.steps // 4 if args.steps >= 400 else 0
+    every = args.steps // 4 if args.steps >= 400 else 0   # progress lines sync the device: long runs only
     for i in range(args.steps):
-        _, _, term, trunc, _ = env.step(acts[args.warmup + i])
+        _, _, term, trunc, _ = env.step(timed_actions[args.warmup + i])
         torch.logical_or(term, trunc, out=done_tmp)
         done_acc.add_(done_tmp)
         if every and (i + 1) % every == 0:
@@ -321,54 +395,261 @@ def main():
     dt = time.perf_counter() - t0
     stages, timed = env.timing_read()
     env.timing(False)
-    frames = env.frames - f0
-    instr = env.instructions() - i0
-    bad = env.bad_ops()
-    p_done = float(done_acc.sum().item()) / (n * args.steps)
-    value = n * args.steps / dt
-    k_step_ms = stages["k_step"] / max(1, timed)
-    workload = f"headline/{n}envs/1-1/rom:{rom_sha}"
-    k_bytes = n * (K_STEP_BYTES + K_STEP_DONE_BYTES * p_done)
+    re1 = env.reemulations()
+    steps = args.steps
+    return dict(dt=dt, stages={k: v / max(1, timed) for k, v in stages.items()},
+                p_done=float(done_acc.sum().item()) / (n * steps),
+                frames=(env.frames - f0) / (n * steps),
+                instr=(env.instructions() - i0) / (n * steps),
+                ff=(env.ff_instructions() - ff0) / (n * steps),
+                instr_total=env.instructions() - i0,
+                reemu={k: re1[k] - re0[k] for k in re1}, bad=env.bad_ops())
+
+
+def env_line(args, metric, n, m, workload_key, config, dtype="u8"):
+    """The JSON line of an env workload from the step_loop measurements."""
+    value = n * args.steps / m["dt"]
+    k_step_ms = m["stages"]["k_step"]
+    k_bytes = n * (K_STEP_BYTES + K_STEP_DONE_BYTES * m["p_done"])
     achieved = k_bytes / (k_step_ms * 1e-3) / 1e9
-    traffic = traffic_from_profiles(workload)
-    out = {
-        "metric": METRIC,
-        "value": round(value, 1),
-        "unit": "agent-steps/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(dt * 1e3 / args.steps, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "u8",
-        "data": "synthetic",
-        "config": {"workload": "headline: full wrapper stack, 32768 envs of 1-1", "envs": n, "level": "1-1",
-                   "rom": rom_name, "rom_sha1": rom_sha, "sticky": 0.25, "noop_max": 30, "skip": 4, "maxpool": True,
-                   "frame_stack": 4, "max_steps": 2000, "seed": 0, "actions": "uniform {0..6}, torch.Generator seed 0"},
+    return {
+        "metric": metric, "value": round(value, 1), "unit": "agent-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(m["dt"] * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config,
         "roofline": {"bound": "hbm", "kernel": "k_step", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
-                     "traffic": traffic,
-                     "algorithmic_bytes_per_launch": round(k_bytes),
-                     "valu_issue_frac": valu_issue_from_profiles(workload),
-                     "note": "k_step is bound by dependent VALU/LDS/memory latency per lane, not by HBM; "
-                             "valu_issue_frac is SQ_INSTS_VALU x 4 cycles over 1024 SIMDs x duration x 2.4 GHz "
-                             "from the committed rocprofv3 SQ-counter summary in profiles/"},
-        "stages_ms_per_step": {k: round(v / max(1, timed), 3) for k, v in stages.items()},
-        "p_done": round(p_done, 5),
-        "frames_per_step": round(frames / (n * args.steps), 3),
-        "instructions_per_step": round(instr / (n * args.steps), 1),
-        "emulated_instructions_per_s": round(instr / dt, 1),
-        "bad_ops": bad,
+                     "traffic": traffic_from_profiles(workload_key), "algorithmic_bytes_per_launch": round(k_bytes),
+                     "note": "the live HBM figure of k_step's algorithmic bytes (console state, env words, action, "
+                             "outputs); k_step is bound by VALU issue and dependent latency, not by HBM: see "
+                             "valu_roofline"},
+        "valu_roofline": valu_roofline(workload_key),
+        "stages_ms_per_step": {k: round(v, 3) for k, v in m["stages"].items()},
+        "p_done": round(m["p_done"], 5),
+        "preroll_steps": args.preroll,
+        "frames_per_step": round(m["frames"], 4),
+        "instructions_per_step": round(m["instr"], 1),
+        "executed_instructions_per_step": round(m["instr"] - m["ff"], 1),
+        "fast_forwarded_instructions_per_step": round(m["ff"], 1),
+        "emulated_instructions_per_s": round(m["instr_total"] / m["dt"], 1),
+        "reemulations_in_window": m["reemu"],
+        "bad_ops": m["bad"],
+        "kernel_source_sha1": kernel_source_sha1(),
     }
+
+
+def run_headline(args):
+    import torch
+
+    from fast_mario_env_amd import HipVecEnv
+    rom, rom_name = pick_rom()
+    rom_sha = hashlib.sha1(rom).hexdigest()[:12]
+    n = args.envs or 32768
+    kw = dict(sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4, maxpool=True)
+    log(f"creating {n} envs on {torch.cuda.get_device_name(0)} ({rom_name})")
+    t0 = time.perf_counter()
+    env = HipVecEnv("1-1", n, seed=0, rom=rom, device="cuda:0", **kw)
+    env.reset()
+    torch.cuda.synchronize()
+    log(f"boot + reset cache + reset: {time.perf_counter() - t0:.1f} s")
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(0)
+    pre = lambda: torch.randint(0, 7, (n,), generator=gen, device="cuda:0", dtype=torch.int64)  # noqa: E731
+    gen_t = torch.Generator(device="cuda:0")
+    gen_t.manual_seed(0)
+    acts = torch.randint(0, 7, (args.warmup + args.steps, n), generator=gen_t, device="cuda:0", dtype=torch.int64)
+    if args.probe_copy_mib:
+        src = torch.ones(args.probe_copy_mib << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.probe_copy_mib} MiB device-to-device")
+        del src, dst
+    m = step_loop(env, args, pre, acts)
+    env.close()
+    config = {"workload": f"headline: full wrapper stack, {n} envs of 1-1", "envs": n, "level": "1-1",
+              "rom": rom_name, "rom_sha1": rom_sha, "seed": 0, **kw,
+              "actions": "uniform {0..6}, torch.Generator seed 0 (preroll: its own seed-0 generator)"}
+    out = env_line(args, METRIC, n, m, f"headline/{n}envs/1-1/rom:{rom_sha}", config)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        out["cpu_baseline"] = cpu_baseline(rom, args.cpu_seconds)
+        import numpy as np
+        rng = np.random.default_rng(0)
+        out["cpu_baseline"] = cpu_baseline_env({"vanilla": rom}, dict(seed=0, **kw), ["1-1"] * args.cpu_envs,
+                                               ["vanilla"] * args.cpu_envs, args.cpu_seconds, args.cpu_envs,
+                                               lambda k: rng.integers(0, 7, k), "headline settings, 1-1")
     else:
         out["cpu_baseline"] = None
-    env.close()
     print(json.dumps(out), flush=True)
+
+
+def stress_actions(gen, n):
+    import torch
+    u = torch.rand(n, generator=gen, device="cuda:0")
+    r = torch.randint(0, 7, (n,), generator=gen, device="cuda:0", dtype=torch.int64)
+    return torch.where(u < 0.5, torch.full_like(r, 2), r)
+
+
+def run_stress(args):
+    import numpy as np
+    import torch
+
+    from build_roms import MODES
+    from fast_mario_env_amd import ALL_LEVELS, HipVecEnv
+    n = args.envs or 65536
+    roms, names = {}, []
+    for m in MODES:
+        roms[m], nm = pick_rom(m)
+        names.append(nm)
+    rom_sha = hashlib.sha1(b"".join(roms[m] for m in MODES)).hexdigest()[:12]
+    levels = [ALL_LEVELS[k] for k in np.random.default_rng(7).integers(0, 32, n)]
+    modes = [MODES[i % 4] for i in range(n)]
+    kw = dict(sticky=0.25, noop_max=30, max_steps=2000, skip=4, frame_stack=4, maxpool=False)
+    log(f"creating {n} envs ({len(set(levels))} levels x 4 rom modes) on {torch.cuda.get_device_name(0)}")
+    t0 = time.perf_counter()
+    env = HipVecEnv(levels, n, seed=0, rom=roms, rom_mode=modes, device="cuda:0", **kw)
+    env.reset()
+    torch.cuda.synchronize()
+    log(f"boot + reset cache + reset: {time.perf_counter() - t0:.1f} s")
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(0)
+    acts = torch.stack([stress_actions(gen, n) for _ in range(args.warmup + args.steps)])
+    m = step_loop(env, args, lambda: stress_actions(gen, n), acts)
+    env.close()
+    config = {"workload": f"stress: {n} envs, 32 levels x 4 rom modes, biased actions", "envs": n,
+              "levels": "ALL_LEVELS[default_rng(7).integers(0, 32, n)]", "rom_mode": "MODES[i % 4]",
+              "roms": names, "rom_sha1": rom_sha, "seed": 0, **kw,
+              "actions": "per env and step: 2 with p=0.5 else uniform {0..6}; torch.Generator seed 0"}
+    metric = f"agent env-steps/sec (skip=4) at {n} envs, divergence stress (32 levels x 4 rom modes) on 1 MI355X"
+    out = env_line(args, metric, n, m, f"stress/{n}envs/rom:{rom_sha}", config)
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        rng = np.random.default_rng(0)
+        ncpu = args.cpu_envs if args.cpu_envs != 32768 else 8192
+
+        def act(k):
+            return np.where(rng.random(k) < 0.5, 2, rng.integers(0, 7, k))
+        out["cpu_baseline"] = cpu_baseline_env(roms, dict(seed=0, **kw), levels, modes, args.cpu_seconds, ncpu, act,
+                                               "the first envs of the stress configuration")
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+def run_raw(args):
+    import numpy as np
+    import torch
+
+    from fast_mario_env_amd import HipRawNES, palette_rgb
+    from fast_mario_env_amd._native import check, lib
+    rom, rom_name = pick_rom()
+    rom_sha = hashlib.sha1(rom).hexdigest()[:12]
+    n, prologue = args.envs or 4096, 40
+    frames = args.steps
+    dev = "cuda:0"
+    log(f"creating {n} raw consoles ({rom_name})")
+    con = HipRawNES(rom, n, device=dev)
+    L = lib()
+    s = torch.cuda.current_stream(0).cuda_stream
+    rgb = torch.empty(n, 240, 256, 3, dtype=torch.uint8, device=dev)
+    ram = torch.empty(n, 2048, dtype=torch.uint8, device=dev)
+    rgb64 = torch.from_numpy(palette_rgb().reshape(-1).copy()).to(dev)
+    tab = torch.tensor(SIMPLE_BUTTONS, dtype=torch.uint8, device=dev)
+    rng = np.random.default_rng(1)
+    sched = [torch.full((n,), 8 if f % 2 == 0 else 0, dtype=torch.uint8, device=dev) for f in range(prologue)]
+    draws = torch.from_numpy(rng.integers(0, 7, (args.warmup + frames, n))).to(dev)
+    buttons = tab[draws]                                          # (W + K, n) button bytes on the device
+
+    def one(b):
+        check(L.mh_raw_frame(con.h, b.data_ptr(), 1, s), "mh_raw_frame")
+        check(L.mh_raw_screen_rgb(con.h, rgb64.data_ptr(), rgb.data_ptr(), s), "mh_raw_screen_rgb")
+        check(L.mh_raw_ram(con.h, ram.data_ptr(), s), "mh_raw_ram")
+
+    for b in sched:
+        one(b)
+    for f in range(args.warmup):
+        one(buttons[f])
+    torch.cuda.synchronize()
+    i0, ff0 = con.instructions(), con.ff_instructions()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * frames)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for f in range(frames):
+        ev[2 * f].record()
+        check(L.mh_raw_frame(con.h, buttons[args.warmup + f].data_ptr(), 1, s), "mh_raw_frame")
+        ev[2 * f + 1].record()
+        check(L.mh_raw_screen_rgb(con.h, rgb64.data_ptr(), rgb.data_ptr(), s), "mh_raw_screen_rgb")
+        check(L.mh_raw_ram(con.h, ram.data_ptr(), s), "mh_raw_ram")
+        if frames >= 1000 and (f + 1) % (frames // 4) == 0:
+            torch.cuda.synchronize()
+            log(f"frame {f + 1}/{frames}")
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    k_raw_ms = sum(ev[2 * f].elapsed_time(ev[2 * f + 1]) for f in range(frames)) / frames
+    instr = con.instructions() - i0
+    ff = con.ff_instructions() - ff0
+    bad = con.bad_ops()
+    # k_raw's algorithmic bytes per console and frame: console state read + written, the button byte, the
+    # rendered palette screen written
+    k_bytes = n * (2 * STATE_BYTES + 1 + 240 * 256)
+    achieved = k_bytes / (k_raw_ms * 1e-3) / 1e9
+    out = {
+        "metric": f"raw emulator env-frames/sec (skip=1, every frame rendered, RGB24 + RAM out) at {n} consoles on 1 MI355X",
+        "value": round(n * frames / dt, 1), "unit": "env-frames/s", "n_gpus": 1, "steps": frames, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / frames, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic",
+        "config": {"workload": f"raw: {n} consoles, 1-1 via a {prologue}-frame Start/none prologue, then SIMPLE_MOVEMENT "
+                               f"buttons from default_rng(1) per console and frame", "envs": n, "rom": rom_name,
+                   "rom_sha1": rom_sha, "outputs_per_frame": "RGB24 screen (184,320 B) + RAM (2,048 B) per console"},
+        "roofline": {"bound": "hbm", "kernel": "k_raw", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
+                     "algorithmic_bytes_per_launch": k_bytes,
+                     "note": "console state read + written, buttons, palette screen written; like k_step, k_raw is "
+                             "an interpreter bound by VALU issue and dependent latency"},
+        "k_raw_ms": round(k_raw_ms, 4),
+        "instructions_per_frame": round(instr / (n * frames), 1),
+        "executed_instructions_per_frame": round((instr - ff) / (n * frames), 1),
+        "fast_forwarded_instructions_per_frame": round(ff / (n * frames), 1),
+        "bad_ops": bad, "kernel_source_sha1": kernel_source_sha1(),
+    }
+    del con
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        out["cpu_baseline"] = cpu_baseline_raw(rom, n, prologue, args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (frames for raw); default 100 (raw 5000)")
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--preroll", type=int, default=None,
+                    help="untimed steps before the warm-up so the timed window has episode ends (default 300 for "
+                         "headline and stress, 0 otherwise)")
+    ap.add_argument("--envs", type=int, default=0, help="env count (default: the workload's configuration)")
+    ap.add_argument("--probe-copy-mib", type=int, default=0,
+                    help="before the steps, copy a buffer of this many MiB once (a kernel of known traffic "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-envs", type=int, default=32768, help="envs of the CPU baseline sample (host RAM allowing)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=["headline", "stress", "raw", "ppo", "replay"], default="headline")
+    ap.add_argument("--ppo-steps", type=int, default=128, help="rollout length of --workload ppo")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: every GPU box in this build has one GPU and the env step "
+              f"needs no collectives (envs shard by env_offset with zero exchange). Got --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}.", file=sys.stderr)
+        sys.exit(2)
+    if args.steps is None:
+        args.steps = 5000 if args.workload == "raw" else 100
+    if args.preroll is None:
+        args.preroll = 300 if args.workload in ("headline", "stress") else 0
+    {"headline": run_headline, "stress": run_stress, "raw": run_raw, "ppo": run_ppo,
+     "replay": run_replay}[args.workload](args)
 
 
 if __name__ == "__main__":

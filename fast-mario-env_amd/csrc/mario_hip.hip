@@ -806,6 +806,7 @@ int mh_replay_add(uint8_t* frames, uint8_t* age, int16_t* act, float* rew, uint8
         !done || !truncated || n_envs < 1 || capacity < 2 || k < 1 || frame_bytes < 16 || frame_bytes % 16) {
         g_err = "invalid arguments"; return -1;
     }
+    if (k > capacity) { g_err = "stack depth k exceeds the ring capacity"; return -1; }
     if (!aligned16(frames) || !aligned16(obs) || !aligned16(next_obs)) { g_err = "frame buffers must be 16-byte aligned"; return -1; }
     ReplayAddArgs A{ReplayRing{frames, age, act, rew, flags, ptr, new_ep, n_envs, capacity, (uint32_t)frame_bytes},
                     obs, next_obs, k, action, reward, done, truncated};
@@ -824,6 +825,8 @@ int mh_replay_gather(const uint8_t* frames, const uint8_t* age, const int16_t* a
         frame_bytes < 16 || frame_bytes % 16 || batch < 0 || n_step < 0) {
         g_err = "invalid arguments"; return -1;
     }
+    // a stack reaches k - 1 slots back from its newest one: deeper than the ring it would wrap onto itself
+    if (k > capacity) { g_err = "stack depth k exceeds the ring capacity"; return -1; }
     if (!aligned16(frames) || !aligned16(obs) || !aligned16(next_obs)) { g_err = "frame buffers must be 16-byte aligned"; return -1; }
     if (batch == 0) return 0;
     ReplayGatherArgs A{ReplayRing{(uint8_t*)frames, (uint8_t*)age, (int16_t*)act, (float*)rew, (uint8_t*)flags,

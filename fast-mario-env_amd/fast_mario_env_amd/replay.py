@@ -47,11 +47,14 @@ class FrameReplay:
     """Replay ring of `capacity_per_env` frames for each of `n_envs` envs, k-frame stacks of hw frames."""
 
     def __init__(self, capacity_per_env: int, n_envs: int, k: int = 4, hw=(84, 84), device="cuda", seed=None):
-        torch = self.torch = _torch()
         self.C, self.E, self.k, self.hw = int(capacity_per_env), int(n_envs), int(k), tuple(hw)
         self.fb = self.hw[0] * self.hw[1]
         if self.C < 2 or self.E < 1 or self.k < 1 or self.fb % 16:
             raise ValueError("FrameReplay needs capacity_per_env >= 2, n_envs >= 1, k >= 1 and H*W a multiple of 16")
+        if self.k > self.C:
+            raise ValueError(f"FrameReplay: stack depth k={self.k} exceeds capacity_per_env={self.C} (a stack would "
+                             "reach past the oldest frame the ring keeps)")
+        torch = self.torch = _torch()
         self.dev = torch.device(device)
         if self.dev.type != "cuda":
             raise ValueError("FrameReplay keeps its ring in GPU memory: device must be a ROCm GPU")

@@ -139,6 +139,7 @@ void    mh_raw_destroy(MhRaw* h);
 #define MH_RESIZE_MAX_IMAGES 65535
 int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
+
 /* ---- frame-deduplicating replay ring (device storage owned by the caller)
  * The ring of FrameReplay (src/fast_mario_env/replay.py:43-60) for n_envs envs and `capacity` slots each,
  * all device memory, slot s of env e at index e * capacity + s:
@@ -149,7 +150,8 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
  *   ptr     i64 [n_envs]             slots written so far
  *   new_ep  u8  [n_envs]             the next add starts an episode (1 initially) */
 
-/* FrameReplay.add (replay.py:76-95): obs / next_obs are (n_envs, k, frame_bytes) stacks, of which only
+/* Both replay entry points require 2 <= capacity and 1 <= k <= capacity (-1 otherwise).
+ * FrameReplay.add (replay.py:76-95): obs / next_obs are (n_envs, k, frame_bytes) stacks, of which only
  * the newest frame is stored (obs's only when new_ep is set); action i64, reward f32, done and truncated
  * u8, n_envs each. Updates ptr and new_ep on the device. */
 int mh_replay_add(uint8_t* frames, uint8_t* age, int16_t* act, float* rew, uint8_t* flags, int64_t* ptr,

@@ -2,8 +2,8 @@
 
 The small parity tests fit in one workgroup (128 env slots). These run many: 4,096 envs (32 workgroups) with
 the headline wrappers, 4,096 raw consoles, and the 65,536-env divergence-stress instance (512 workgroups; its
-second frame buffer starts 4.03e9 bytes in and ends past 2^33). Every env's outputs are recorded on the
-device; a sample of envs (a fixed stride, the last env, and envs whose episodes ended, which take the reset,
+second frame buffer starts 4.03e9 bytes in and ends past 2^33). The outputs are recorded on the device; a
+sample of envs (a fixed stride, the last env, and envs whose episodes ended, which take the reset,
 final_obs and re-emulation paths) is then replayed by one-env CPU oracles on the sampled env's own PCG64
 stream (env_offset = its index, as the reference's env_offset equivalence allows, env.py:155-156), bit for
 bit. Every env is also checked against size-independent properties: the frame-stack shift and reset stack of
@@ -33,46 +33,45 @@ def _first_diff(a, b):
     return d[:8].tolist()
 
 
-def _record(env, actions):
-    """Reset, then step every row of `actions` (T, N) on the device; every output kept on the device."""
-    rec = {"obs0": env.reset().clone(), "canon0": env.canon()}
+def _record(env, actions, keep=None):
+    """Reset, then step every row of `actions` (T, N) on the device. Checks k_stack's invariants on every env as
+    it goes (the stack shifts by one frame; a finished episode's final_obs is the shifted stack plus the last
+    frame, and its new stack is [0, ..., 0, reset frame]) and keeps the outputs of the envs `keep` (all if
+    None) on the device, plus every env's done flags."""
+    idx = None if keep is None else torch.as_tensor(keep, dtype=torch.long, device=env.dev)
+    rows = (lambda x: x) if idx is None else (lambda x: x[idx])
+    prev = env.reset().clone()
+    rec = {"obs0": rows(prev).clone(), "canon0": rows(env.canon()), "done": []}
     keys = ("obs", "rew", "term", "trunc", "info", "ram", "fin", "ep_ret", "ep_len")
     for k in keys:
         rec[k] = []
-    for a in actions:
+    for t, a in enumerate(actions):
         obs, rew, term, trunc, _ = env.step(a)
         done = term | trunc
-        rec["obs"].append(obs.clone())
-        rec["rew"].append(rew.clone())
-        rec["term"].append(term.clone())
-        rec["trunc"].append(trunc.clone())
-        rec["info"].append(env.info_t.clone())
-        rec["ram"].append(env.ram())
-        # final_obs / episode stats are valid only where the episode ended: keep those rows as a dense copy
-        rec["fin"].append(torch.where(done[:, None, None, None], env.final_obs, 0))
-        rec["ep_ret"].append(torch.where(done, env.ep_ret, 0))
-        rec["ep_len"].append(torch.where(done, env.ep_len, 0))
+        live = ~done
+        assert torch.equal(obs[live][:, :-1], prev[live][:, 1:]), (t, "stack shift")
+        if done.any():
+            assert torch.equal(env.final_obs[done][:, :-1], prev[done][:, 1:]), (t, "final_obs shift")
+            assert not obs[done][:, :-1].any(), (t, "reset stack")
+        prev.copy_(obs)
+        rec["done"].append(done.clone())
+        rec["obs"].append(rows(obs).clone())
+        rec["rew"].append(rows(rew).clone())
+        rec["term"].append(rows(term).clone())
+        rec["trunc"].append(rows(trunc).clone())
+        rec["info"].append(rows(env.info_t).clone())
+        rec["ram"].append(rows(env.ram()))
+        # final_obs / episode stats are valid only where the episode ended
+        d = rows(done)
+        rec["fin"].append(torch.where(d[:, None, None, None], rows(env.final_obs), 0))
+        rec["ep_ret"].append(torch.where(d, rows(env.ep_ret), 0))
+        rec["ep_len"].append(torch.where(d, rows(env.ep_len), 0))
     torch.cuda.synchronize()
     return rec
 
 
-def _check_stack_invariants(rec):
-    """k_stack on every env: the stack shifts by one frame, a finished episode's final_obs is the shifted stack
-    plus the last frame, and its new stack is [0, ..., 0, reset frame]."""
-    prev = rec["obs0"]
-    for t, obs in enumerate(rec["obs"]):
-        done = rec["term"][t] | rec["trunc"][t]
-        live = ~done
-        assert torch.equal(obs[live][:, :-1], prev[live][:, 1:]), (t, "stack shift")
-        if done.any():
-            fin = rec["fin"][t][done]
-            assert torch.equal(fin[:, :-1], prev[done][:, 1:]), (t, "final_obs shift")
-            assert not obs[done][:, :-1].any(), (t, "reset stack")
-        prev = obs
-
-
-def _sample(n, stride, rec, extra):
-    done_any = torch.stack([a | b for a, b in zip(rec["term"], rec["trunc"])]).any(0).cpu().numpy()
+def _sample(n, stride, done_steps, extra):
+    done_any = torch.stack(done_steps).any(0).cpu().numpy()
     picks = set(range(0, n, stride)) | {n - 1}
     done_idx = np.flatnonzero(done_any)
     picks |= set(done_idx[np.linspace(0, len(done_idx) - 1, min(extra, len(done_idx))).astype(int)].tolist()) \
@@ -81,11 +80,12 @@ def _sample(n, stride, rec, extra):
 
 
 def _replay_samples(rec, samples, names, modes, kw, seed, actions):
+    """rec holds the outputs of exactly the envs `samples`, in that order."""
     acts = actions.cpu().numpy()
-    host = {k: [x[samples].cpu().numpy() for x in rec[k]] for k in
+    host = {k: [x.cpu().numpy() for x in rec[k]] for k in
             ("obs", "rew", "term", "trunc", "info", "ram", "fin", "ep_ret", "ep_len")}
-    obs0 = rec["obs0"][samples].cpu().numpy()
-    canon0 = rec["canon0"][samples].cpu().numpy()
+    obs0 = rec["obs0"].cpu().numpy()
+    canon0 = rec["canon0"].cpu().numpy()
     eps = 0
     for j, i in enumerate(samples):
         cpu = OracleVec(ROMS[modes[i]], _levels([names[i]]), 1, seed=seed, env_offset=i, **kw)
@@ -107,16 +107,31 @@ def _replay_samples(rec, samples, names, modes, kw, seed, actions):
     return eps
 
 
-def _run(names, modes, kw, seed, actions, stride, extra):
+def _run(names, modes, kw, seed, actions, stride, extra, two_pass=False):
+    """Run the GPU instance, pick the samples (a stride, the last env, envs whose episodes ended) and replay them
+    on the CPU. With two_pass, a first run only finds the samples and a second, identical instance records
+    just their outputs (the device then holds a few envs' outputs per step instead of every env's)."""
     from fast_mario_env_amd import HipVecEnv
     n = len(names)
     rom = {m: ROMS[m] for m in set(modes)}
-    env = HipVecEnv(names, n, seed=seed, rom=rom, rom_mode=modes, device="cuda:0", **kw)
+
+    def make():
+        return HipVecEnv(names, n, seed=seed, rom=rom, rom_mode=modes, device="cuda:0", **kw)
+    env = make()
     print(f"scale run: {n} envs, {len(actions)} steps", flush=True)
-    rec = _record(env, actions)
-    _check_stack_invariants(rec)
+    rec = _record(env, actions, keep=[] if two_pass else None)
     assert env.bad_ops() == 0
-    samples, n_done = _sample(n, stride, rec, extra)
+    samples, n_done = _sample(n, stride, rec["done"], extra)
+    if two_pass:
+        env.close()
+        del rec
+        env = make()
+        rec = _record(env, actions, keep=samples)
+        assert env.bad_ops() == 0
+    else:
+        idx = torch.as_tensor(samples, device="cuda:0")
+        rec = {k: (v[idx] if k in ("obs0", "canon0") else [x[idx] for x in v]) if k != "done" else v
+               for k, v in rec.items()}
     print(f"  {n_done} envs ended an episode; replaying {len(samples)} sampled envs on the CPU", flush=True)
     eps = _replay_samples(rec, samples, names, modes, kw, seed, actions)
     re = env.reemulations()
@@ -142,14 +157,14 @@ def test_divergence_stress_65536_envs():
     world-stage pairs, rom_mode cycled over the four variants per env, sticky 0.25, no-op 30, skip 4, no
     max-pool; per env, action 2 (right + A) with p = 0.5, else uniform over 0..6."""
     from fast_mario_env_amd import ALL_LEVELS
-    n, T = 65536, 8
+    n, T = 65536, 30
     lv = np.random.default_rng(7).integers(0, 32, n)
     names = [ALL_LEVELS[k] for k in lv]
     modes = [MODES[i % 4] for i in range(n)]
     rng = np.random.default_rng(3)
     acts = np.where(rng.random((T, n)) < 0.5, 2, rng.integers(0, 7, (T, n)))
     actions = torch.from_numpy(acts).to("cuda:0")
-    n_done, eps, re = _run(names, modes, STRESS, 0, actions, stride=1021, extra=24)
+    n_done, eps, re = _run(names, modes, STRESS, 0, actions, stride=1021, extra=24, two_pass=True)
     assert n_done > 0 and eps > 0
     assert re["one"] > 0, re
 

@@ -191,3 +191,23 @@ def test_replay_exact_on_env_transitions():
                 bad += not ok
                 checked += 1
     assert bad == 0, f"{bad}/{checked} sampled transitions differ"
+
+
+def test_replay_rejects_stacks_deeper_than_the_ring():
+    """k > capacity would make a stack reach past the oldest ring slot (the gather's slot arithmetic assumes
+    k <= C): the C ABI refuses it before touching the device, and so does FrameReplay."""
+    import ctypes
+
+    from fast_mario_env_amd import _native
+    L = ctypes.CDLL(_native.lib_path())
+    L.mh_last_error.restype = ctypes.c_char_p
+    P, I = ctypes.c_void_p, ctypes.c_int
+    fake = P(1 << 20)                        # never dereferenced: validation fails first
+    C, k, fb = 2, 4, 16
+    rc = L.mh_replay_add(*[fake] * 7, I(1), I(C), I(fb), I(k), *[fake] * 6, P(0))
+    assert rc == -1 and b"exceeds the ring capacity" in L.mh_last_error()
+    rc = L.mh_replay_gather(*[fake] * 5, I(1), I(C), I(fb), I(k), fake, fake, I(1), I(1), *[fake] * 9, P(0))
+    assert rc == -1 and b"exceeds the ring capacity" in L.mh_last_error()
+    from fast_mario_env_amd.replay import FrameReplay
+    with pytest.raises(ValueError, match="exceeds capacity"):
+        FrameReplay(2, 1, k=4, device="cuda")
