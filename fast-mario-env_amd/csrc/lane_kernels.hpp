@@ -19,14 +19,16 @@ struct AreaTables {
     int32_t xn[84], yn[84];
 };
 
-inline void area_taps(int ssize, int dsize, int32_t* idx, float* w, int32_t* cnt) {
+// Host and device: the device computes the same IEEE double arithmetic (division, ceil, floor and the
+// double -> float conversion are correctly rounded on both).
+__host__ __device__ inline void area_taps(int ssize, int dsize, int32_t* idx, float* w, int32_t* cnt) {
     double scale = 1.0 / ((double)dsize / ssize);
     for (int d = 0; d < dsize; d++) cnt[d] = 0;
     auto add = [&](int d, int s, float a) { idx[d * TAPS + cnt[d]] = s; w[d * TAPS + cnt[d]] = a; cnt[d]++; };
     for (int d = 0; d < dsize; d++) {
         double f1 = d * scale, f2 = f1 + scale;
         double cell = scale < ssize - f1 ? scale : ssize - f1;
-        int s1 = (int)std::ceil(f1), s2 = (int)std::floor(f2);
+        int s1 = (int)__builtin_ceil(f1), s2 = (int)__builtin_floor(f2);
         if (s2 > ssize - 1) s2 = ssize - 1;
         if (s1 > s2) s1 = s2;
         if (s1 - f1 > 1e-3) add(d, s1 - 1, (float)((s1 - f1) / cell));
@@ -39,8 +41,8 @@ inline void area_taps(int ssize, int dsize, int32_t* idx, float* w, int32_t* cnt
     }
 }
 
-inline void area_tables(AreaTables* T) {
-    memset(T, 0, sizeof(*T));
+__host__ __device__ inline void area_tables(AreaTables* T) {
+    for (int i = 0; i < 84 * TAPS; i++) { T->xs[i] = T->ys[i] = 0; T->xw[i] = T->yw[i] = 0.f; }
     area_taps(256, 84, T->xs, T->xw, T->xn);
     area_taps(240, 84, T->ys, T->yw, T->yn);
 }

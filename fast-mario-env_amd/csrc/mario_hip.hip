@@ -796,6 +796,51 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
     return 0;
 }
 
+// ---- the allocation-free resize (mh_resize_noalloc)
+// Its filter tables live in `scratch`, a file-scope device array: every GPU the library runs on holds one
+// copy, at its own address, until the process ends. The first call on a device looks up that device's
+// address of the array (hipGetSymbolAddress; the array's name in host code is only a host-side stand-in)
+// and writes the tables there with one kernel on the caller's stream; later calls only read them.
+constexpr size_t MH_SCRATCH_BYTES = 16384;
+static_assert(sizeof(AreaTables) <= MH_SCRATCH_BYTES, "the area tables must fit the scratch array");
+static __device__ __align__(256) uint8_t scratch[MH_SCRATCH_BYTES];
+constexpr int MH_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static AreaTables* g_scratch_tables[MH_MAX_DEVICES];   // the device address of `scratch`, per device
+
+__global__ void k_area_tables(AreaTables* T) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) area_tables(T);
+}
+
+static AreaTables* scratch_tables(hipStream_t s) {
+    int dev = 0;
+    if (!ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (dev < 0 || dev >= MH_MAX_DEVICES) { g_err = "device index beyond the allocation-free path's table"; return nullptr; }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_tables[dev]) {
+        void* p = nullptr;
+        if (!ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return nullptr;
+        hipLaunchKernelGGL(k_area_tables, dim3(1), dim3(64), 0, s, (AreaTables*)p);
+        if (!ok(hipGetLastError(), "k_area_tables launch")) return nullptr;
+        g_scratch_tables[dev] = (AreaTables*)p;
+    }
+    return g_scratch_tables[dev];
+}
+
+int mh_resize_noalloc(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
+    if (!d_src || !d_dst) { g_err = "null image buffer"; return -1; }
+    if (n < 1 || n > MH_RESIZE_MAX_IMAGES) {
+        g_err = "mh_resize_noalloc: n = " + std::to_string(n) + " images; one call takes 1 .. 65535";
+        return -1;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    AreaTables* T = scratch_tables(s);
+    if (!T) return -1;
+    hipLaunchKernelGGL(k_resize_images, dim3((OBS_PIX + 255) / 256, n), dim3(256), 0, s, d_src, d_dst, n, (const AreaTables*)T);
+    CK(hipGetLastError());
+    return 0;
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int mh_replay_add(uint8_t* frames, uint8_t* age, int16_t* act, float* rew, uint8_t* flags, int64_t* ptr,

@@ -139,6 +139,13 @@ void    mh_raw_destroy(MhRaw* h);
 #define MH_RESIZE_MAX_IMAGES 65535
 int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
+/* mh_resize without any device allocation: no counterpart in the reference. For callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same
+ * kernel and results as mh_resize; its filter tables (8.7 KB) sit in a 16 KB file-scope device array the
+ * library holds on every GPU it runs on until the process ends, written by the first call on a device (one
+ * kernel on that call's stream). At most MH_RESIZE_MAX_IMAGES images per call; more is refused (-1).
+ * A call on another stream that overlaps the first call on the same GPU races with the tables' set-up. */
+int mh_resize_noalloc(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
 /* ---- frame-deduplicating replay ring (device storage owned by the caller)
  * The ring of FrameReplay (src/fast_mario_env/replay.py:43-60) for n_envs envs and `capacity` slots each,
