@@ -195,7 +195,7 @@ struct LaneCtx {
     const uint8_t* lut;
     uint32_t* sp;     // this lane's sprite line buffer (stride LDS_LANES words)
     uint32_t* gp;     // this lane's gray palette, tile row and OAM (stride LDS_LANES words)
-    uint8_t twin;     // which of the env's two twin lanes this is
+    uint8_t part;     // which of the env's LANES_PER_ENV lanes this is
 };
 
 // console e of the memory block `mem` (np consoles), on CHR bank `bank` of the staged cartridge
@@ -205,7 +205,7 @@ __device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* me
     c.cart = x.cart; c.cart.chr += bank * 0x2000u; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
     c.lds_bg = x.gp + LDS_GP_WORDS * LDS_LANES; c.bg_key = -1;
     c.lds_oam = x.gp + (LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES;
-    c.twin = x.twin;
+    c.part = x.part;
     c.bad_ops = 0; c.instructions = 0; c.ff_instructions = 0;
     c.pend_line = -1; c.sp_line = -1; c.pal_dirty = true;
 }
@@ -248,6 +248,7 @@ struct StepArgs {
     const int64_t* actions;
     float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
     const uint8_t* key_bank;      // CHR bank of each (level, ROM) key (E_LEVEL)
+    const int32_t* slot_env;      // env of each console slot (actions in and outputs out are in env order)
 };
 
 struct ResetArgs {
@@ -362,8 +363,9 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
     A.cframes[ci] = ev.frames; A.cinstr[ci] = c.instructions; A.cff[ci] = c.ff_instructions; A.cbad[ci] = c.bad_ops;
 }
 
-// One agent step of env e (fastmario.cpp:403-411 + 336-374).
+// One agent step of the env in console slot e (fastmario.cpp:403-411 + 336-374).
 __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e) {
+    const uint32_t o = (uint32_t)A.slot_env[e];   // the env's index in the action and output arrays
     Console c;
     attach(c, x, A.mem, A.np, e, A.key_bank[A.ev[(size_t)E_LEVEL * A.np + e]]);
     c.load(A.sc, e);
@@ -371,7 +373,7 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     load_env(ev, A.ev, A.np, e);
     Pcg rng;
     rng.load(A.ev, A.np, e);
-    int64_t a64 = A.actions[e];
+    int64_t a64 = A.actions[o];
     const int act = (a64 >= 0 && a64 < 7) ? (int)a64 : 0;
     Stepper stp{c, ev, A.cfg, &rng, A.gray + gray_lane_offset(e), A.gray + (size_t)GRAY_PIX * A.np + gray_lane_offset(e),
                 Region{A.mem, A.sc, A.np, e}, A.snap_mem, A.snap_sc};
@@ -380,12 +382,12 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     ev.t++;
     const bool tr = ev.t >= A.cfg.max_steps;
     ev.ep_ret += r; ev.ep_len++;
-    A.rew[e] = (float)r;
-    A.term[e] = tm;
-    A.trunc[e] = tr;
-    for (int k = 0; k < 10; k++) A.info[(size_t)e * 10 + k] = (int32_t)ev.info.v[k];
+    A.rew[o] = (float)r;
+    A.term[o] = tm;
+    A.trunc[o] = tr;
+    for (int k = 0; k < 10; k++) A.info[(size_t)o * 10 + k] = (int32_t)ev.info.v[k];
     const bool done = tm || tr;
-    if (done) { A.ep_ret_out[e] = ev.ep_ret; A.ep_len_out[e] = ev.ep_len; }
+    if (done) { A.ep_ret_out[o] = ev.ep_ret; A.ep_len_out[o] = ev.ep_len; }
     c.store(A.sc, e);
     store_env(ev, A.ev, A.np, e);
     rng.store(A.ev, A.np, e);

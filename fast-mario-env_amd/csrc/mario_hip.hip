@@ -8,7 +8,9 @@
 //   k_stack         LDS-transposed frame-stack shift, final_obs, reset observation
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
+#include <tuple>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -42,52 +44,68 @@ __device__ __forceinline__ void stage_rom(const RomArgs& R, uint8_t* s_rom, uint
     __shared__ uint32_t s_sp[LDS_SP_WORDS * LDS_LANES];              \
     __shared__ uint32_t s_gp[LDS_GP_REGION * LDS_LANES];
 
-// Env slot of this thread within its block (0 .. LDS_LANES-1). Lanes l and l + 32 of a wave are twins:
-// they carry the same env, run its console in lockstep (identical state, identical loads and stores of
-// identical values) and share its LDS buffers; only the renderer gives them different work.
+// Env slot of this thread within its block (0 .. LDS_LANES-1). Lanes l, l + ENVS_PER_WAVE, ... of a wave are
+// the parts of one env: they run its console in lockstep (identical state, identical loads and stores of
+// identical values) and share its LDS buffers; only the renderer and the sprite evaluation give them
+// different work.
 __device__ __forceinline__ int lane_slot() {
     return (int)(threadIdx.x >> 6) * ENVS_PER_WAVE + (int)(threadIdx.x & (ENVS_PER_WAVE - 1));
 }
-__device__ __forceinline__ uint8_t lane_twin() { return (uint8_t)((threadIdx.x / ENVS_PER_WAVE) & 1u); }
+__device__ __forceinline__ uint8_t lane_part() {
+    return (uint8_t)(((threadIdx.x & 63u) / ENVS_PER_WAVE) & (LANES_PER_ENV - 1));
+}
 
 __device__ __forceinline__ LaneCtx lane_ctx(const RomArgs& R, const uint8_t* s_rom, const uint8_t* s_lut,
                                             const uint32_t* s_dec, uint32_t* s_sp, uint32_t* s_gp, int slot) {
-    return LaneCtx{make_cart(R, s_rom, s_dec), s_lut, s_sp + slot, s_gp + slot, lane_twin()};
+    return LaneCtx{make_cart(R, s_rom, s_dec), s_lut, s_sp + slot, s_gp + slot, lane_part()};
 }
 
 constexpr int EMU_THREADS = 64 * WAVES_PER_BLOCK;
+#define EMU_BOUNDS __launch_bounds__(EMU_THREADS, EMU_WAVES_PER_SIMD)
 // blocks of an emulator kernel over `count` envs
-static inline dim3 emu_grid(int count) { return dim3((unsigned)((count + LDS_LANES - 1) / LDS_LANES)); }
+// Launch shape of an emulator kernel over `count` consoles on a GPU with `cus` compute units: blocks of up to
+// WAVES_PER_BLOCK waves (one block per CU: its LDS). When count is too small to give every CU a full block, the
+// blocks shrink (down to one wave) so that the waves spread over all CUs instead of sharing a few CUs' SIMDs.
+struct EmuLaunch { dim3 grid, block; };
+static inline EmuLaunch emu_launch(int count, int cus) {
+    const int per_full_wave = ENVS_PER_WAVE * (cus > 0 ? cus : 1);
+    int waves = (count + per_full_wave - 1) / per_full_wave;
+    waves = waves < 1 ? 1 : waves > WAVES_PER_BLOCK ? WAVES_PER_BLOCK : waves;
+    const int slots = waves * ENVS_PER_WAVE;
+    return EmuLaunch{dim3((unsigned)((count + slots - 1) / slots)), dim3((unsigned)(64 * waves))};
+}
+// first console slot of this block (blocks of blockDim.x / 64 waves)
+__device__ __forceinline__ uint32_t block_base() { return blockIdx.x * ((blockDim.x >> 6) * ENVS_PER_WAVE); }
 
-__global__ void __launch_bounds__(EMU_THREADS) k_boot(BootArgs A) {
+__global__ void EMU_BOUNDS k_boot(BootArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    const int l = (int)(blockIdx.x * LDS_LANES + slot);
+    const int l = (int)(block_base() + slot);
     if (l < A.nl) boot_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), l);
 }
 
-__global__ void __launch_bounds__(EMU_THREADS) k_cache(CacheArgs A) {
+__global__ void EMU_BOUNDS k_cache(CacheArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    const int ci = (int)(blockIdx.x * LDS_LANES + slot);
+    const int ci = (int)(block_base() + slot);
     if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), ci);
 }
 
-__global__ void __launch_bounds__(EMU_THREADS) k_step(StepArgs A) {
+__global__ void EMU_BOUNDS k_step(StepArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    const uint32_t e = (uint32_t)(blockIdx.x * LDS_LANES + slot);
+    const uint32_t e = block_base() + (uint32_t)slot;
     if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }
 
-__global__ void __launch_bounds__(EMU_THREADS) k_raw(RawArgs A) {
+__global__ void EMU_BOUNDS k_raw(RawArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     const int slot = lane_slot();
-    const uint32_t e = (uint32_t)(blockIdx.x * LDS_LANES + slot);
+    const uint32_t e = block_base() + (uint32_t)slot;
     if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }
 
@@ -162,7 +180,8 @@ __global__ void __launch_bounds__(192) k_obs(ObsArgs A) {
 
 struct StackArgs {
     int n; uint32_t np; int K;
-    uint8_t* obs; uint8_t* fin;   // [e][K][OBS_PIX]
+    uint8_t* obs; uint8_t* fin;   // [env][K][OBS_PIX]
+    const int32_t* slot_env;      // env of each console slot
     const uint8_t* fresh;         // word w (pixels 4w .. 4w+3) of env e at 32-bit word [w * np + e]
     const uint32_t* ev;
     const uint8_t* cobs;          // [ci * OBS_PIX + o]
@@ -191,7 +210,8 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
         const uint32_t e = e0 + j;
         const int w = w0 + wl;
         if (w >= nw || e >= (uint32_t)A.n) continue;
-        uint32_t* st = (uint32_t*)A.obs + e * fw;
+        const size_t env = (size_t)A.slot_env[e];
+        uint32_t* st = (uint32_t*)A.obs + env * fw;
         const uint32_t ri = A.ev[(size_t)E_RESET_IDX * A.np + e];
         if (A.mode == 1) {
             for (int s = 0; s < A.K - 1; s++) st[(size_t)s * nw + w] = 0;
@@ -200,7 +220,7 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
         }
         const uint32_t fresh = tile[wl][j];
         if (ri != 0xffffffffu) {
-            uint32_t* fo = (uint32_t*)A.fin + e * fw;
+            uint32_t* fo = (uint32_t*)A.fin + env * fw;
             for (int s = 0; s < A.K - 1; s++) { fo[(size_t)s * nw + w] = st[(size_t)(s + 1) * nw + w]; st[(size_t)s * nw + w] = 0; }
             fo[(size_t)(A.K - 1) * nw + w] = fresh;
             st[(size_t)(A.K - 1) * nw + w] = ((const uint32_t*)A.cobs)[(size_t)ri * nw + w];
@@ -211,17 +231,19 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
     }
 }
 
-__global__ void k_canon(const uint8_t* mem, const uint32_t* sc, uint32_t np, int n, uint8_t* out) {
+// slot_env (nullable): the output row of each console slot
+__global__ void k_canon(const uint8_t* mem, const uint32_t* sc, uint32_t np, int n, const int32_t* slot_env, uint8_t* out) {
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < (uint32_t)n) canon_lane(mem, sc, np, e, out + (size_t)e * MH_CANON_BYTES);
+    if (e < (uint32_t)n) canon_lane(mem, sc, np, e, out + (size_t)(slot_env ? slot_env[e] : (int32_t)e) * MH_CANON_BYTES);
 }
 
-// Lane-interleaved rows -> env-major (n x rows). Threads: x = env, y = row.
-__global__ void k_rows_out(const uint8_t* src, uint32_t np, int n, uint32_t rows, uint8_t* out) {
+// Lane-interleaved rows -> env-major (n x rows), slot e to row slot_env[e] (identity if null). Threads: x = slot,
+// y = row.
+__global__ void k_rows_out(const uint8_t* src, uint32_t np, int n, uint32_t rows, const int32_t* slot_env, uint8_t* out) {
     const uint32_t e = blockIdx.x * 64 + (threadIdx.x & 63);
     const uint32_t r = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (e >= (uint32_t)n || r >= rows) return;
-    out[(size_t)e * rows + r] = src[(size_t)r * np + e];
+    out[(size_t)(slot_env ? slot_env[e] : (int32_t)e) * rows + r] = src[(size_t)r * np + e];
 }
 
 // Frame buffer (4-pixel words, lane-interleaved) -> env-major 240x256 frames. Threads: x = env, y = word.
@@ -304,8 +326,14 @@ static bool load_cart(const uint8_t* d, int64_t n, std::vector<uint8_t>& img, ui
 
 }  // namespace
 
+// compute units of a device (the emulator kernels' launch shape depends on it)
+static int device_cus(int device) {
+    hipDeviceProp_t prop;
+    return hipGetDeviceProperties(&prop, device) == hipSuccess ? prop.multiProcessorCount : 0;
+}
+
 struct MhEnv {
-    int n = 0, K = 4, nl = 0, nk = 1, nc = 0, device = 0;
+    int n = 0, K = 4, nl = 0, nk = 1, nc = 0, device = 0, cus = 0;
     uint32_t np = 0, nlp = 0, ncp = 0;
     Cfg cfg{};
     DevBufs B;
@@ -320,6 +348,7 @@ struct MhEnv {
     int64_t *x0 = nullptr, *t0 = nullptr;
     uint8_t *cmem = nullptr, *cgray = nullptr, *cobs = nullptr, *cboot = nullptr;
     uint8_t* key_bank = nullptr;     // CHR bank of each (level, ROM) key
+    int32_t* slot_env = nullptr;     // env of each console slot (slots grouped by (level, ROM) key)
     uint32_t *csc = nullptr;
     uint8_t* csnap_mem = nullptr;    // 2 snapshot slots of the cache consoles
     uint32_t* csnap_sc = nullptr;
@@ -341,11 +370,11 @@ struct MhEnv {
         return ResetArgs{n, np, cfg, nk, ncp, mem, sc, ev, cmem, csc, cx, ct, clives, cdraws, cboot,
                          cframes, cinstr, cff, cbad, all};
     }
-    StackArgs stack_args(int mode) const { return StackArgs{n, np, K, obs, fin, fresh, ev, cobs, mode}; }
+    StackArgs stack_args(int mode) const { return StackArgs{n, np, K, obs, fin, slot_env, fresh, ev, cobs, mode}; }
 };
 
 struct MhRaw {
-    int n = 0, device = 0;
+    int n = 0, device = 0, cus = 0;
     uint32_t np = 0;
     DevBufs B;
     RomArgs R{};
@@ -398,7 +427,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     MhEnv* h = new MhEnv();
     auto fail = [&]() -> MhEnv* { delete h; return nullptr; };
     bool good = true;
-    h->n = n; h->K = frame_stack; h->device = device; h->np = pad64(n);
+    h->n = n; h->K = frame_stack; h->device = device; h->np = pad64(n); h->cus = device_cus(device);
     h->cfg = Cfg{skip, max_steps, noop_max, maxpool ? 1 : 0, sticky};
     // distinct (level, ROM) keys in order of first appearance (levels: fastmario.cpp:584-593); a key has its
     // own boot state and reset-cache entries
@@ -418,6 +447,21 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
         env_level[i] = li;
     }
     h->nl = (int)lv.size() / 3; h->nlp = pad64(h->nl);
+    // Console slots grouped by key, ordered by (world, stage, area, ROM), envs of a key in index order: a wave then
+    // holds envs of one level (one game code path) wherever the batch mixes levels, so its lanes diverge less.
+    // State lives in slot order; actions, outputs, RAM and state dumps stay in env order (slot_env).
+    std::vector<int32_t> slot_env(h->np, 0), env_slot(n);
+    {
+        std::vector<int> order(n);
+        for (int i = 0; i < n; i++) order[i] = i;
+        auto key_of = [&](int i) {
+            const int k = env_level[i];
+            return std::make_tuple(lv[3 * k], lv[3 * k + 1], lv[3 * k + 2], (int)key_bank[k], i);
+        };
+        std::sort(order.begin(), order.end(), [&](int a, int b) { return key_of(a) < key_of(b); });
+        for (int s = 0; s < n; s++) { slot_env[s] = order[s]; env_slot[order[s]] = s; }
+        for (uint32_t s = (uint32_t)n; s < h->np; s++) slot_env[s] = (int32_t)s;   // padding slots: never used
+    }
     h->nk = noop_max + 1; h->nc = h->nl * h->nk; h->ncp = pad64(h->nc);
     auto& B = h->B;
     uint8_t* d_rom = B.alloc<uint8_t>(img.size(), good);
@@ -425,6 +469,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     h->T = B.alloc<AreaTables>(1, good);
     int* d_levels = B.alloc<int>(lv.size(), good);
     h->key_bank = B.alloc<uint8_t>(key_bank.size(), good);
+    h->slot_env = B.alloc<int32_t>(h->np, good);
     h->mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->np, good);
     h->sc = B.alloc<uint32_t>((size_t)S_COUNT * h->np, good);
     h->ev = B.alloc<uint32_t>((size_t)E_COUNT * h->np, good);
@@ -456,7 +501,8 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     // per-env words: level, RNG, lives = -1 (reset() installs the real start state)
     std::vector<uint32_t> ev((size_t)E_COUNT * h->np, 0);
     for (int i = 0; i < n; i++) {
-        auto w = [&](int k) -> uint32_t& { return ev[(size_t)k * h->np + i]; };
+        const size_t slot = (size_t)env_slot[i];
+        auto w = [&](int k) -> uint32_t& { return ev[(size_t)k * h->np + slot]; };
         w(E_LEVEL) = (uint32_t)env_level[i];
         const uint64_t* r = rng + 6 * i;
         w(E_RNG_S3) = (uint32_t)(r[0] >> 32); w(E_RNG_S2) = (uint32_t)r[0];
@@ -468,6 +514,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     }
     if (!ok(hipMemcpy(d_rom, img.data(), img.size(), hipMemcpyHostToDevice), "upload rom") ||
         !ok(hipMemcpy(h->key_bank, key_bank.data(), key_bank.size(), hipMemcpyHostToDevice), "upload key banks") ||
+        !ok(hipMemcpy(h->slot_env, slot_env.data(), slot_env.size() * 4, hipMemcpyHostToDevice), "upload slot map") ||
         !ok(hipMemcpy(d_lut, lut, 256, hipMemcpyHostToDevice), "upload lut") ||
         !ok(hipMemcpy(h->T, &T, sizeof(T), hipMemcpyHostToDevice), "upload tables") ||
         !ok(hipMemcpy(d_levels, lv.data(), lv.size() * sizeof(int), hipMemcpyHostToDevice), "upload levels") ||
@@ -478,14 +525,16 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     // boot every level, build the reset cache
     BootArgs ba{h->R, h->nl, h->nlp, d_levels, h->key_bank, h->boot_mem, h->boot_sc, h->boot_gray, h->x0, h->t0, d_err};
-    hipLaunchKernelGGL(k_boot, emu_grid(h->nl), dim3(EMU_THREADS), 0, 0, ba);
+    const EmuLaunch lb = emu_launch(h->nl, h->cus);
+    hipLaunchKernelGGL(k_boot, lb.grid, lb.block, 0, 0, ba);
     if (!ok(hipGetLastError(), "k_boot launch")) return fail();
     SmallObsArgs so{h->boot_gray, h->nlp, nullptr, nullptr, 1, h->boot_obs, h->nl, h->T};
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nl), dim3(256), 0, 0, so);
     CacheArgs ca{h->R, h->cfg, h->key_bank, h->nl, h->nk, h->nc, h->nlp, h->ncp, h->boot_mem, h->boot_sc, h->x0, h->t0,
                  h->cmem, h->csc, h->cgray, h->csnap_mem, h->csnap_sc, h->cx, h->ct, h->clives, h->cdraws, h->cboot,
                  h->cframes, h->cinstr, h->cff, h->cbad};
-    hipLaunchKernelGGL(k_cache, emu_grid(h->nc), dim3(EMU_THREADS), 0, 0, ca);
+    const EmuLaunch lc = emu_launch(h->nc, h->cus);
+    hipLaunchKernelGGL(k_cache, lc.grid, lc.block, 0, 0, ca);
     if (!ok(hipGetLastError(), "k_cache launch")) return fail();
     SmallObsArgs co{h->cgray, h->ncp, h->cboot, h->boot_obs, h->nk, h->cobs, h->nc, h->T};
     hipLaunchKernelGGL(k_small_obs, dim3((OBS_PIX + 255) / 256, h->nc), dim3(256), 0, 0, co);
@@ -559,8 +608,9 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     if (mark(h, s, 0)) return -1;
     StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->ev, h->gray, h->snap_mem, h->snap_sc, d_actions,
-                h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len, h->key_bank};
-    hipLaunchKernelGGL(k_step, emu_grid(h->n), dim3(EMU_THREADS), 0, s, sa);
+                h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len, h->key_bank, h->slot_env};
+    const EmuLaunch ls = emu_launch(h->n, h->cus);
+    hipLaunchKernelGGL(k_step, ls.grid, ls.block, 0, s, sa);
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
     ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
@@ -641,19 +691,21 @@ int mh_reemulations(MhEnv* h, int64_t* out) {
 int mh_env_ram(MhEnv* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
     hipLaunchKernelGGL(k_rows_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n,
-                       2048u, d_out);
+                       2048u, (const int32_t*)h->slot_env, d_out);
     CK(hipGetLastError());
     return 0;
 }
 int mh_env_canon(MhEnv* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
-    hipLaunchKernelGGL(k_canon, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, h->mem, h->sc, h->np, h->n, d_out);
+    hipLaunchKernelGGL(k_canon, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, h->mem, h->sc, h->np, h->n,
+                       (const int32_t*)h->slot_env, d_out);
     CK(hipGetLastError());
     return 0;
 }
 int mh_level_canon(MhEnv* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
-    hipLaunchKernelGGL(k_canon, dim3(h->nlp / 64), dim3(64), 0, (hipStream_t)stream, h->boot_mem, h->boot_sc, h->nlp, h->nl, d_out);
+    hipLaunchKernelGGL(k_canon, dim3(h->nlp / 64), dim3(64), 0, (hipStream_t)stream, h->boot_mem, h->boot_sc, h->nlp, h->nl,
+                       nullptr, d_out);
     CK(hipGetLastError());
     return 0;
 }
@@ -680,7 +732,7 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     CKN(hipSetDevice(device));
     MhRaw* h = new MhRaw();
     bool good = true;
-    h->n = n; h->np = pad64(n); h->device = device;
+    h->n = n; h->np = pad64(n); h->device = device; h->cus = device_cus(device);
     auto& B = h->B;
     uint8_t* d_rom = B.alloc<uint8_t>(0xa000, good);
     uint8_t* d_lut = B.alloc<uint8_t>(256, good);
@@ -701,21 +753,23 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     h->R.nt_bits = 0;
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
     RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, h->ff, 1};
-    hipLaunchKernelGGL(k_raw, emu_grid(h->n), dim3(EMU_THREADS), 0, 0, ra);
+    const EmuLaunch lr = emu_launch(h->n, h->cus);
+    hipLaunchKernelGGL(k_raw, lr.grid, lr.block, 0, 0, ra);
     if (!ok(hipDeviceSynchronize(), "raw power-on")) { delete h; return nullptr; }
     return h;
 }
 int mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream) {
     if (!h || !d_buttons) return -1;
     RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, d_buttons, render, h->bad, h->instr, h->ff, 0};
-    hipLaunchKernelGGL(k_raw, emu_grid(h->n), dim3(EMU_THREADS), 0, (hipStream_t)stream, ra);
+    const EmuLaunch lr = emu_launch(h->n, h->cus);
+    hipLaunchKernelGGL(k_raw, lr.grid, lr.block, 0, (hipStream_t)stream, ra);
     CK(hipGetLastError());
     return 0;
 }
 int mh_raw_ram(MhRaw* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
     hipLaunchKernelGGL(k_rows_out, dim3(h->np / 64, 2048 / 4), dim3(256), 0, (hipStream_t)stream, h->mem, h->np, h->n,
-                       2048u, d_out);
+                       2048u, nullptr, d_out);
     CK(hipGetLastError());
     return 0;
 }
@@ -735,7 +789,8 @@ int mh_raw_screen_rgb(MhRaw* h, const uint8_t* d_rgb64, uint8_t* d_out, void* st
 }
 int mh_raw_canon(MhRaw* h, uint8_t* d_out, void* stream) {
     if (!h || !d_out) return -1;
-    hipLaunchKernelGGL(k_canon, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, h->mem, h->sc, h->np, h->n, d_out);
+    hipLaunchKernelGGL(k_canon, dim3(h->np / 64), dim3(64), 0, (hipStream_t)stream, h->mem, h->sc, h->np, h->n, nullptr,
+                       d_out);
     CK(hipGetLastError());
     return 0;
 }

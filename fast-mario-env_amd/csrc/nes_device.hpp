@@ -18,19 +18,29 @@
 namespace mh {
 
 constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
-// Emulator launch shape: a 64-lane wave carries ENVS_PER_WAVE envs, each on two twin lanes (l and l + 32),
-// and a block holds WAVES_PER_BLOCK waves sharing one LDS copy of the cartridge. 32768 envs in full waves
-// are 512 waves, which leave half of the 1024 SIMDs of the chip empty; half-full waves put a wave on every
-// SIMD and halve the lanes whose divergent paths one wave has to walk. The twins run the same console in
-// lockstep, which costs the wave nothing, and split the renderer's pixel groups between them.
-constexpr int ENVS_PER_WAVE = 32;
-constexpr int WAVES_PER_BLOCK = 4;
-constexpr int LDS_LANES = ENVS_PER_WAVE * WAVES_PER_BLOCK;  // env slots sharing one block's per-lane LDS buffers
+// Emulator launch shape. Each env runs on LANES_PER_ENV lanes of a 64-lane wave (its parts: lanes
+// s, s + ENVS_PER_WAVE, ...), so a wave carries ENVS_PER_WAVE = 64 / LANES_PER_ENV envs, and a block of
+// WAVES_PER_BLOCK waves holds LDS_LANES = 128 env slots sharing one LDS copy of the cartridge. The parts run
+// the same console in lockstep, which costs the wave nothing (an instruction issues once for all its lanes),
+// and split the renderer's pixel groups and the sprite evaluation between them. Fewer envs per wave means
+// fewer divergent instruction streams per wave; with 2 parts, 32768 envs are 1024 waves, one per SIMD; with
+// 4 parts they are 2048 waves in blocks of 8, two per SIMD, so one wave issues while the other waits.
+#ifndef MH_LANES_PER_ENV
+#define MH_LANES_PER_ENV 4
+#endif
+constexpr int LANES_PER_ENV = MH_LANES_PER_ENV;
+static_assert(LANES_PER_ENV == 2 || LANES_PER_ENV == 4, "an env runs on 2 or 4 lanes");
+constexpr int ENVS_PER_WAVE = 64 / LANES_PER_ENV;
+constexpr int LDS_LANES = 128;                                  // env slots sharing one block's per-lane LDS buffers
+constexpr int WAVES_PER_BLOCK = LDS_LANES / ENVS_PER_WAVE;
+constexpr int EMU_WAVES_PER_SIMD = WAVES_PER_BLOCK / 4;        // one block per CU (its LDS), 4 SIMDs per CU
+// a wave's ballot bit of every part of the env in its lane 0 (shifted by the env's slot in the wave)
+constexpr uint64_t PART_LANES = LANES_PER_ENV == 2 ? 0x0000000100000001ull : 0x0001000100010001ull;
 constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
 constexpr int LDS_BG_WORDS = 20;                   // words per lane: two name-table rows (64 tiles) + their attributes
 constexpr int LDS_BG_ATTR = 64;                    // byte offset of the attribute bytes in the tile row
 constexpr int LDS_OAM_WORDS = 64;                  // words per lane: OAM (sprite i = word i: y, tile, attr, x)
-constexpr int LDS_XCHG_WORDS = 2;                 // words per env slot: the twins' halves of the sprite-range mask
+constexpr int LDS_XCHG_WORDS = LANES_PER_ENV;     // words per env slot: the parts' pieces of the sprite-range mask
 constexpr int LDS_GP_REGION = LDS_GP_WORDS + LDS_BG_WORDS + LDS_OAM_WORDS + LDS_XCHG_WORDS;   // palette, tile row, OAM, exchange
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
 // Render lines per frame slice (a power of two). A wave runs its lanes' CPUs to the end of a group of
@@ -49,8 +59,8 @@ __device__ __forceinline__ size_t vram_word_offset(uint32_t np, uint32_t e, uint
 enum : uint8_t { FN = 0x01, FV = 0x02, FONE = 0x04, FB = 0x08, FD = 0x10, FI = 0x20, FZ = 0x40, FC = 0x80 };
 // Error flags or-ed into a console's bad-op counter (every parity check requires a zero count):
 // ERR_HACK_LIMIT  the env layer's busy-state loop hit its frame limit;
-// ERR_TWIN        a sprite evaluation ran on one twin lane without the other, so the sprite-range half it
-//                 read from its partner's exchange word was stale.
+// ERR_TWIN        a sprite evaluation ran on some of an env's lanes without the others, so the pieces of the
+//                 sprite-range mask it read from their exchange words were stale.
 constexpr uint32_t ERR_HACK_LIMIT = 1u << 24, ERR_TWIN = 1u << 25, ERR_FLAGS = ERR_HACK_LIMIT | ERR_TWIN;
 enum : uint8_t { ST_PRE = 0, ST_RENDER = 1, ST_POST = 2, ST_VBLANK = 3 };
 
@@ -205,8 +215,8 @@ struct Console {
     uint8_t* gray;           // GRAY slot + 4 e: pixels 4i..4i+3 in the 32-bit word at gray + 4 i np
     const uint8_t* lut;      // palette value -> gray (LDS, 256 entries)
     bool render;
-    uint8_t twin;            // 0 or 1: which of the env's two lanes this is (both run the console; the
-                             // renderer splits the 8-pixel groups between them)
+    uint8_t part;            // which of the env's LANES_PER_ENV lanes this is (all run the console; the
+                             // renderer and the sprite evaluation split their work between them)
     // ---- CPU
     uint16_t pc;
     uint8_t sp, a, x, y, p, zero_skip;
@@ -508,20 +518,29 @@ struct Console {
         // in-range sprites as a 64-bit mask (bit i: pend_line - y_i in [0, h)), from index oam_addr / 4 on;
         // the list is its first (at most 8) set bits, entries past the count keep their old values
         const uint32_t h = long_spr ? 16u : 8u;
-        // The env's twin lanes each test one half of OAM (twin t: sprites 32 t .. 32 t + 31) into exchange word
-        // t of the env, then both read both words. The wave barrier is a convergence point: every lane active
-        // here has stored its word before any lane loads (a wave's LDS accesses complete in order).
-        if (!((__ballot(1) >> (__lane_id() ^ 32u)) & 1ull)) bad_ops |= ERR_TWIN;   // the partner must be here
-        uint32_t half = 0;
+        // The env's parts each test 64 / LANES_PER_ENV sprites (part q: sprites NS q .. NS q + NS - 1) into
+        // exchange word q of the env, then every part reads every word. The wave barrier is a convergence
+        // point: every lane active here has stored its word before any lane loads (a wave's LDS accesses
+        // complete in order). All parts must be here together, or a part would read a stale word: a part
+        // missing from the wave's active lanes sets ERR_TWIN.
+        constexpr int NS = 64 / LANES_PER_ENV;
+        const uint32_t in_wave = __lane_id() & (ENVS_PER_WAVE - 1);
+        if (((__ballot(1) >> in_wave) & PART_LANES) != PART_LANES) bad_ops |= ERR_TWIN;
+        uint32_t piece = 0;
 #pragma unroll
-        for (int i = 0; i < 32; i++)
-            half |= ((uint32_t)(pend_line - (int)(oam_sprite(32 * twin + i) & 0xffu)) < h ? 1u : 0u) << i;
+        for (int i = 0; i < NS; i++)
+            piece |= ((uint32_t)(pend_line - (int)(oam_sprite(NS * part + i) & 0xffu)) < h ? 1u : 0u) << i;
         uint32_t* const xw = lds_oam + LDS_OAM_WORDS * LDS_LANES;
-        xw[twin * LDS_LANES] = half;
+        xw[part * LDS_LANES] = piece;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        uint32_t mlo = xw[0], mhi = xw[LDS_LANES];
+        uint32_t mlo, mhi;
+        if (LANES_PER_ENV == 2) {
+            mlo = xw[0]; mhi = xw[LDS_LANES];
+        } else {
+            mlo = xw[0] | xw[LDS_LANES] << 16; mhi = xw[2 * LDS_LANES] | xw[3 * LDS_LANES] << 16;
+        }
         const int i0 = oam_addr >> 2;
         if (i0 < 32) mlo &= ~0u << i0;
         else { mlo = 0; mhi &= ~0u << (i0 - 32); }
@@ -773,22 +792,23 @@ struct Console {
         // pixel bb of a group takes the second tile's attribute when f + bb >= 8: bytes bb >= 8 - f
         const uint64_t second = f ? (~0ull << (8 * (8 - f))) : 0ull;
         const uint32_t tsel0 = (uint32_t)second & 0x04040404u, tsel1 = (uint32_t)(second >> 32) & 0x04040404u;
-        // The two twin lanes of the env split the groups in pairs: this lane draws groups 4m + 2 twin and
-        // 4m + 2 twin + 1 (a fixed owner per group, so a group cut by a catch-up boundary is finished by the
+        // The env's parts split the groups in pairs: part q draws groups S m + 2 q and S m + 2 q + 1, S = 2 x
+        // LANES_PER_ENV (a fixed owner per group, so a group cut by a catch-up boundary is finished by the
         // lane that started it). One iteration draws one pair (p, p + 1) from tiles p, p + 1 and p + 2, and
         // fetches the planes of the next pair's three tiles, the indices of the pair after it and the next
         // pair's sprite bytes, which are used one iteration later, so no LDS round trip sits between two
         // pairs. The fetches are unconditional (indices clamped to the buffers; a layer that is off masks
         // its values afterwards), so every iteration issues the same LDS operations. A group of a pair that
         // lies outside [x0, x1) gets an empty pixel mask and is not written.
+        constexpr int S = 2 * LANES_PER_ENV;   // groups between two pairs of one part
         auto tile_of = [&](int k) { return bg_tile_of(k < 32 ? k : 32, bc0, bcy); };
-        int pg = (g0 & ~3) + 2 * (int)twin;
-        if (pg + 1 < g0) pg += 4;
+        int pg = (g0 & ~(S - 1)) + 2 * (int)part;
+        if (pg + 1 < g0) pg += S;
         uint32_t alo, ahi, agt, blo, bhi, bgt, clo, chi, cgt;
         bg_planes(tile_of(pg), fy, bgpal, alo, ahi, agt);
         bg_planes(tile_of(pg + 1), fy, bgpal, blo, bhi, bgt);
         bg_planes(tile_of(pg + 2), fy, bgpal, clo, chi, cgt);
-        uint32_t nxa = tile_of(pg + 4), nxb = tile_of(pg + 5), nxc = tile_of(pg + 6);
+        uint32_t nxa = tile_of(pg + S), nxb = tile_of(pg + S + 1), nxc = tile_of(pg + S + 2);
         if (!show_bg) { alo = ahi = blo = bhi = clo = chi = 0; agt = bgt = cgt = ubg; }
         const int ws0 = 2 * pg < 60 ? 2 * pg : 60;
         uint32_t s0 = lds_sp[ws0 * LDS_LANES], s1 = lds_sp[(ws0 + 1) * LDS_LANES];   // the pair's sprite bytes
@@ -840,13 +860,13 @@ struct Console {
                 }
             }
         };
-        for (; pg < g1; pg += 4) {
+        for (; pg < g1; pg += S) {
             uint32_t dlo, dhi, dgt, elo, ehi, egt, flo, fhi, fgt;
             bg_planes(nxa, fy, bgpal, dlo, dhi, dgt);
             bg_planes(nxb, fy, bgpal, elo, ehi, egt);
             bg_planes(nxc, fy, bgpal, flo, fhi, fgt);
-            const uint32_t na = tile_of(pg + 8), nb = tile_of(pg + 9), nc = tile_of(pg + 10);
-            const int ws = 2 * pg + 8 < 60 ? 2 * pg + 8 : 60;
+            const uint32_t na = tile_of(pg + 2 * S), nb = tile_of(pg + 2 * S + 1), nc = tile_of(pg + 2 * S + 2);
+            const int ws = 2 * pg + 2 * S < 60 ? 2 * pg + 2 * S : 60;
             const uint32_t t0 = lds_sp[ws * LDS_LANES], t1 = lds_sp[(ws + 1) * LDS_LANES];
             const uint32_t t2 = lds_sp[(ws + 2) * LDS_LANES], t3 = lds_sp[(ws + 3) * LDS_LANES];
             uint32_t out0[2], out1[2];
@@ -856,7 +876,7 @@ struct Console {
             group_words(blo, bhi, bgt, clo, chi, cgt, s2, s3, ~0u, ~0u, out1);
             store_group(8 * pg, wp, out0);
             store_group(8 * pg + 8, wp + 2 * np, out1);
-            wp += 8 * np;
+            wp += 2 * S * np;
             alo = show_bg ? dlo : 0u; ahi = show_bg ? dhi : 0u; agt = show_bg ? dgt : ubg;
             blo = show_bg ? elo : 0u; bhi = show_bg ? ehi : 0u; bgt = show_bg ? egt : ubg;
             clo = show_bg ? flo : 0u; chi = show_bg ? fhi : 0u; cgt = show_bg ? fgt : ubg;
