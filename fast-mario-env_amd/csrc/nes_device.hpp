@@ -15,6 +15,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// an empty asm that makes the compiler hold x in a vector register at this point (the host build of this
+// code, tests/hostbuild, defines it with a host register constraint)
+#ifndef MH_REG_BARRIER
+#define MH_REG_BARRIER(x) asm volatile("" : "+v"(x))
+#endif
+
 namespace mh {
 
 constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
@@ -29,13 +35,15 @@ constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_
 #define MH_LANES_PER_ENV 4
 #endif
 constexpr int LANES_PER_ENV = MH_LANES_PER_ENV;
-static_assert(LANES_PER_ENV == 2 || LANES_PER_ENV == 4, "an env runs on 2 or 4 lanes");
+// (1 lane per env is the host build of this code, tests/hostbuild: one lane plays the whole wave of an env)
+static_assert(LANES_PER_ENV == 1 || LANES_PER_ENV == 2 || LANES_PER_ENV == 4, "an env runs on 1, 2 or 4 lanes");
 constexpr int ENVS_PER_WAVE = 64 / LANES_PER_ENV;
 constexpr int LDS_LANES = 128;                                  // env slots sharing one block's per-lane LDS buffers
 constexpr int WAVES_PER_BLOCK = LDS_LANES / ENVS_PER_WAVE;
 constexpr int EMU_WAVES_PER_SIMD = WAVES_PER_BLOCK / 4;        // one block per CU (its LDS), 4 SIMDs per CU
 // a wave's ballot bit of every part of the env in its lane 0 (shifted by the env's slot in the wave)
-constexpr uint64_t PART_LANES = LANES_PER_ENV == 2 ? 0x0000000100000001ull : 0x0001000100010001ull;
+constexpr uint64_t PART_LANES = LANES_PER_ENV == 1 ? 1ull : LANES_PER_ENV == 2 ? 0x0000000100000001ull
+                                                                            : 0x0001000100010001ull;
 constexpr int LDS_SP_WORDS = 64, LDS_GP_WORDS = 8; // words per lane: sprite line (256 B), gray palette (32 B)
 constexpr int LDS_BG_WORDS = 20;                   // words per lane: two name-table rows (64 tiles) + their attributes
 constexpr int LDS_BG_ATTR = 64;                    // byte offset of the attribute bytes in the tile row
@@ -526,20 +534,25 @@ struct Console {
         constexpr int NS = 64 / LANES_PER_ENV;
         const uint32_t in_wave = __lane_id() & (ENVS_PER_WAVE - 1);
         if (((__ballot(1) >> in_wave) & PART_LANES) != PART_LANES) bad_ops |= ERR_TWIN;
-        uint32_t piece = 0;
+        auto in_range = [&](int i) { return ((uint32_t)(pend_line - (int)(oam_sprite(i) & 0xffu)) < h ? 1u : 0u); };
+        uint32_t mlo = 0, mhi = 0;
+        if constexpr (LANES_PER_ENV == 1) {
 #pragma unroll
-        for (int i = 0; i < NS; i++)
-            piece |= ((uint32_t)(pend_line - (int)(oam_sprite(NS * part + i) & 0xffu)) < h ? 1u : 0u) << i;
-        uint32_t* const xw = lds_oam + LDS_OAM_WORDS * LDS_LANES;
-        xw[part * LDS_LANES] = piece;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        uint32_t mlo, mhi;
-        if (LANES_PER_ENV == 2) {
-            mlo = xw[0]; mhi = xw[LDS_LANES];
+            for (int i = 0; i < 32; i++) { mlo |= in_range(i) << i; mhi |= in_range(32 + i) << i; }
         } else {
-            mlo = xw[0] | xw[LDS_LANES] << 16; mhi = xw[2 * LDS_LANES] | xw[3 * LDS_LANES] << 16;
+            uint32_t piece = 0;
+#pragma unroll
+            for (int i = 0; i < NS; i++) piece |= in_range(NS * part + i) << i;
+            uint32_t* const xw = lds_oam + LDS_OAM_WORDS * LDS_LANES;
+            xw[part * LDS_LANES] = piece;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (LANES_PER_ENV == 2) {
+                mlo = xw[0]; mhi = xw[LDS_LANES];
+            } else {
+                mlo = xw[0] | xw[LDS_LANES] << 16; mhi = xw[2 * LDS_LANES] | xw[3 * LDS_LANES] << 16;
+            }
         }
         const int i0 = oam_addr >> 2;
         if (i0 < 32) mlo &= ~0u << i0;
@@ -626,7 +639,7 @@ struct Console {
     }
 
     // an optimization barrier: the value is materialized in a register here
-    __device__ __forceinline__ static void in_register(uint32_t& x) { asm volatile("" : "+v"(x)); }
+    __device__ __forceinline__ static void in_register(uint32_t& x) { MH_REG_BARRIER(x); }
     // bytes of the 8-byte value hi:lo picked by the selector bytes of sel (each 0..7)
     __device__ __forceinline__ static uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
         return __builtin_amdgcn_perm(hi, lo, sel);
