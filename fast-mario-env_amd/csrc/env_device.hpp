@@ -295,7 +295,7 @@ struct Stepper {
                 render = true;
                 slot = ((K - 1 - rf) & 1) ? gray1 : gray0;
             }
-            c.joy_buttons0 = buttons;
+            c.set_buttons0(buttons);
             c.render = render;
             c.gray = slot;
             c.frame();

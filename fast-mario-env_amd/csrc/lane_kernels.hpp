@@ -308,7 +308,7 @@ __device__ inline void boot_lane(const BootArgs& A, const LaneCtx& x, int l) {
     attach(c, x, A.mem, A.nlp, (uint32_t)l, A.key_bank[l]);
     c.gray = A.gray + gray_lane_offset(l); c.render = true;
     c.power_on();
-    auto fr = [&](uint8_t b) { c.joy_buttons0 = b; c.frame(); };
+    auto fr = [&](uint8_t b) { c.set_buttons0(b); c.frame(); };
     const int w = A.levels[3 * l], s = A.levels[3 * l + 1], ar = A.levels[3 * l + 2];
     fr(8); fr(0);
     int guard = 0;
@@ -438,7 +438,7 @@ __device__ inline void raw_lane(const RawArgs& A, const LaneCtx& x, uint32_t e) 
         c.power_on();
     } else {
         c.load(A.sc, e);
-        c.joy_buttons0 = A.buttons[e];
+        c.set_buttons0(A.buttons[e]);
         c.render = A.render != 0;
         c.frame();
     }

@@ -64,6 +64,9 @@ constexpr int GRAY_PIX = 256 * 240;
 __device__ __forceinline__ size_t vram_word_offset(uint32_t np, uint32_t e, uint32_t w) {
     return (size_t)ROW_VRAM * np + ((size_t)w * np + e) * 4;
 }
+// Console::ppu_flags bits: PPUMASK (show / hide-edge, bits 0-3) and PPUCTRL (bits 4-8) settings
+enum : uint32_t { PF_SHOW_BG = 1, PF_SHOW_SPR = 2, PF_HIDE_EDGE_BG = 4, PF_HIDE_EDGE_SPR = 8, PF_LONG_SPR = 16,
+                  PF_NMI_EN = 32, PF_BG_PAGE = 64, PF_SPR_PAGE = 128, PF_INC32 = 256 };
 enum : uint8_t { FN = 0x01, FV = 0x02, FONE = 0x04, FB = 0x08, FD = 0x10, FI = 0x20, FZ = 0x40, FC = 0x80 };
 // Error flags or-ed into a console's bad-op counter (every parity check requires a zero count):
 // ERR_HACK_LIMIT  the env layer's busy-state loop hit its frame limit;
@@ -225,35 +228,45 @@ struct Console {
     bool render;
     uint8_t part;            // which of the env's LANES_PER_ENV lanes this is (all run the console; the
                              // renderer and the sprite evaluation split their work between them)
+    // Small fields share 32-bit words as bitfields (8 or 16 bits wide, so they wrap as the byte and
+    // half-word types they stand for): the compiler keeps a word in one register instead of one per
+    // field. Fewer live registers mean fewer spills, and fewer register copies where the paths of
+    // the frame loop join.
     // ---- CPU
     uint16_t pc;
-    uint8_t sp, a, x, y, p, zero_skip;
+    uint32_t a : 8, x : 8, y : 8, sp : 8;
+    uint8_t p;
     int32_t exec_at, ppu_calls, nmi_thresh;  // relative to the current frame start
     uint32_t iter_lo;                        // low word of the iteration count at the frame start
     uint32_t iter_hi;
     int32_t cur, skip;
     // ---- joypads
-    // two ports as separate scalars: a dynamically indexed array would put the object in scratch
-    uint8_t joy_strobe0, joy_strobe1, joy_buttons0, joy_buttons1, joy_bits0, joy_bits1;
+    // both ports in one word (buttons 0 | buttons 1 << 8 | shift register 0 << 16 | shift register 1 << 24);
+    // their strobes are bits 0 and 1 of joy_strobe (below)
+    uint32_t joy;
     // ---- PPU
-    uint8_t pstate, even, vblank, s0hit, first_write, data_buffer, oam_addr, fine_x;
-    uint8_t show_bg, show_spr, hide_edge_bg, hide_edge_spr, long_spr, nmi_en, bg_page, spr_page;
-    uint8_t nsl;
+    uint32_t pstate : 8, even : 8, vblank : 8, s0hit : 8;
+    uint32_t first_write : 8, joy_strobe : 8, zero_skip : 8, pal_dirty : 8;   // zero_skip: CPU, pal_dirty: derived
+    uint32_t fine_x : 8, oam_addr : 8, data_buffer : 8, nsl : 8;
+    // ppu_flags: the PPUCTRL / PPUMASK settings as PF_* bits; bg_key: name table and coarse y (v bits 5-11)
+    // of the tile row held in LDS (-1: none)
+    uint32_t ppu_flags : 16;
+    int32_t bg_key : 16;
     uint32_t sl_lo, sl_hi;                   // sprite list: 8 indices packed in two words
     int32_t pcyc, scanline;
-    uint16_t v, t, inc;
+    uint32_t v : 16, t : 16;
     // ---- counters
     uint32_t bad_ops, instructions;          // instructions: retired, poll-loop fast-forwards included
     uint32_t ff_instructions;                // of those, the ones poll_skip fast-forwarded without executing
     // ---- derived state (not part of the machine state)
-    int32_t pend_line;       // scanline of a sprite evaluation not yet materialized (-1: the list is current)
-    int32_t sp_line;         // scanline the LDS sprite line buffer holds (-1: invalid)
-    bool pal_dirty;          // the LDS gray palette must be rebuilt
+    // pend_line: scanline of a sprite evaluation not yet materialized (-1: the list is current);
+    // sp_line: scanline the LDS sprite line buffer holds (-1: invalid); pal_dirty (above): the LDS gray
+    // palette must be rebuilt
+    int32_t pend_line : 16, sp_line : 16;
     uint32_t* lds_sp;        // per-lane sprite line buffer: word (x / 4) of this lane at lds_sp[(x / 4) * LDS_LANES]
     uint32_t* lds_gp;        // per-lane gray palette: word (i / 4) at lds_gp[(i / 4) * LDS_LANES]
     uint32_t* lds_bg;        // per-lane background tile row (same word stride), valid for v's bits 5-11 == bg_key
     uint32_t* lds_oam;       // per-lane OAM (same word stride): the live copy between load()/power_on() and store()
-    int32_t bg_key;          // name table and coarse y (v bits 5-11) of the tile row held (-1: none)
 
     // ------------------------------------------------------------ interleaved memory
     __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mem[(size_t)__umul24(row, np)]; }
@@ -291,6 +304,18 @@ struct Console {
         else sl_hi = (sl_hi & ~(0xffu << (8 * (k - 4)))) | ((uint32_t)i << (8 * (k - 4)));
     }
     __device__ __forceinline__ uint8_t prg(uint16_t a) const { return cart.prg[a & 0x7fff]; }
+    // PPUCTRL / PPUMASK settings (0 or 1; inc(): the VRAM address increment, 1 or 32)
+    __device__ __forceinline__ uint32_t show_bg() const { return ppu_flags & 1u; }
+    __device__ __forceinline__ uint32_t show_spr() const { return (ppu_flags >> 1) & 1u; }
+    __device__ __forceinline__ uint32_t hide_edge_bg() const { return (ppu_flags >> 2) & 1u; }
+    __device__ __forceinline__ uint32_t hide_edge_spr() const { return (ppu_flags >> 3) & 1u; }
+    __device__ __forceinline__ uint32_t long_spr() const { return (ppu_flags >> 4) & 1u; }
+    __device__ __forceinline__ uint32_t nmi_en() const { return (ppu_flags >> 5) & 1u; }
+    __device__ __forceinline__ uint32_t bg_page() const { return (ppu_flags >> 6) & 1u; }
+    __device__ __forceinline__ uint32_t spr_page() const { return (ppu_flags >> 7) & 1u; }
+    __device__ __forceinline__ uint16_t inc() const { return (ppu_flags & PF_INC32) ? 32 : 1; }
+    // joypad port 0's buttons for the next frames (the env layer's action)
+    __device__ __forceinline__ void set_buttons0(uint8_t b) { joy = (joy & ~0xffu) | b; }
 
     // ------------------------------------------------------------ state in / out
     __device__ void load(const uint32_t* sc, uint32_t e) {
@@ -300,19 +325,20 @@ struct Console {
         ppu_calls = 0;
         pc = (uint16_t)w(S_PC); sp = (uint8_t)w(S_SP); a = (uint8_t)w(S_A); x = (uint8_t)w(S_X);
         y = (uint8_t)w(S_Y); p = (uint8_t)w(S_P); zero_skip = (uint8_t)w(S_ZERO_SKIP);
-        joy_strobe0 = (uint8_t)w(S_JOY_STROBE0); joy_strobe1 = (uint8_t)w(S_JOY_STROBE1);
-        joy_buttons0 = (uint8_t)w(S_JOY_BUTTONS0); joy_buttons1 = (uint8_t)w(S_JOY_BUTTONS1);
-        joy_bits0 = (uint8_t)w(S_JOY_BITS0); joy_bits1 = (uint8_t)w(S_JOY_BITS1);
+        joy_strobe = (uint8_t)((w(S_JOY_STROBE0) & 1u) | (w(S_JOY_STROBE1) & 1u) << 1);
+        joy = (w(S_JOY_BUTTONS0) & 0xffu) | (w(S_JOY_BUTTONS1) & 0xffu) << 8 | (w(S_JOY_BITS0) & 0xffu) << 16 |
+              (w(S_JOY_BITS1) & 0xffu) << 24;
         pstate = (uint8_t)w(S_PSTATE); even = (uint8_t)w(S_EVEN); vblank = (uint8_t)w(S_VBLANK);
         s0hit = (uint8_t)w(S_S0HIT); first_write = (uint8_t)w(S_FIRST_WRITE);
         data_buffer = (uint8_t)w(S_DATA_BUFFER); oam_addr = (uint8_t)w(S_OAM_ADDR); fine_x = (uint8_t)w(S_FINE_X);
-        show_bg = (uint8_t)w(S_SHOW_BG); show_spr = (uint8_t)w(S_SHOW_SPR);
-        hide_edge_bg = (uint8_t)w(S_HIDE_EDGE_BG); hide_edge_spr = (uint8_t)w(S_HIDE_EDGE_SPR);
-        long_spr = (uint8_t)w(S_LONG_SPR); nmi_en = (uint8_t)w(S_NMI_EN);
-        bg_page = (uint8_t)w(S_BG_PAGE); spr_page = (uint8_t)w(S_SPR_PAGE);
+        ppu_flags = (w(S_SHOW_BG) ? PF_SHOW_BG : 0u) | (w(S_SHOW_SPR) ? PF_SHOW_SPR : 0u) |
+                    (w(S_HIDE_EDGE_BG) ? PF_HIDE_EDGE_BG : 0u) | (w(S_HIDE_EDGE_SPR) ? PF_HIDE_EDGE_SPR : 0u) |
+                    (w(S_LONG_SPR) ? PF_LONG_SPR : 0u) | (w(S_NMI_EN) ? PF_NMI_EN : 0u) |
+                    (w(S_BG_PAGE) ? PF_BG_PAGE : 0u) | (w(S_SPR_PAGE) ? PF_SPR_PAGE : 0u) |
+                    (w(S_INC) == 32 ? PF_INC32 : 0u);
         nsl = (uint8_t)w(S_NSL); sl_lo = w(S_SL_LO); sl_hi = w(S_SL_HI);
         pcyc = (int32_t)w(S_PCYC); scanline = (int32_t)w(S_SCANLINE);
-        v = (uint16_t)w(S_V); t = (uint16_t)w(S_T); inc = (uint16_t)w(S_INC);
+        v = (uint16_t)w(S_V); t = (uint16_t)w(S_T);
         pend_line = -1; sp_line = -1; pal_dirty = true; bg_key = -1;
         for (int k = 0; k < LDS_OAM_WORDS; k++) {
             const uint32_t r = ROW_OAM + 4 * k;
@@ -330,16 +356,16 @@ struct Console {
         auto w = [&](int k, uint32_t val) { sc[(size_t)k * np + e] = val; };
         w(S_ITER_LO, iter_lo); w(S_ITER_HI, iter_hi); w(S_EXEC_REL, (uint32_t)exec_at);
         w(S_PC, pc); w(S_SP, sp); w(S_A, a); w(S_X, x); w(S_Y, y); w(S_P, p); w(S_ZERO_SKIP, zero_skip);
-        w(S_JOY_STROBE0, joy_strobe0); w(S_JOY_STROBE1, joy_strobe1);
-        w(S_JOY_BUTTONS0, joy_buttons0); w(S_JOY_BUTTONS1, joy_buttons1);
-        w(S_JOY_BITS0, joy_bits0); w(S_JOY_BITS1, joy_bits1);
+        w(S_JOY_STROBE0, joy_strobe & 1u); w(S_JOY_STROBE1, (joy_strobe >> 1) & 1u);
+        w(S_JOY_BUTTONS0, joy & 0xffu); w(S_JOY_BUTTONS1, (joy >> 8) & 0xffu);
+        w(S_JOY_BITS0, (joy >> 16) & 0xffu); w(S_JOY_BITS1, joy >> 24);
         w(S_PSTATE, pstate); w(S_EVEN, even); w(S_VBLANK, vblank); w(S_S0HIT, s0hit);
         w(S_FIRST_WRITE, first_write); w(S_DATA_BUFFER, data_buffer); w(S_OAM_ADDR, oam_addr);
-        w(S_FINE_X, fine_x); w(S_SHOW_BG, show_bg); w(S_SHOW_SPR, show_spr);
-        w(S_HIDE_EDGE_BG, hide_edge_bg); w(S_HIDE_EDGE_SPR, hide_edge_spr); w(S_LONG_SPR, long_spr);
-        w(S_NMI_EN, nmi_en); w(S_BG_PAGE, bg_page); w(S_SPR_PAGE, spr_page);
+        w(S_FINE_X, fine_x); w(S_SHOW_BG, show_bg()); w(S_SHOW_SPR, show_spr());
+        w(S_HIDE_EDGE_BG, hide_edge_bg()); w(S_HIDE_EDGE_SPR, hide_edge_spr()); w(S_LONG_SPR, long_spr());
+        w(S_NMI_EN, nmi_en()); w(S_BG_PAGE, bg_page()); w(S_SPR_PAGE, spr_page());
         w(S_NSL, nsl); w(S_SL_LO, sl_lo); w(S_SL_HI, sl_hi); w(S_PCYC, (uint32_t)pcyc);
-        w(S_SCANLINE, (uint32_t)scanline); w(S_V, v); w(S_T, t); w(S_INC, inc);
+        w(S_SCANLINE, (uint32_t)scanline); w(S_V, v); w(S_T, t); w(S_INC, inc());
     }
 
     // power-on: zeroed machine, then CPU and PPU reset (nes_core.hpp:123-147)
@@ -348,14 +374,13 @@ struct Console {
             if (r < ROW_VRAM || r >= ROW_VRAM + 2048) st(r, 0);
         for (uint32_t w = 0; w < 512; w++) *(uint32_t*)(vmem + (size_t)__umul24(w, 4 * np)) = 0;
         iter_lo = iter_hi = 0; exec_at = 0; ppu_calls = 0;
-        joy_strobe0 = joy_strobe1 = 1; joy_buttons0 = joy_buttons1 = 0; joy_bits0 = joy_bits1 = 0;
+        joy_strobe = 3; joy = 0;
         zero_skip = 0; a = x = y = 0; p = 0x34;
         pc = (uint16_t)(prg(0xfffc) | prg(0xfffd) << 8);
         sp = 0xfd;
-        s0hit = 0; data_buffer = 0; hide_edge_bg = hide_edge_spr = 0;
-        long_spr = 0; nmi_en = 0; vblank = 0; show_bg = 1; show_spr = 1; even = 1;
-        first_write = 1; bg_page = 0; spr_page = 0; v = 0; pcyc = 0; scanline = 0;
-        oam_addr = 0; fine_x = 0; t = 0; inc = 1; pstate = ST_PRE; nsl = 0; sl_lo = sl_hi = 0;
+        s0hit = 0; data_buffer = 0; vblank = 0; even = 1; ppu_flags = PF_SHOW_BG | PF_SHOW_SPR;
+        first_write = 1; v = 0; pcyc = 0; scanline = 0;
+        oam_addr = 0; fine_x = 0; t = 0; pstate = ST_PRE; nsl = 0; sl_lo = sl_hi = 0;
         pend_line = -1; sp_line = -1; pal_dirty = true; bg_key = -1;
         for (int k = 0; k < LDS_OAM_WORDS; k++) lds_oam[k * LDS_LANES] = 0;
         nmi_threshold();
@@ -421,31 +446,30 @@ struct Console {
             sp_line = -1;
             return;
         }
-        if (ad == 0x4016) {
-            joy_strobe0 = joy_strobe1 = val & 1;
-            if (!(val & 1)) { joy_bits0 = joy_buttons0; joy_bits1 = joy_buttons1; }
+        if (ad == 0x4016) {   // strobe both ports; its falling edge latches the buttons into the shift registers
+            joy_strobe = (val & 1) ? 3 : 0;
+            if (!(val & 1)) joy = (joy & 0xffffu) | (joy << 16);
         }
     }
+    // port i: while strobed, button A; else the next bit of its shift register, which then shifts
     __device__ __forceinline__ uint8_t pad_read(int i) {
-        uint8_t bit;
-        if (i == 0) {
-            if (joy_strobe0) bit = joy_buttons0 & 1;
-            else { bit = joy_bits0 & 1; joy_bits0 >>= 1; }
-        } else {
-            if (joy_strobe1) bit = joy_buttons1 & 1;
-            else { bit = joy_bits1 & 1; joy_bits1 >>= 1; }
-        }
+        const uint32_t sh = 16 + 8 * i;
+        const uint8_t bit = (joy_strobe >> i) & 1 ? (uint8_t)((joy >> (8 * i)) & 1u) : (uint8_t)((joy >> sh) & 1u);
+        if (!((joy_strobe >> i) & 1)) joy = (joy & ~(0xffu << sh)) | ((((joy >> sh) & 0xffu) >> 1) << sh);
         return bit | 0x40;
     }
 
     // ------------------------------------------------------------ PPU registers (nes_core.hpp:211-260)
     __device__ void ctrl_write(uint8_t c) {
-        nmi_en = (c >> 7) & 1; long_spr = (c >> 5) & 1; bg_page = (c >> 4) & 1; spr_page = (c >> 3) & 1;
-        inc = (c & 4) ? 32 : 1;
+        ppu_flags = (ppu_flags & (PF_SHOW_BG | PF_SHOW_SPR | PF_HIDE_EDGE_BG | PF_HIDE_EDGE_SPR)) |
+                    ((c >> 7) & 1 ? PF_NMI_EN : 0u) | ((c >> 5) & 1 ? PF_LONG_SPR : 0u) |
+                    ((c >> 4) & 1 ? PF_BG_PAGE : 0u) | ((c >> 3) & 1 ? PF_SPR_PAGE : 0u) | ((c & 4) ? PF_INC32 : 0u);
         t = (uint16_t)((t & 0xf3ff) | ((c & 3) << 10));
     }
     __device__ void mask_write(uint8_t k) {
-        hide_edge_bg = !(k & 2); hide_edge_spr = !(k & 4); show_bg = (k >> 3) & 1; show_spr = (k >> 4) & 1;
+        ppu_flags = (ppu_flags & ~(PF_SHOW_BG | PF_SHOW_SPR | PF_HIDE_EDGE_BG | PF_HIDE_EDGE_SPR)) |
+                    (!(k & 2) ? PF_HIDE_EDGE_BG : 0u) | (!(k & 4) ? PF_HIDE_EDGE_SPR : 0u) |
+                    ((k >> 3) & 1 ? PF_SHOW_BG : 0u) | ((k >> 4) & 1 ? PF_SHOW_SPR : 0u);
     }
     __device__ uint8_t status_read() {
         uint8_t r = (uint8_t)((s0hit << 6) | (vblank << 7));
@@ -458,11 +482,11 @@ struct Console {
     }
     __device__ uint8_t data_read() {
         uint8_t d = vbus_read(v);
-        v = (uint16_t)(v + inc);
+        v = (uint16_t)(v + inc());
         if (v < 0x3f00) { uint8_t b = data_buffer; data_buffer = d; d = b; }
         return d;
     }
-    __device__ void data_write(uint8_t d) { vbus_write(v, d); v = (uint16_t)(v + inc); }
+    __device__ void data_write(uint8_t d) { vbus_write(v, d); v = (uint16_t)(v + inc()); }
     __device__ void scroll_write(uint8_t d) {
         if (first_write) { t = (uint16_t)((t & ~0x1f) | (d >> 3)); fine_x = d & 7; first_write = 0; }
         else { t = (uint16_t)((t & ~0x73e0) | ((d & 7) << 12) | ((d & 0xf8) << 2)); first_write = 1; }
@@ -525,7 +549,7 @@ struct Console {
         if (pend_line < 0) return;
         // in-range sprites as a 64-bit mask (bit i: pend_line - y_i in [0, h)), from index oam_addr / 4 on;
         // the list is its first (at most 8) set bits, entries past the count keep their old values
-        const uint32_t h = long_spr ? 16u : 8u;
+        const uint32_t h = long_spr() ? 16u : 8u;
         // The env's parts each test 64 / LANES_PER_ENV sprites (part q: sprites NS q .. NS q + NS - 1) into
         // exchange word q of the env, then every part reads every word. The wave barrier is a convergence
         // point: every lane active here has stored its word before any lane loads (a wave's LDS accesses
@@ -575,12 +599,12 @@ struct Console {
         if (pend_line < 0) return nsl > 0 && sl(0) == 0;
         if (oam_addr >= 4) return false;
         int d = pend_line - (int)(oam_sprite(0) & 0xffu);
-        return d >= 0 && d < (long_spr ? 16 : 8);
+        return d >= 0 && d < (long_spr() ? 16 : 8);
     }
     __device__ uint8_t bg_colour(int px, uint8_t* pattern) const {
         int xf = (fine_x + px) % 8;
         uint8_t tile = nametable((uint16_t)(0x2000 | (v & 0x0fff)));
-        uint16_t pa = (uint16_t)(((tile * 16) + ((v >> 12) & 7)) | (bg_page << 12));
+        uint16_t pa = (uint16_t)(((tile * 16) + ((v >> 12) & 7)) | (bg_page() << 12));
         uint8_t c = (uint8_t)(((cart.chr[pa] >> (7 ^ xf)) & 1) | (((cart.chr[pa + 8] >> (7 ^ xf)) & 1) << 1));
         *pattern = c;
         uint16_t aa = (uint16_t)(0x23c0 | (v & 0x0c00) | ((v >> 4) & 0x38) | ((v >> 2) & 7));
@@ -592,14 +616,14 @@ struct Console {
         const uint32_t ow = oam_sprite(i);
         uint8_t sx = (uint8_t)(ow >> 24);
         uint8_t sy = (uint8_t)((ow & 0xffu) + 1), tile = (uint8_t)(ow >> 8), attr = (uint8_t)(ow >> 16);
-        int h = long_spr ? 16 : 8;
+        int h = long_spr() ? 16 : 8;
         int xs = (px - sx) % 8, yo = (py - sy) % h;
         if (!(attr & 0x40)) xs ^= 7;
         if (attr & 0x80) yo ^= (h - 1);
         uint16_t ad;
-        if (!long_spr) {
+        if (!long_spr()) {
             ad = (uint16_t)(tile * 16 + yo);
-            if (spr_page) ad += 0x1000;
+            if (spr_page()) ad += 0x1000;
         } else {
             yo = (yo & 7) | ((yo & 8) << 1);
             ad = (uint16_t)((tile >> 1) * 32 + yo);
@@ -611,16 +635,16 @@ struct Console {
     // Visible dots [x0, x1): sprite-0 hit and the coarse-x increments of v (nes_core.hpp:394-413).
     // Rendered and unrendered frames both take the hit from here; dots_drawn only adds pixels.
     __device__ __forceinline__ void dots_hit_scroll(int x0, int x1) {
-        if (!show_bg) return;
-        if (!s0hit && show_spr && sprite0_first()) {
+        if (!show_bg()) return;
+        if (!s0hit && show_spr() && sprite0_first()) {
             int sx = (int)(oam_sprite(0) >> 24);
             int lo = x0 > sx ? x0 : sx;
             int hi = x1 < sx + 8 ? x1 : sx + 8;
-            if (hide_edge_spr && lo < 8) lo = 8;
+            if (hide_edge_spr() && lo < 8) lo = 8;
             if (lo < hi) {
                 coarse_x_add(inc_count(x0, lo));
                 for (int px = lo; px < hi; px++) {
-                    if (!s0hit && (!hide_edge_bg || px >= 8)) {
+                    if (!s0hit && (!hide_edge_bg() || px >= 8)) {
                         uint8_t pat;
                         bg_colour(px, &pat);
                         if (pat && sprite_pattern(0, px, scanline)) s0hit = 1;
@@ -664,7 +688,7 @@ struct Console {
     // fetched once, with the addressing of sprite_pattern().
     __device__ void build_sprite_line(int py) {
         for (int w = 0; w < LDS_SP_WORDS; w++) lds_sp[w * LDS_LANES] = 0;
-        const int h = long_spr ? 16 : 8;
+        const int h = long_spr() ? 16 : 8;
         for (int k = 0; k < nsl; k++) {
             const int i = sl(k);
             const uint32_t ow = oam_sprite(i);
@@ -673,9 +697,9 @@ struct Console {
             int yo = (py - sy) % h;
             if (attr & 0x80) yo ^= (h - 1);
             uint16_t ad;
-            if (!long_spr) {
+            if (!long_spr()) {
                 ad = (uint16_t)(tile * 16 + yo);
-                if (spr_page) ad += 0x1000;
+                if (spr_page()) ad += 0x1000;
             } else {
                 yo = (yo & 7) | ((yo & 8) << 1);
                 ad = (uint16_t)((tile >> 1) * 32 + yo);
@@ -752,7 +776,7 @@ struct Console {
     // 4 at + p). pal[w]: gray values of palette addresses 4w .. 4w+3.
     __device__ __forceinline__ void bg_planes(uint32_t ta, int fy, const uint32_t (&pal)[4], uint32_t& lo, uint32_t& hi,
                                               uint32_t& gt) const {
-        const uint16_t pa = (uint16_t)((((ta & 0xffu) * 16) + fy) | (bg_page << 12));
+        const uint16_t pa = (uint16_t)((((ta & 0xffu) * 16) + fy) | (bg_page() << 12));
         lo = cart.chr[pa];
         hi = cart.chr[pa + 8];
         const uint32_t at = (ta >> (8 + (ta >> 16))) & 3u;
@@ -775,12 +799,12 @@ struct Console {
         const int py = scanline;
         materialize_sprites();
         if (pal_dirty) build_gray_palette();
-        const bool spr = show_spr && nsl;
+        const bool spr = show_spr() && nsl;
         if (spr && sp_line != py) build_sprite_line(py);
         const int f = fine_x, fy = (v >> 12) & 7;
         const int g0 = x0 >> 3, g1 = (x1 + 7) >> 3;
         uint32_t bc0 = 0, bcy = 0;             // line-start coarse x and coarse y
-        if (show_bg) {
+        if (show_bg()) {
             // line-start address: v addresses the tile of pixel x0, (f + x0) / 8 tiles into the line
             const int kb = (f + x0) >> 3;
             int c0 = (v & 0x1f) - kb;
@@ -822,7 +846,7 @@ struct Console {
         bg_planes(tile_of(pg + 1), fy, bgpal, blo, bhi, bgt);
         bg_planes(tile_of(pg + 2), fy, bgpal, clo, chi, cgt);
         uint32_t nxa = tile_of(pg + S), nxb = tile_of(pg + S + 1), nxc = tile_of(pg + S + 2);
-        if (!show_bg) { alo = ahi = blo = bhi = clo = chi = 0; agt = bgt = cgt = ubg; }
+        if (!show_bg()) { alo = ahi = blo = bhi = clo = chi = 0; agt = bgt = cgt = ubg; }
         const int ws0 = 2 * pg < 60 ? 2 * pg : 60;
         uint32_t s0 = lds_sp[ws0 * LDS_LANES], s1 = lds_sp[(ws0 + 1) * LDS_LANES];   // the pair's sprite bytes
         uint32_t s2 = lds_sp[(ws0 + 2) * LDS_LANES], s3 = lds_sp[(ws0 + 3) * LDS_LANES];
@@ -884,15 +908,15 @@ struct Console {
             const uint32_t t2 = lds_sp[(ws + 2) * LDS_LANES], t3 = lds_sp[(ws + 3) * LDS_LANES];
             uint32_t out0[2], out1[2];
             // pixels 0-7 may hide either layer
-            group_words(alo, ahi, agt, blo, bhi, bgt, s0, s1, (pg == 0 && hide_edge_bg) ? 0u : ~0u,
-                        (pg == 0 && hide_edge_spr) ? 0u : ~0u, out0);
+            group_words(alo, ahi, agt, blo, bhi, bgt, s0, s1, (pg == 0 && hide_edge_bg()) ? 0u : ~0u,
+                        (pg == 0 && hide_edge_spr()) ? 0u : ~0u, out0);
             group_words(blo, bhi, bgt, clo, chi, cgt, s2, s3, ~0u, ~0u, out1);
             store_group(8 * pg, wp, out0);
             store_group(8 * pg + 8, wp + 2 * np, out1);
             wp += 2 * S * np;
-            alo = show_bg ? dlo : 0u; ahi = show_bg ? dhi : 0u; agt = show_bg ? dgt : ubg;
-            blo = show_bg ? elo : 0u; bhi = show_bg ? ehi : 0u; bgt = show_bg ? egt : ubg;
-            clo = show_bg ? flo : 0u; chi = show_bg ? fhi : 0u; cgt = show_bg ? fgt : ubg;
+            alo = show_bg() ? dlo : 0u; ahi = show_bg() ? dhi : 0u; agt = show_bg() ? dgt : ubg;
+            blo = show_bg() ? elo : 0u; bhi = show_bg() ? ehi : 0u; bgt = show_bg() ? egt : ubg;
+            clo = show_bg() ? flo : 0u; chi = show_bg() ? fhi : 0u; cgt = show_bg() ? fgt : ubg;
             nxa = na; nxb = nb; nxc = nc;
             s0 = spr ? t0 : 0u; s1 = spr ? t1 : 0u; s2 = spr ? t2 : 0u; s3 = spr ? t3 : 0u;
         }
@@ -914,7 +938,7 @@ struct Console {
         while (n > 0) {
             int c = pcyc;
             if (pstate == ST_PRE) {
-                bool on = show_bg && show_spr;
+                bool on = show_bg() && show_spr();
                 int end = LINE_END - (!even && on);
                 int k = c >= end ? 1 : (n < end - c ? n : end - c);
                 int lo = c, hi = c + k;
@@ -939,18 +963,18 @@ struct Console {
                 } else if (c == 257 && n >= LINE_END - 256) {
                     // the rest of the line in one step when all of it is due: dot 257 (fine y), dot 258
                     // (copy_h), dots 259..340, and the line end (85 calls), as the cases below would
-                    if (show_bg) fine_y_step();
-                    if (show_bg && show_spr) copy_h();
+                    if (show_bg()) fine_y_step();
+                    if (show_bg() && show_spr()) copy_h();
                     pend_line = scanline;   // sprite evaluation for the next line (materialized lazily)
                     sp_line = -1;
                     scanline++;
                     pcyc = 1; ppu_calls += LINE_END - 256; n -= LINE_END - 256;
                     if (scanline >= 240) pstate = ST_POST;
                 } else if (c == 257) {
-                    if (show_bg) fine_y_step();
+                    if (show_bg()) fine_y_step();
                     pcyc++; ppu_calls++; n--;
                 } else if (c == 258) {
-                    if (show_bg && show_spr) copy_h();
+                    if (show_bg() && show_spr()) copy_h();
                     pcyc++; ppu_calls++; n--;
                 } else if (c > 258 && c < LINE_END) {
                     int k = n < LINE_END - c ? n : LINE_END - c;
@@ -974,7 +998,7 @@ struct Console {
                     ppu_calls++; n--;
                 } else if (c == 1 && scanline == 241) {
                     vblank = 1; ppu_calls++; n--; pcyc = 2;
-                    if (nmi_en) nmi(ppu_calls);
+                    if (nmi_en()) nmi(ppu_calls);
                 } else {
                     int lim = LINE_END - c;
                     if (scanline == 241 && c < 1) lim = 1 - c;
@@ -1176,7 +1200,7 @@ struct Console {
             // frame); with OAM, oam_addr and sprite size fixed (the loop writes nothing) sprite 0 can
             // head one only for y0 <= m < y0 + h.
             if (sprite0_first() && pstate == ST_RENDER) return false;
-            const int y0 = (int)(oam_sprite(0) & 0xffu), h = long_spr ? 16 : 8;
+            const int y0 = (int)(oam_sprite(0) & 0xffu), h = long_spr() ? 16 : 8;
             const int m = pstate == ST_RENDER && scanline > y0 ? scanline : y0;
             if (m <= 239 && m < y0 + h) limit = ppu_calls + calls_until(m + 1, 1) - 2;
             else if (y0 <= 238) limit = ppu_calls + calls_until(y0 + 1, 1) - 2;   // next frame
