@@ -15,6 +15,7 @@ enum EnvWord : int {
     E_RNG_HAS32, E_RNG_HALF, E_DONE, E_RESET_IDX,
     E_FF_LO, E_FF_HI,                                  // poll-loop instructions fast-forwarded (in E_INSTR too)
     E_REEMU_ONE, E_REEMU_PAIR, E_REEMU_K2,             // early-termination re-emulations by kind (REEMU_*)
+    E_HACK_REDRAWS,                                     // hack frames run a second time to be drawn
     E_COUNT
 };
 
@@ -198,6 +199,7 @@ struct EnvRegs {
     uint64_t frames;
     uint32_t draws;     // sticky draws taken (counted by the reset-cache builder)
     uint32_t reemu;     // REEMU_* bits of the last agent step
+    uint32_t hack_redraws;   // hack frames run again to be drawn in the last agent step
     Info info;
 };
 
@@ -269,12 +271,26 @@ struct Stepper {
         uint32_t n0 = 0, b0 = 0, f0 = 0;   // instruction, bad-op and fast-forward counters at the start of agent frame i
         int it = 0, resume_at = 0;         // loop iterations so far; the iteration a re-emulation starts at
         uint8_t* slot = gray0;
+        bool undrawn = false;              // the hack frame just run was not drawn; its start state is in slot 0
+        bool redraw = false;               // this iteration runs that hack frame again, drawn
+        uint32_t hn = 0, hb = 0, hf = 0;   // instruction, bad-op and fast-forward counters at that start state
+        ev.hack_redraws = 0;
         for (;;) {
             if (rf >= 0 && it < resume_at) { it++; continue; }   // waiting for the wave's rendered frames
             it++;
             uint8_t buttons = 0;
             if (hack) {
                 c.st(ROW_RAM + 0x7a0, 0);
+                // A hack frame of a drawn agent frame is drawn only if it ends the busy run: it runs undrawn
+                // from a snapshot and, when busy() clears after it, runs again drawn (below). A CPU frame
+                // covers a whole PPU frame, so the last frame's pixels are the whole picture, as in the
+                // reference, which draws every one. Slot 0 is free: a drawn agent frame followed by hack
+                // frames did not end the episode, so no re-emulation can follow in this step.
+                undrawn = rf < 0 && render && !redraw;
+                if (undrawn) {
+                    save_console(c, live, snap(0));
+                    hn = c.instructions; hb = c.bad_ops; hf = c.ff_instructions;
+                }
             } else if (rf < 0) {
                 int act = act0;
                 if (cfg.sticky != 0.0) {
@@ -296,7 +312,7 @@ struct Stepper {
                 slot = ((K - 1 - rf) & 1) ? gray1 : gray0;
             }
             c.set_buttons0(buttons);
-            c.render = render;
+            c.render = render && !undrawn;
             c.gray = slot;
             c.frame();
             ev.frames++;
@@ -310,6 +326,17 @@ struct Stepper {
                     if (++guard <= HACK_FRAME_LIMIT) { hack = true; continue; }
                     c.bad_ops |= ERR_HACK_LIMIT;
                 }
+                if (undrawn && !(c.bad_ops & ERR_HACK_LIMIT)) {
+                    // the busy run ended with an undrawn hack frame: back to its start, counted once
+                    restore_console(c, live, snap(0));
+                    c.instructions = hn; c.bad_ops = hb; c.ff_instructions = hf;
+                    ev.frames--;
+                    ev.hack_redraws++;
+                    undrawn = false;
+                    redraw = true;
+                    continue;
+                }
+                undrawn = redraw = false;
                 hack = false;
                 if (!done && i < K - 1) { i++; continue; }
                 // the first pass ended at agent frame i

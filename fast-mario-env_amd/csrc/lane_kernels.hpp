@@ -398,6 +398,7 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     A.ev[(size_t)E_BAD * A.np + e] += c.bad_ops;
     for (int k = 0; k < 3; k++)
         if ((ev.reemu >> k) & 1u) A.ev[(size_t)(E_REEMU_ONE + k) * A.np + e] += 1;
+    A.ev[(size_t)E_HACK_REDRAWS * A.np + e] += ev.hack_redraws;
 }
 
 // Auto-reset (fastmario.cpp:389-401): k = integers(noop_max + 1) from the env's stream, the draws of

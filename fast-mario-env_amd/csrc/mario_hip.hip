@@ -681,6 +681,7 @@ int64_t mh_frames(MhEnv* h) { return h ? sum_words(h, E_FRAMES_LO, true) : -1; }
 int64_t mh_bad_ops(MhEnv* h) { return h ? sum_words(h, E_BAD, false) : -1; }
 int64_t mh_instructions(MhEnv* h) { return h ? sum_words(h, E_INSTR_LO, true) : -1; }
 int64_t mh_ff_instructions(MhEnv* h) { return h ? sum_words(h, E_FF_LO, true) : -1; }
+int64_t mh_hack_redraws(MhEnv* h) { return h ? sum_words(h, E_HACK_REDRAWS, false) : -1; }
 int mh_reemulations(MhEnv* h, int64_t* out) {
     if (!h || !out) { g_err = "null handle or buffer"; return -1; }
     for (int k = 0; k < 3; k++)

@@ -47,7 +47,7 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).argtypes = [_P, _P]
     L.mh_step_async.argtypes = [_P, _P, _P]
     L.mh_destroy.argtypes = [_P]
-    for f in ("mh_frames", "mh_bad_ops", "mh_instructions", "mh_ff_instructions", "mh_env_bytes"):
+    for f in ("mh_frames", "mh_bad_ops", "mh_instructions", "mh_ff_instructions", "mh_env_bytes", "mh_hack_redraws"):
         getattr(L, f).restype = _i64
         getattr(L, f).argtypes = [_P]
     for f in ("mh_env_ram", "mh_env_canon", "mh_level_canon", "mh_level_obs"):

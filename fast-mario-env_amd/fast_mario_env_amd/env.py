@@ -271,6 +271,11 @@ class HipVecEnv:
         """Of instructions(), those the exact sprite-0 poll-loop fast-forward retired without executing."""
         return int(lib().mh_ff_instructions(self.h))
 
+    def hack_redraws(self) -> int:
+        """Hack frames of drawn agent frames run a second time to be drawn: the busy run's last frame (the others
+        run undrawn; frames and instructions count it once)."""
+        return int(lib().mh_hack_redraws(self.h))
+
     REEMU_KINDS = ("one", "pair", "k2")
 
     def reemulations(self) -> dict:

@@ -100,6 +100,11 @@ int64_t mh_ff_instructions(MhEnv* h);
  * last < K-1 re-ran frame last alone, out[1] it re-ran the max-pool partner last-1 as well (the two
  * branches of fastmario.cpp:351-362), out[2] of all of these, the ends at frame K-2 under max-pool. */
 int mh_reemulations(MhEnv* h, int64_t* out);
+/* Hack frames run a second time so far (synchronizing). The hack frames after a drawn agent frame
+ * (fastmario.cpp:297-308 with render on) run undrawn, each from a snapshot; the one that ends the busy run
+ * runs again from its snapshot, drawn. Frames and instructions count it once, as the reference does.
+ * No counterpart in the reference (it draws every hack frame): a measure of how often this path runs. */
+int64_t mh_hack_redraws(MhEnv* h);
 
 /* RAM of every env into d_out (n * 2048 u8, device). Replaces fm_env_ram (fastmario.cpp:630). */
 int mh_env_ram(MhEnv* h, uint8_t* d_out, void* stream);

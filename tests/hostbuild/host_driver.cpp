@@ -14,7 +14,8 @@
 //   env <config file> (rom_len:i64 rom n:i32 levels:i32[3n] lut:u8[256] skip max_steps:i32 sticky:f64
 //                    noop_max maxpool frame_stack:i32 rng:u64[6n]):
 //                    'R' -> obs;  'T' actions:i64[n] -> obs rew:f32[n] term:u8[n] trunc:u8[n] info:i64[10n]
-//                    ram[2048 n] fin ep_ret:f64[n] ep_len:i64[n];  'Q' -> frames bad_ops instructions ff:i64, exit
+//                    ram[2048 n] fin ep_ret:f64[n] ep_len:i64[n];  'Q' -> frames bad_ops instructions ff
+//                    hack_redraws:i64, exit
 //   plant <bytes>:   reads one byte past a buffer of that size (the tests check that the sanitizers catch it)
 #include <cstdio>
 #include <cstdlib>
@@ -326,13 +327,14 @@ int run_env(const char* cfg_file) {
             put(epl64.data(), 8 * (size_t)n);
             std::fflush(stdout);
         } else if (c == 'Q') {
-            int64_t out[4] = {0, 0, 0, 0};
+            int64_t out[5] = {0, 0, 0, 0, 0};
             for (int e = 0; e < n; e++) {
                 auto w = [&](int k) { return (uint64_t)v.ev[(size_t)k * np + e]; };
                 out[0] += (int64_t)(w(E_FRAMES_LO) | w(E_FRAMES_HI) << 32);
                 out[1] += (int64_t)w(E_BAD);
                 out[2] += (int64_t)(w(E_INSTR_LO) | w(E_INSTR_HI) << 32);
                 out[3] += (int64_t)(w(E_FF_LO) | w(E_FF_HI) << 32);
+                out[4] += (int64_t)w(E_HACK_REDRAWS);
             }
             put(out, sizeof out);
             std::fflush(stdout);

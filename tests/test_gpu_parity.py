@@ -206,6 +206,46 @@ def _env_run(names, config, steps):
         assert eps > 0
 
 
+def test_hack_frames_redrawn_vs_oracle():
+    """Busy runs after drawn agent frames (the player in a pipe / area transition while frames K-2 and K-1 are
+    drawn): the HIP path runs such hack frames undrawn from a snapshot and runs the last one again drawn; the
+    oracle draws every one, as the reference does. 512 envs of levels whose busy runs are common, right+jump
+    with p = 0.5 (as in the divergence-stress workload), headline wrappers, every output every step. The
+    oracle runs as 16 instances of 32 envs (their own PCG64 streams by env_offset) on a thread pool."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    import torch
+
+    from fast_mario_env_amd import HipVecEnv
+    kw = CONFIGS["headline"]
+    names = ["4-4", "5-1"] * 256
+    n, m = len(names), 32
+    cpu = [OracleVec(MINI, _levels(names[k:k + m]), m, seed=3, env_offset=k, **kw) for k in range(0, n, m)]
+    gpu = HipVecEnv(names, n, seed=3, rom=MINI, **kw)
+    pool = ThreadPoolExecutor(min(16, os.cpu_count() or 1))
+    o1 = np.concatenate([c.reset() for c in cpu])
+    assert np.array_equal(o1, gpu.reset().cpu().numpy()), "reset obs"
+    rng = np.random.default_rng(17)
+    for t in range(scaled(240)):
+        a = np.where(rng.random(n) < 0.5, 2, rng.integers(0, 7, n))
+        outs = list(pool.map(lambda kc: [x.copy() for x in kc[1].step(a[kc[0]:kc[0] + m])], zip(range(0, n, m), cpu)))
+        o1, r1, te1, tr1, i1 = (np.concatenate(z) for z in zip(*outs))
+        o2, r2, te2, tr2, _ = gpu.step(torch.from_numpy(a).cuda())
+        o2, r2, te2, tr2, i2 = (x.cpu().numpy() for x in (o2, r2, te2, tr2, gpu.info_t))
+        assert np.array_equal(r1, r2) and np.array_equal(te1, te2) and np.array_equal(tr1, tr2), (t, "reward/done")
+        assert np.array_equal(i1, i2), (t, "info")
+        assert np.array_equal(o1, o2), (t, "obs", np.argwhere(o1 != o2)[:5].tolist())
+    pool.shutdown()
+    ram = gpu.ram().cpu().numpy()
+    for i in range(n):
+        assert np.array_equal(cpu[i // m].ram(i % m), ram[i]), (i, "ram")
+    assert gpu.frames == sum(c.frames() for c in cpu)
+    assert gpu.instructions() == sum(c.instructions() for c in cpu)
+    assert gpu.bad_ops() == 0
+    assert gpu.hack_redraws() > 0, "no busy run after a drawn frame: the redraw path was not exercised"
+
+
 def test_config1_golden_trace_on_gpu():
     """The CPU golden-trace workload (32 envs of 1-1, seed 0, no sticky / no-op / max-pool, actions from
     default_rng(0)) through the HIP path, against the digests the reference C++ wrote for all 1,000 steps

@@ -125,7 +125,7 @@ class HostVec:
         return self._ram[i]
 
     def finish(self):
-        return self.proc.quit(32)        # frames, bad ops, instructions, fast-forwarded instructions
+        return self.proc.quit(40)        # frames, bad ops, instructions, fast-forwarded instructions, hack redraws
 
 
 def test_hostbuild_sanitizer_catches_a_planted_overrun(exe):
@@ -160,5 +160,5 @@ def test_hostbuild_env_golden(exe, tmp_path, config):
     tr = G.run_env(venv, G.env_actions(len(names), G.ENV_STEPS))
     bad = [i for i, (a, b) in enumerate(zip(tr, g["trace"])) if a != b]
     assert not bad, f"first mismatching step {bad[0] - 1}"
-    frames, bad_ops, instr, ff = venv.finish()
-    assert frames == g["frames"] and bad_ops == 0 and 0 <= ff <= instr
+    frames, bad_ops, instr, ff, redraws = venv.finish()
+    assert frames == g["frames"] and bad_ops == 0 and 0 <= ff <= instr and redraws >= 0
