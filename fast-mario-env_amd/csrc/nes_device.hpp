@@ -1124,10 +1124,11 @@ struct Console {
         if (fl == FL_BIT) { keep &= ~(uint32_t)(FZ | FV | FN); set |= bitv; }
         if (fl == FL_OP) { keep &= ~fm; set |= fset; }
         p = (uint8_t)((p & keep) | set);
-        a = dst == D_A ? r8 : a;
-        x = dst == D_X ? r8 : x;
-        y = dst == D_Y ? r8 : y;
-        sp = dst == D_SP ? r8 : sp;
+        // the destination register as a byte insert into the packed a | x << 8 | y << 16 | sp << 24 (D_A .. D_SP
+        // are 1 .. 4): the four fields share one word, so writing all four from it is one register write
+        const uint32_t dsh = 8u * (dst - D_A), dmask = 0xffu << dsh;
+        const uint32_t nregs = (dst - D_A) < 4u ? (regs & ~dmask) | ((uint32_t)r8 << dsh) : regs;
+        a = nregs; x = nregs >> 8; y = nregs >> 16; sp = nregs >> 24;
         if (wr) write(ea, r8);
         // control flow: the next pc by instruction length, branches and JMP as selects
         constexpr uint32_t ABS3 = 1u << M_ABS | 1u << M_ABSX | 1u << M_ABSY;
