@@ -1126,7 +1126,7 @@ struct Console {
         p = (uint8_t)((p & keep) | set);
         // the destination register as a byte insert into the packed a | x << 8 | y << 16 | sp << 24 (D_A .. D_SP
         // are 1 .. 4): the four fields share one word, so writing all four from it is one register write
-        const uint32_t dsh = 8u * (dst - D_A), dmask = 0xffu << dsh;
+        const uint32_t dsh = (8u * (dst - D_A)) & 31u, dmask = 0xffu << dsh;   // masked: no register for D_NONE / D_MEM
         const uint32_t nregs = (dst - D_A) < 4u ? (regs & ~dmask) | ((uint32_t)r8 << dsh) : regs;
         a = nregs; x = nregs >> 8; y = nregs >> 16; sp = nregs >> 24;
         if (wr) write(ea, r8);
