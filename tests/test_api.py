@@ -149,3 +149,54 @@ def test_resize_kernel_has_no_fma(tmp_path):
         assert not re.search(r"\bv_(fma|fmac|mac|mad|pk_fma)\w*_f32", body), name
         checked += 1
     assert checked == 3
+
+
+class _FakeVec:
+    """Stands in for FastVecEnv in the SB3 translation tests: fixed outputs, two envs, env 1 ends its episode."""
+
+    def __init__(self, k):
+        self.k = k
+        self.o = np.arange(2 * k * 84 * 84, dtype=np.int64).astype(np.uint8).reshape(2, k, 84, 84)
+        self.fin = (255 - self.o[1]).copy()
+
+    def reset(self):
+        return self.o
+
+    def step_wait(self):
+        infos = [{"x_pos": 40}, {"x_pos": 41, "final_obs": self.fin, "TimeLimit.truncated": True,
+                                  "episode": {"r": 1.0, "l": 5}}]
+        return self.o, np.array([0.5, 1.0], np.float32), np.array([False, False]), np.array([False, True]), infos
+
+
+@pytest.mark.parametrize("stacked", [False, True])
+def test_sb3_translation(stacked):
+    """sb3.py:38-49 of the reference: channels-last single frames or the stack as is, dones = term | trunc,
+    final_obs renamed terminal_observation in the same layout, episode dropped (VecMonitor writes its own)."""
+    k = 4 if stacked else 1
+    venv = _FakeVec(k)
+    core = fme.Sb3Frames(venv, stacked)
+    o = core.reset()
+    assert core.shape == ((4, 84, 84) if stacked else (84, 84, 1))
+    assert o.shape == (2,) + core.shape
+    assert np.array_equal(o, venv.o if stacked else venv.o[:, 0, :, :, None])
+    o, r, d, infos = core.step_wait()
+    assert d.tolist() == [False, True] and r.tolist() == [0.5, 1.0]
+    assert "terminal_observation" not in infos[0] and infos[0]["x_pos"] == 40
+    t = infos[1]["terminal_observation"]
+    assert np.array_equal(t, venv.fin if stacked else venv.fin[0][:, :, None])
+    assert "episode" not in infos[1] and "final_obs" not in infos[1] and infos[1]["TimeLimit.truncated"]
+    if not stacked:
+        with pytest.raises(ValueError, match="frame_stack=1"):
+            fme.Sb3Frames(_FakeVec(4), False)
+
+
+def test_sb3_adapter_without_sb3():
+    """sb3_vec_env needs stable-baselines3 and gymnasium, which this image lacks: the call says so."""
+    try:
+        import gymnasium  # noqa: F401
+        import stable_baselines3  # noqa: F401
+        pytest.skip("stable-baselines3 is installed")
+    except ImportError:
+        pass
+    with pytest.raises(ImportError, match="stable-baselines3"):
+        fme.sb3_vec_env("1-1", 2)

@@ -158,3 +158,96 @@ def test_set_buffers_device_and_refusals():
     v.step(np.array([0, 0]))
     torch.cuda.synchronize()
     v.close()
+
+
+class _StackLikeSb3:
+    """SB3's VecFrameStack rule for channels-last Box observations, restated for this test (SB3 is not installed):
+    reset zero-fills the stack and puts the frame last; each step shifts the stack one frame towards the front,
+    and for an env that is done builds its terminal_observation as the stack's newest k-1 frames followed by the
+    final frame, zero-fills the stack, then puts the new frame last."""
+
+    def __init__(self, k):
+        self.k = k
+
+    def reset(self, o):
+        self.s = np.zeros(o.shape[:3] + (self.k,), np.uint8)
+        self.s[..., -1:] = o
+        return self.s.copy()
+
+    def step(self, o, dones, infos):
+        self.s = np.roll(self.s, -1, axis=-1)
+        for i in np.flatnonzero(dones):
+            t = infos[i].get("terminal_observation")
+            if t is not None:
+                infos[i]["terminal_observation"] = np.concatenate([self.s[i, ..., :-1], t], axis=-1)
+            self.s[i] = 0
+        self.s[..., -1:] = o
+        return self.s.copy()
+
+
+def _fake_sb3(monkeypatch):
+    """Minimal gymnasium.spaces and SB3 VecEnv base modules, enough for sb3_vec_env to build its class."""
+    import sys
+    import types
+
+    class VecEnv:
+        def __init__(self, num_envs, observation_space, action_space):
+            self.num_envs, self.observation_space, self.action_space = num_envs, observation_space, action_space
+
+        def step(self, actions):
+            self.step_async(actions)
+            return self.step_wait()
+
+    class Box:
+        def __init__(self, low, high, shape, dtype):
+            self.low, self.high, self.shape, self.dtype = low, high, tuple(shape), dtype
+
+    class Discrete:
+        def __init__(self, n):
+            self.n = n
+
+    mods = {"gymnasium": types.ModuleType("gymnasium"), "gymnasium.spaces": types.ModuleType("gymnasium.spaces")}
+    mods["gymnasium.spaces"].Box, mods["gymnasium.spaces"].Discrete = Box, Discrete
+    mods["gymnasium"].spaces = mods["gymnasium.spaces"]
+    for name in ("stable_baselines3", "stable_baselines3.common", "stable_baselines3.common.vec_env",
+                 "stable_baselines3.common.vec_env.base_vec_env"):
+        mods[name] = types.ModuleType(name)
+    mods["stable_baselines3.common.vec_env.base_vec_env"].VecEnv = VecEnv
+    for name, m in mods.items():
+        monkeypatch.setitem(sys.modules, name, m)
+
+
+def test_sb3_adapter(monkeypatch):
+    """test_api.py:101-116 of the reference: single frames stacked by SB3's VecFrameStack rule equal the env's own
+    stacks (stack_in_cpp=True), observations, dones and terminal observations, over 30 steps with time-limit
+    ends (max_steps=12); the stacked env is also checked against the oracle."""
+    import fast_mario_env_amd as fme
+    _fake_sb3(monkeypatch)
+    kw = dict(seed=0, max_steps=12, rom=MINI)
+    single = fme.sb3_vec_env("1-1", 2, **kw)
+    fast = fme.sb3_vec_env("1-1", 2, stack_in_cpp=True, **kw)
+    assert single.observation_space.shape == (84, 84, 1) and fast.observation_space.shape == (4, 84, 84)
+    assert single.action_space.n == 7 and single.num_envs == 2
+    assert single.get_attr("x") == [None, None] and single.env_is_wrapped(object, indices=1) == [False]
+    ref = OracleVec(MINI, _levels(["1-1"] * 2), 2, seed=0, max_steps=12)
+    stack = _StackLikeSb3(4)
+    o1, o2 = stack.reset(single.reset()), fast.reset()
+    assert o1.shape == (2, 84, 84, 4) and o2.shape == (2, 4, 84, 84)
+    assert np.array_equal(o1.transpose(0, 3, 1, 2), o2) and np.array_equal(o2, ref.reset())
+    ends = 0
+    for t in range(30):
+        a = np.array([t % 7, (t * 3) % 7])
+        s1, _, d1, i1 = single.step(a)
+        o2, r2, d2, i2 = fast.step(a)
+        o1 = stack.step(s1, d1, i1)
+        ref.step(a)
+        assert np.array_equal(o1.transpose(0, 3, 1, 2), o2) and np.array_equal(d1, d2)
+        assert np.array_equal(o2, ref.obs) and np.array_equal(r2, ref.rew)
+        for i in np.flatnonzero(d2):
+            ends += 1
+            assert np.array_equal(i1[i]["terminal_observation"].transpose(2, 0, 1), i2[i]["terminal_observation"])
+            assert np.array_equal(i2[i]["terminal_observation"], ref.fin[i])
+            assert "episode" not in i2[i]
+            assert i2[i]["TimeLimit.truncated"] == bool(ref.trunc[i] and not ref.term[i])
+    assert ends >= 4
+    single.close(); fast.close()
