@@ -1030,6 +1030,51 @@ struct Console {
         return s < cap ? s : cap;
     }
 
+    // The data operation of decode word D: the result byte and the new flags, from the packed registers regs
+    // (a | x << 8 | y << 16 | sp << 24), the data operand m (the first operand byte when nothing was read), the
+    // flags p and whether a data operand was read. Every choice is a select on bits of the decode word: chains of
+    // equality tests on one small field would be lowered to a branch tree, i.e. exec-mask branches on every
+    // instruction of a divergent wave.
+    struct AluOut { uint32_t r8, p; };
+    __device__ __forceinline__ static AluOut alu_op(uint32_t D, uint32_t regs, uint32_t m, uint32_t p, bool rd) {
+        using namespace dec;
+        const uint32_t alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, fl = (D >> FL_SH) & 7u;
+        const uint32_t a = regs & 0xffu;
+        const uint32_t rv = src ? (regs >> (8 * (src - 1))) & 0xffu : (uint32_t)m;   // R_A, R_X, R_Y, R_SP, or M
+        const uint32_t sv = rd ? (uint32_t)m : rv;                // operand of the unary operations
+        const uint32_t cin = (p & FC) ? 1u : 0u;
+        const uint32_t sum = a + m + cin;                         // ADC
+        const uint32_t dif = a - m - (1u - cin);                  // SBC
+        const uint32_t cmp = rv - m;                              // CMP / CPX / CPY
+        const bool u0 = alu & 1u, u1 = alu & 2u, u2 = alu & 4u, u3 = alu & 8u;
+        const uint32_t rc = u0 ? cin : 0u;                        // ROL / ROR carry in
+        // OP_ results by the bits of alu: PASS ORA AND EOR ADC SBC CMP BIT ASL ROL LSR ROR INC DEC FLAG NOP
+        const uint32_t g0 = u0 ? (uint32_t)(a | m) : sv, g1 = u0 ? (uint32_t)(a ^ m) : (uint32_t)(a & m);
+        const uint32_t g2 = u0 ? dif : sum, g3 = u0 ? sv : cmp;
+        const uint32_t g4 = (sv << 1) | rc, g5 = (sv >> 1) | (rc << 7), g6 = u0 ? sv - 1 : sv + 1, g7 = sv;
+        const uint32_t h0 = u1 ? g1 : g0, h1 = u1 ? g3 : g2, h2 = u1 ? g5 : g4, h3 = u1 ? g7 : g6;
+        const uint32_t res = u3 ? (u2 ? h3 : h2) : (u2 ? h1 : h0);
+        const uint32_t r8 = res & 0xffu;
+        // carry: ADC bit 8 of the sum; SBC / CMP no borrow; ASL / ROL bit 7; LSR / ROR bit 0
+        const uint32_t c_sub = ((res >> 8) & 1u) ^ 1u, c_adc = (sum >> 8) & 1u;
+        const uint32_t carry = u3 ? (u1 ? (sv & 1u) : ((sv >> 7) & 1u)) : ((u0 | u1) ? c_sub : c_adc);
+        const uint32_t ovf = u0 ? ((a ^ dif) & (~(uint32_t)m ^ dif) & 0x80u) : ((a ^ sum) & (m ^ sum) & 0x80u);
+        // flag groups NONE NZ NZC NZCV BIT OP as masks of the bits they replace
+        const uint32_t nzv = (r8 ? 0u : FZ) | (r8 >> 7);          // FN is bit 0
+        const uint32_t fz = (a & m) ? 0u : FZ;
+        const uint32_t bitv = fz | (m & 0x40 ? FV : 0u) | (m >> 7);
+        const uint32_t fop = (D >> FOP_SH) & 7u;
+        const uint32_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;   // CLC SEC CLI SEI CLV CLD SED
+        const uint32_t fset = (fop == 1 || fop == 3 || fop == 6) ? fm : 0u;
+        uint32_t keep = 0xffu, set = 0u;
+        if ((0xeu >> fl) & 1u) { keep &= ~(uint32_t)(FZ | FN); set |= nzv; }             // NZ, NZC, NZCV
+        if ((0xcu >> fl) & 1u) { keep &= ~(uint32_t)FC; set |= carry ? FC : 0u; }        // NZC, NZCV
+        if (fl == FL_NZCV) { keep &= ~(uint32_t)FV; set |= ovf ? FV : 0u; }
+        if (fl == FL_BIT) { keep &= ~(uint32_t)(FZ | FV | FN); set |= bitv; }
+        if (fl == FL_OP) { keep &= ~fm; set |= fset; }
+        return AluOut{r8, (p & keep) | set};
+    }
+
     // One whole instruction from its decode word: addressing, at most one data read and one data
     // write through the bus, the ALU as register selects, and one small switch for the stack /
     // control-flow operations, in the reference's bus order (operand bytes, pointer, data read, data
@@ -1087,43 +1132,10 @@ struct Console {
         if (D & PEN) cross_penalty(base, (uint16_t)(base + idx), 1);
         // data operand and ALU
         const uint8_t m = rd && am != M_IMM ? read(ea) : b1;
-        const uint32_t alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, fl = (D >> FL_SH) & 7u;
-        // Every choice below is a select on bits of the decode word: chains of equality tests on one small
-        // field would be lowered to a branch tree, i.e. exec-mask branches on every instruction.
         const uint32_t regs = (uint32_t)a | (uint32_t)x << 8 | (uint32_t)y << 16 | (uint32_t)sp << 24;
-        const uint32_t rv = src ? (regs >> (8 * (src - 1))) & 0xffu : (uint32_t)m;   // R_A, R_X, R_Y, R_SP, or M
-        const uint32_t sv = rd ? (uint32_t)m : rv;                // operand of the unary operations
-        const uint32_t cin = (p & FC) ? 1u : 0u;
-        const uint32_t sum = a + m + cin;                         // ADC
-        const uint32_t dif = a - m - (1u - cin);                  // SBC
-        const uint32_t cmp = rv - m;                              // CMP / CPX / CPY
-        const bool u0 = alu & 1u, u1 = alu & 2u, u2 = alu & 4u, u3 = alu & 8u;
-        const uint32_t rc = u0 ? cin : 0u;                        // ROL / ROR carry in
-        // OP_ results by the bits of alu: PASS ORA AND EOR ADC SBC CMP BIT ASL ROL LSR ROR INC DEC FLAG NOP
-        const uint32_t g0 = u0 ? (uint32_t)(a | m) : sv, g1 = u0 ? (uint32_t)(a ^ m) : (uint32_t)(a & m);
-        const uint32_t g2 = u0 ? dif : sum, g3 = u0 ? sv : cmp;
-        const uint32_t g4 = (sv << 1) | rc, g5 = (sv >> 1) | (rc << 7), g6 = u0 ? sv - 1 : sv + 1, g7 = sv;
-        const uint32_t h0 = u1 ? g1 : g0, h1 = u1 ? g3 : g2, h2 = u1 ? g5 : g4, h3 = u1 ? g7 : g6;
-        const uint32_t res = u3 ? (u2 ? h3 : h2) : (u2 ? h1 : h0);
-        const uint8_t r8 = (uint8_t)res;
-        // carry: ADC bit 8 of the sum; SBC / CMP no borrow; ASL / ROL bit 7; LSR / ROR bit 0
-        const uint32_t c_sub = ((res >> 8) & 1u) ^ 1u, c_adc = (sum >> 8) & 1u;
-        const uint32_t carry = u3 ? (u1 ? (sv & 1u) : ((sv >> 7) & 1u)) : ((u0 | u1) ? c_sub : c_adc);
-        const uint32_t ovf = u0 ? ((a ^ dif) & (~(uint32_t)m ^ dif) & 0x80u) : ((a ^ sum) & (m ^ sum) & 0x80u);
-        // flag groups NONE NZ NZC NZCV BIT OP as masks of the bits they replace
-        const uint32_t nzv = (r8 ? 0u : FZ) | (r8 >> 7);          // FN is bit 0
-        const uint32_t fz = (a & m) ? 0u : FZ;
-        const uint32_t bitv = fz | (m & 0x40 ? FV : 0u) | (m >> 7);
-        const uint32_t fop = (D >> FOP_SH) & 7u;
-        const uint32_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;   // CLC SEC CLI SEI CLV CLD SED
-        const uint32_t fset = (fop == 1 || fop == 3 || fop == 6) ? fm : 0u;
-        uint32_t keep = 0xffu, set = 0u;
-        if ((0xeu >> fl) & 1u) { keep &= ~(uint32_t)(FZ | FN); set |= nzv; }             // NZ, NZC, NZCV
-        if ((0xcu >> fl) & 1u) { keep &= ~(uint32_t)FC; set |= carry ? FC : 0u; }        // NZC, NZCV
-        if (fl == FL_NZCV) { keep &= ~(uint32_t)FV; set |= ovf ? FV : 0u; }
-        if (fl == FL_BIT) { keep &= ~(uint32_t)(FZ | FV | FN); set |= bitv; }
-        if (fl == FL_OP) { keep &= ~fm; set |= fset; }
-        p = (uint8_t)((p & keep) | set);
+        const AluOut ao = alu_op(D, regs, m, p, rd);
+        p = (uint8_t)ao.p;
+        const uint8_t r8 = (uint8_t)ao.r8;
         // the destination register as a byte insert into the packed a | x << 8 | y << 16 | sp << 24 (D_A .. D_SP
         // are 1 .. 4): the four fields share one word, so writing all four from it is one register write
         const uint32_t dsh = (8u * (dst - D_A)) & 31u, dmask = 0xffu << dsh;   // masked: no register for D_NONE / D_MEM
@@ -1171,6 +1183,201 @@ struct Console {
         exec_at = j + (skip >= 1 ? skip : 1);
         zero_skip = skip <= 0;
         return true;
+    }
+
+    // ------------------------------------------------------------ a lone console's instruction run
+    // While a console is the only one of its wave with an instruction to run (the others parked at their slice
+    // end, or out of the frame loop), an iteration of frame()'s loop costs about what it costs a full wave: every
+    // opcode's work as selects, the wave votes and the catch-up checks. lone_run() runs that console's
+    // instructions back to back instead, with its registers and decode word wave-uniform, so that the compiler
+    // branches over the work an opcode does not need. It runs the instructions whose opcode and operands are in
+    // PRG and whose bus accesses touch only RAM, PRG, or addresses that read as 0 or ignore writes ($4000-$7FFF
+    // but the joypads and OAM DMA), as instruction() would; it stops before any other instruction (PPU register,
+    // joypad or DMA access, invalid opcode), before the idle loop `JMP *` (fast-forwarded by frame()), before an
+    // instruction at the NMI check, and at the slice or frame end, leaving that instruction to frame()'s own
+    // iteration. Returns the number of instructions run. Called by this console's lanes only (its parts, with
+    // identical values), while no lane of the wave waits for a catch-up.
+    __device__ __forceinline__ static uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+    __device__ __forceinline__ static bool lone_reads(uint32_t ad) {
+        return ad < 0x2000u || ad >= 0x8000u || (ad >= 0x4000u && ad != 0x4016u && ad != 0x4017u);
+    }
+    __device__ __forceinline__ static bool lone_writes(uint32_t ad) {
+        return ad < 0x2000u || (ad >= 0x4000u && ad != 0x4014u && ad != 0x4016u);
+    }
+    // read() for the addresses lone_reads() admits
+    __device__ __forceinline__ uint32_t lone_read(uint32_t ad) const {
+        if (ad < 0x2000u) return uniform(ram(ad));
+        if (ad >= 0x8000u) return uniform(prg((uint16_t)ad));
+        return 0u;
+    }
+    __device__ __forceinline__ uint32_t lone_run(int32_t end, int32_t slice) {
+        using namespace dec;
+        uint32_t upc = uniform(pc), ua = uniform(a), ux = uniform(x), uy = uniform(y), us = uniform(sp), up = uniform(p);
+        int32_t ex = (int32_t)uniform((uint32_t)exec_at);
+        const int32_t calls = (int32_t)uniform((uint32_t)ppu_calls), nmi = (int32_t)uniform((uint32_t)nmi_thresh);
+        const int32_t last = (int32_t)uniform((uint32_t)slice);
+        uint32_t n = 0, zs = 0;
+        for (;;) {
+            const int32_t j = ex, tgt = 3 * (j + 1);
+            if (j >= end || tgt > last) break;                  // parks in frame()
+            if (tgt >= nmi && calls < tgt) break;               // frame() catches up first
+            if (upc < 0x8000u || upc > 0xfffdu) break;          // opcode or operands through the bus
+            const uint32_t pa = upc & 0x7fffu;
+            const uint32_t* pw = (const uint32_t*)cart.prg + (pa >> 2);
+            const uint64_t w = (uint64_t)uniform(pw[1]) << 32 | uniform(pw[0]);
+            const uint32_t b0 = (uint32_t)(w >> (8 * (pa & 3u)));                // bytes pc .. pc + 3
+            const uint32_t op = b0 & 0xffu, b1 = (b0 >> 8) & 0xffu, b2 = (b0 >> 16) & 0xffu, absv = b1 | b2 << 8;
+            if (op == 0x4cu && absv == upc) break;               // JMP *: frame()'s idle fast-forward
+            const uint32_t D = uniform(cart.dec[op]);
+            if (!(D & OK)) break;                               // invalid opcode: frame() counts it
+            const uint32_t am = D & 15u, alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, dst = (D >> DST_SH) & 7u;
+            const uint32_t xop = (D >> X_SH) & 15u, fl = (D >> FL_SH) & 7u;
+            const bool rd = (D & RD) != 0;
+            // addressing (instruction()'s rules): effective address, page-cross penalty, instruction length
+            uint32_t ea = 0, len = 2;
+            int32_t sk = 0;
+            switch (am) {
+                case M_NONE: len = 1; break;
+                case M_IMM: ea = (upc + 1u) & 0xffffu; break;
+                case M_ZP: ea = b1; break;
+                case M_ZPX: ea = (b1 + ux) & 0xffu; break;
+                case M_ZPY: ea = (b1 + uy) & 0xffu; break;
+                case M_ABS: ea = absv; len = 3; break;
+                case M_ABSX: case M_ABSY: {
+                    const uint32_t i = am == M_ABSX ? ux : uy;
+                    ea = (absv + i) & 0xffffu; len = 3;
+                    if ((D & PEN) && ((absv ^ (absv + i)) & 0xff00u)) sk = 1;
+                    break;
+                }
+                case M_INDX: {
+                    const uint32_t z = (b1 + ux) & 0xffu;
+                    ea = lone_read(z) | lone_read((z + 1u) & 0xffu) << 8;
+                    break;
+                }
+                default: {   // M_INDY
+                    const uint32_t base = lone_read(b1) | lone_read((b1 + 1u) & 0xffu) << 8;
+                    ea = (base + uy) & 0xffffu;
+                    if ((D & PEN) && ((base ^ (base + uy)) & 0xff00u)) sk = 1;
+                    break;
+                }
+            }
+            const uint32_t p2 = (absv & 0xff00u) | ((absv + 1u) & 0xffu);   // JMP (ind): high byte, page wrap
+            const bool wr = dst == D_MEM;
+            if (xop == X_JMPI ? !(lone_reads(absv) && lone_reads(p2))
+                              : ((rd && am != M_IMM && !lone_reads(ea)) || (wr && !lone_writes(ea)))) break;
+            const uint32_t m = rd && am != M_IMM ? lone_read(ea) : b1;
+            // the data operation (alu_op()'s results, by cases): result, carry out and overflow
+            const uint32_t rv = src == R_M ? m : src == R_A ? ua : src == R_X ? ux : src == R_Y ? uy : us;
+            const uint32_t sv = rd ? m : rv, cin = up & FC ? 1u : 0u;
+            uint32_t r = sv, c = 0, v = 0;
+            switch (alu) {
+                case OP_ORA: r = ua | m; break;
+                case OP_AND: r = ua & m; break;
+                case OP_EOR: r = ua ^ m; break;
+                case OP_ADC: { const uint32_t t = ua + m + cin; r = t & 0xffu; c = (t >> 8) & 1u; v = (ua ^ t) & (m ^ t) & 0x80u; break; }
+                case OP_SBC: { const uint32_t t = ua - m - (1u - cin); r = t & 0xffu; c = ((t >> 8) & 1u) ^ 1u; v = (ua ^ t) & (~m ^ t) & 0x80u; break; }
+                case OP_CMP: { const uint32_t t = rv - m; r = t & 0xffu; c = ((t >> 8) & 1u) ^ 1u; break; }
+                case OP_ASL: r = (sv << 1) & 0xffu; c = (sv >> 7) & 1u; break;
+                case OP_ROL: r = ((sv << 1) | cin) & 0xffu; c = (sv >> 7) & 1u; break;
+                case OP_LSR: r = sv >> 1; c = sv & 1u; break;
+                case OP_ROR: r = (sv >> 1) | cin << 7; c = sv & 1u; break;
+                case OP_INC: r = (sv + 1u) & 0xffu; break;
+                case OP_DEC: r = (sv - 1u) & 0xffu; break;
+                default: break;   // PASS, BIT, FLAG, NOP: the operand
+            }
+            const uint32_t nz = (r ? 0u : FZ) | (r >> 7);          // FN is bit 0
+            switch (fl) {
+                case FL_NZ: up = (up & ~(uint32_t)(FZ | FN)) | nz; break;
+                case FL_NZC: up = (up & ~(uint32_t)(FZ | FN | FC)) | nz | (c ? FC : 0u); break;
+                case FL_NZCV: up = (up & ~(uint32_t)(FZ | FN | FC | FV)) | nz | (c ? FC : 0u) | (v ? FV : 0u); break;
+                case FL_BIT: up = (up & ~(uint32_t)(FZ | FV | FN)) | ((ua & m) ? 0u : FZ) | (m & 0x40u ? FV : 0u) | (m >> 7); break;
+                case FL_OP: {   // CLC SEC CLI SEI CLV CLD SED
+                    const uint32_t fop = (D >> FOP_SH) & 7u;
+                    const uint32_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;
+                    up = (up & ~fm) | ((fop == 1 || fop == 3 || fop == 6) ? fm : 0u);
+                    break;
+                }
+                default: break;
+            }
+            switch (dst) {
+                case D_A: ua = r; break;
+                case D_X: ux = r; break;
+                case D_Y: uy = r; break;
+                case D_SP: us = r; break;
+                case D_MEM: if (ea < 0x2000u) st(ROW_RAM + (ea & 0x7ffu), (uint8_t)r); break;   // else ignored
+                default: break;
+            }
+            uint32_t npc = (upc + len) & 0xffffu;
+            const uint32_t ret = (upc + 2u) & 0xffffu;
+            switch (xop) {
+                case X_NONE: break;
+                case X_BRANCH: {   // on N, V, C, Z (op bits 6-7) equal to op bit 5
+                    const uint32_t fbit = (0x40800201u >> (8 * (op >> 6))) & 0xffu;   // FN FV FC FZ
+                    if (((up & fbit) != 0) == ((op & 0x20u) != 0)) {
+                        npc = (ret + (uint32_t)(int32_t)(int8_t)b1) & 0xffffu;
+                        sk += ((ret ^ npc) & 0xff00u) ? 3 : 1;
+                    } else {
+                        npc = ret;
+                    }
+                    break;
+                }
+                case X_JMP: npc = absv; break;
+                case X_JMPI: npc = lone_read(absv) | lone_read(p2) << 8; break;
+                case X_JSR:
+                    st(ROW_RAM + (0x100u | us), (uint8_t)(ret >> 8));
+                    st(ROW_RAM + (0x100u | ((us - 1u) & 0xffu)), (uint8_t)ret);
+                    us = (us - 2u) & 0xffu;
+                    npc = absv;
+                    break;
+                case X_BRK:
+                    st(ROW_RAM + (0x100u | us), (uint8_t)(ret >> 8));
+                    st(ROW_RAM + (0x100u | ((us - 1u) & 0xffu)), (uint8_t)ret);
+                    st(ROW_RAM + (0x100u | ((us - 2u) & 0xffu)), (uint8_t)(up | 0x30u));
+                    us = (us - 3u) & 0xffu;
+                    up |= FI;
+                    npc = uniform(prg(0xfffe)) | uniform(prg(0xffff)) << 8;
+                    sk += 7;
+                    break;
+                case X_PHA: case X_PHP:
+                    st(ROW_RAM + (0x100u | us), (uint8_t)(xop == X_PHA ? ua : up));
+                    us = (us - 1u) & 0xffu;
+                    break;
+                case X_RTS: {
+                    const uint32_t lo = lone_read(0x100u | ((us + 1u) & 0xffu)), hi = lone_read(0x100u | ((us + 2u) & 0xffu));
+                    us = (us + 2u) & 0xffu;
+                    npc = ((lo | hi << 8) + 1u) & 0xffffu;
+                    break;
+                }
+                case X_RTI: {
+                    const uint32_t f = lone_read(0x100u | ((us + 1u) & 0xffu)), lo = lone_read(0x100u | ((us + 2u) & 0xffu)),
+                                   hi = lone_read(0x100u | ((us + 3u) & 0xffu));
+                    us = (us + 3u) & 0xffu;
+                    up = f; npc = lo | hi << 8;
+                    break;
+                }
+                default: {   // PLA, PLP
+                    const uint32_t u = lone_read(0x100u | ((us + 1u) & 0xffu));
+                    us = (us + 1u) & 0xffu;
+                    if (xop == X_PLA) { ua = u; up = (up & ~(uint32_t)(FZ | FN)) | (u ? 0u : FZ) | (u >> 7); }
+                    else up = u;
+                    break;
+                }
+            }
+            upc = npc;
+            sk += (int32_t)((D >> CYC_SH) & 7u);
+            ex = j + (sk >= 1 ? sk : 1);
+            zs = sk <= 0;   // opcodes the cycle table gives 0 cycles (and no penalty)
+            n++;
+        }
+        if (n) {
+            pc = (uint16_t)upc;
+            a = ua; x = ux; y = uy; sp = us;
+            p = (uint8_t)up;
+            exec_at = ex;
+            zero_skip = zs;
+            instructions += n;
+        }
+        return n;
     }
 
     // PPU calls from the current PPU position to (line, dot) on the frame timeline of
@@ -1287,6 +1494,15 @@ struct Console {
             bool act = !parked;
             if (act && (j >= end || tgt > slice)) { parked = true; act = false; }
             if (act && tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; act = false; }
+            {   // one console left to run instructions and no catch-up asked for: its run of lone instructions
+                const uint64_t go = __ballot(act);
+                const uint64_t env = PART_LANES << (__builtin_ctzll(go | (1ull << 63)) & (ENVS_PER_WAVE - 1));
+                if (go && !(go & ~env) && !__any(want >= 0)) {
+                    uint32_t ran = 0;
+                    if (act) ran = lone_run(end, slice);
+                    if (__any(ran != 0)) continue;
+                }
+            }
             // PRG bytes pc .. pc + 6 for the fast paths, from three aligned LDS words and two byte-aligns (the
             // words past the last PRG word are the staged CHR bank's first ones: in bounds, and the bytes taken
             // from them are not used); the idle check reads 0xff past 0xffff
