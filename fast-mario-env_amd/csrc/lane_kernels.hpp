@@ -47,6 +47,37 @@ __host__ __device__ inline void area_tables(AreaTables* T) {
     area_taps(240, 84, T->ys, T->yw, T->yn);
 }
 
+// The first source column of each output column's taps, at compile time: area_taps(256, 84)'s steps for the
+// start index (the same double operations; ceil and floor of non-negative values by truncation), so that a
+// kernel can address a column's pixels with constant word and byte indices. The library checks at start-up that
+// they equal the run-time tables' (x_cols_match()); the taps of a column are at most 4 consecutive pixels.
+struct XCols { int x0[84]; };
+constexpr XCols x_cols() {
+    XCols r{};
+    const double scale = 1.0 / ((double)84 / 256);
+    for (int d = 0; d < 84; d++) {
+        const double f1 = d * scale, f2 = f1 + scale;
+        int s1 = (int)f1;
+        if ((double)s1 < f1) s1++;
+        int s2 = (int)f2;
+        if (s2 > 255) s2 = 255;
+        if (s1 > s2) s1 = s2;
+        r.x0[d] = s1 - f1 > 1e-3 ? s1 - 1 : s1;
+    }
+    return r;
+}
+constexpr XCols kXCols = x_cols();
+inline bool x_cols_match(const AreaTables& T) {
+    for (int d = 0; d < 84; d++) {
+        if (T.xs[d * TAPS] != kXCols.x0[d] || T.xn[d] < 1 || T.xn[d] > 4) return false;
+        for (int k = 1; k < T.xn[d]; k++)
+            if (T.xs[d * TAPS + k] != kXCols.x0[d] + k) return false;
+        for (int k = T.xn[d]; k < 4; k++)
+            if (T.xw[d * TAPS + k] != 0.f) return false;
+    }
+    return true;
+}
+
 __device__ __forceinline__ uint8_t round_sat(float v) {
     float r = __builtin_rintf(v);           // round half to even, like lrintf
     int iv = (int)r;
@@ -92,82 +123,67 @@ __device__ __forceinline__ uint32_t max_u8x4(uint32_t a, uint32_t b) {
     const uint32_t k0 = t0 - (t0 >> 8), k1 = t1 - (t1 >> 8);
     return ((a0 & k0) | (b0 & ~k0)) | (((a1 & k1) | (b1 & ~k1)) << 8);
 }
-__device__ __forceinline__ uint32_t pick4(const uint32_t (&m)[4], uint32_t i) {
-    return i == 0 ? m[0] : i == 1 ? m[1] : i == 2 ? m[2] : m[3];
+// ---- INTER_AREA of a staged source row, by column groups (k_obs)
+constexpr int OBS_COLS = 24;   // output columns one row-sum call covers: 20 G .. 20 G + 23
+
+// The horizontal sums of one source row for output columns 20 G .. 20 G + 23 of one env: word i of the row
+// (pixels 4 i .. 4 i + 3, max-pooled if the env pools) at rw[i * stride + lane]; xw[c]: column c's 4 tap
+// weights (+0 past its tap count). The words these columns' taps cover are read once, and every tap is a
+// constant byte of one of them (kXCols). Always 4 taps: adding +0 * pixel leaves the non-negative sum
+// unchanged, bit for bit, and the pixel is still inside the row.
+template <int G>
+__device__ __forceinline__ void obs_row_sums(const uint32_t* rw, uint32_t stride, uint32_t lane, const float (*xw)[4],
+                                             float (&rs)[OBS_COLS]) {
+    constexpr int c0 = 20 * G, wlo = kXCols.x0[c0] >> 2, whi = (kXCols.x0[c0 + OBS_COLS - 1] + 3) >> 2;
+    constexpr int NW = whi - wlo + 1;
+    static_assert(G >= 0 && G <= 3 && c0 + OBS_COLS <= 84 && whi < 64, "columns and taps inside the row");
+    uint32_t wv[NW];
+#pragma unroll
+    for (int i = 0; i < NW; i++) wv[i] = rw[(uint32_t)(wlo + i) * stride + lane];
+#pragma unroll
+    for (int q = 0; q < OBS_COLS; q++) {
+        const int c = c0 + q;
+        float row = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int px = kXCols.x0[c] + k;
+            row += (float)((wv[(px >> 2) - wlo] >> (8 * (px & 3))) & 0xffu) * xw[c][k];
+        }
+        rs[q] = row;
+    }
+}
+__device__ __forceinline__ void obs_row_sums(int g, const uint32_t* rw, uint32_t stride, uint32_t lane,
+                                             const float (*xw)[4], float (&rs)[OBS_COLS]) {
+    switch (g) {
+        case 0: obs_row_sums<0>(rw, stride, lane, xw, rs); break;
+        case 1: obs_row_sums<1>(rw, stride, lane, xw, rs); break;
+        case 2: obs_row_sums<2>(rw, stride, lane, xw, rs); break;
+        default: obs_row_sums<3>(rw, stride, lane, xw, rs); break;
+    }
 }
 
-// INTER_AREA output columns 4 chunk .. 4 chunk + 3 of one image of a frame buffer (4-pixel words, word w of
-// lane e at w np + e), max-pooled with a second one if `pool`: out[dy * row_stride + q * col_stride] =
-// output pixel (dy, 4 chunk + q). The float operations and their order are area_pixel's. The four
-// columns' taps (at most 4 consecutive source pixels each) lie in 4 consecutive words of a source row, so
-// a row is 4 word loads per image; a source row shared by two output rows is summed once. Output rows
-// dy0 .. dy1-1 only (a band; out still addresses row 0). The words of source row sy + 1 are loaded while
-// row sy is summed: the distinct source rows of consecutive output rows are consecutive.
-__device__ __forceinline__ void area_columns4(const uint32_t* g0, const uint32_t* g1, uint32_t np, uint32_t e,
-                                              bool pool, int chunk, const AreaTables* T, uint32_t* out,
-                                              size_t row_stride, int dy0 = 0, int dy1 = 84) {
-    const int c0 = 4 * chunk;
-    const uint32_t wl = (uint32_t)T->xs[c0 * TAPS] >> 2;
-    int nx[4];
-    uint32_t iq[4], sh[4];
-    float w[4][4];
+// The vertical step for source row sy: every (output row dy, tap j) from the current (dy, j) on, up to output
+// row dy_end, that takes row sy, in order (consecutive output rows take consecutive source rows, the one they
+// share summed once); emit(dy, acc) when output row dy is complete.
+template <class Emit>
+__device__ __forceinline__ void obs_rows_take(int sy, int& dy, int& j, int dy_end, const int32_t* ys, const float* yw,
+                                              const int32_t* yn, const float (&rs)[OBS_COLS], float (&acc)[OBS_COLS],
+                                              Emit&& emit) {
+    while (dy < dy_end && ys[dy * TAPS + j] == sy) {
+        const float w = yw[dy * TAPS + j];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const uint32_t rel = (uint32_t)T->xs[(c0 + q) * TAPS] - 4 * wl;
-        nx[q] = T->xn[c0 + q];
-        iq[q] = rel >> 2;
-        sh[q] = (rel & 3) * 8;
-#pragma unroll
-        for (int k = 0; k < 4; k++) w[q][k] = T->xw[(c0 + q) * TAPS + k];
-    }
-    float acc[4] = {0.f, 0.f, 0.f, 0.f}, rs[4] = {0.f, 0.f, 0.f, 0.f};
-    int last_sy = -1;
-    // the source row's four words (max-pooled when pool) at row sy
-    auto row_words = [&](int sy, uint32_t* m) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const size_t wi = (size_t)((uint32_t)sy * 64 + (wl + i < 63 ? wl + i : 63)) * np + e;
-            m[i] = pool ? max_u8x4(g0[wi], g1[wi]) : g0[wi];
+        for (int q = 0; q < OBS_COLS; q++) {
+            const float term = w * rs[q];
+            acc[q] = j == 0 ? term : acc[q] + term;
         }
-    };
-    int pf_sy = T->ys[dy0 * TAPS];           // the row held in pm
-    uint32_t pm[4];
-    row_words(pf_sy, pm);
-    for (int dy = dy0; dy < dy1; dy++) {
-        const int ny = T->yn[dy];
-        for (int j = 0; j < ny; j++) {
-            const int sy = T->ys[dy * TAPS + j];
-            if (sy != last_sy) {
-                uint32_t m[4];
-                if (sy == pf_sy) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) m[i] = pm[i];
-                } else {
-                    row_words(sy, m);
-                }
-                if (sy + 1 < 240) { pf_sy = sy + 1; row_words(pf_sy, pm); }
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint64_t win = ((uint64_t)pick4(m, iq[q] < 3 ? iq[q] + 1 : 3) << 32 | pick4(m, iq[q])) >> sh[q];
-                    float row = 0.f;
-#pragma unroll
-                    for (int k = 0; k < 4; k++)
-                        if (k < nx[q]) row += (float)(uint32_t)((win >> (8 * k)) & 0xffu) * w[q][k];
-                    rs[q] = row;
-                }
-                last_sy = sy;
-            }
-            const float yw = T->yw[dy * TAPS + j];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float term = yw * rs[q];
-                acc[q] = j == 0 ? term : acc[q] + term;
-            }
-        }
-        // the four output pixels of the row as one word (pixel 4 chunk + q in byte q)
-        out[(size_t)dy * row_stride] = (uint32_t)round_sat(acc[0]) | (uint32_t)round_sat(acc[1]) << 8 |
-                                       (uint32_t)round_sat(acc[2]) << 16 | (uint32_t)round_sat(acc[3]) << 24;
+        if (++j == yn[dy]) { emit(dy); dy++; j = 0; }
     }
+}
+
+// output pixels 4 wq .. 4 wq + 3 of a column group as one word (pixel 4 wq + i in byte i)
+__device__ __forceinline__ uint32_t obs_word(const float (&acc)[OBS_COLS], int wq) {
+    return (uint32_t)round_sat(acc[4 * wq]) | (uint32_t)round_sat(acc[4 * wq + 1]) << 8 |
+           (uint32_t)round_sat(acc[4 * wq + 2]) << 16 | (uint32_t)round_sat(acc[4 * wq + 3]) << 24;
 }
 
 // ------------------------------------------------------------------ arguments

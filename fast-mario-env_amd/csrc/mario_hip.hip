@@ -154,28 +154,90 @@ struct ObsArgs {
 // New observation of every env: the boot observation right after a reset, else INTER_AREA of the last
 // frame, max-pooled with its partner frame (fastmario.cpp:377-386). E_POOLED bit 0: pool; bit 1: the
 // last frame is in frame buffer 1 (the episode ended at an agent frame of the other parity than K-1).
-// Threads: x = env (64 per block), y = a chunk of 4 output columns (3 per block, 7 blocks per env group);
-// the grid's x walks the chunks of one env group first, so the source words they share are still in the L2.
-constexpr int OBS_BAND_ROWS = 21;   // output rows per k_obs workgroup: 4 bands, 4x the loads in flight
-__global__ void __launch_bounds__(192) k_obs(ObsArgs A) {
-    const uint32_t e = blockIdx.y * 64 + (threadIdx.x & 63);
-    const int chunk = blockIdx.x * 3 + (threadIdx.x >> 6);
-    if (e >= (uint32_t)A.n || chunk >= 21) return;
-    uint32_t* out = (uint32_t*)A.out + (size_t)chunk * A.np + e;   // word (row, chunk): pixels 4 chunk .. + 3
-    const size_t row_stride = (size_t)21 * A.np;
-    const int dy0 = OBS_BAND_ROWS * blockIdx.z, dy1 = dy0 + OBS_BAND_ROWS;   // this workgroup's output rows
-    if (A.ev[(size_t)E_SHOWS_BOOT * A.np + e]) {
-        const uint8_t* src = A.boot_obs + (size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX + 4 * chunk;
-        for (int dy = dy0; dy < dy1; dy++)
-            out[(size_t)dy * row_stride] = (uint32_t)src[dy * 84] | (uint32_t)src[dy * 84 + 1] << 8 |
-                                           (uint32_t)src[dy * 84 + 2] << 16 | (uint32_t)src[dy * 84 + 3] << 24;
-        return;
+// Block: 64 envs (a wave's lanes) x a band of OBS_BAND_ROWS output rows; wave g sums output columns
+// 20 g .. 20 g + 23 and stores 20 g .. 20 g + 19 (wave 3: all 24, 60 .. 83). The band's source rows are staged in LDS one at a time, double
+// buffered: all 256 threads load a row's 64 words of the 64 envs (each load 64 consecutive envs' word, 256
+// contiguous bytes), max-pool them and store them, and while row sy is summed from LDS the loads of row
+// sy + 1 are in flight. Every source byte is read from HBM once. The float operations and their order are
+// area_pixel's: per source row and column the taps in order, per output row the source rows in order, a
+// source row shared by two output rows summed once.
+constexpr int OBS_BAND_ROWS = 21;   // output rows per block: 4 bands
+__global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
+    __shared__ uint32_t srow[2][64 * 64];          // [buffer][word * 64 + env]: one source row of the 64 envs
+    __shared__ int32_t s_ys[84 * TAPS], s_yn[84];
+    __shared__ __attribute__((aligned(16))) float s_xw[84][4];   // a column's 4 tap weights (+0 past its tap count)
+    __shared__ float s_yw[84 * TAPS];   // (in LDS: a table load from memory would wait for the row loads)
+    const int lane = threadIdx.x & 63, g = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t e = blockIdx.x * 64 + lane;       // < np: the buffers hold np lanes
+    const int dy0 = OBS_BAND_ROWS * blockIdx.y, dy1 = dy0 + OBS_BAND_ROWS;
+    const AreaTables* T = A.T;
+    for (int i = threadIdx.x; i < 84; i += 256) {
+        s_yn[i] = T->yn[i];
+        for (int k = 0; k < 4; k++) s_xw[i][k] = T->xw[i * TAPS + k];
     }
+    for (int i = threadIdx.x; i < 84 * TAPS; i += 256) { s_ys[i] = T->ys[i]; s_yw[i] = T->yw[i]; }
+    // this thread's loads: words 16 g .. 16 g + 15 of a row of env e
     const uint32_t pw = A.ev[(size_t)E_POOLED * A.np + e];
-    const uint32_t* g0 = (const uint32_t*)A.gray;
-    const uint32_t* g1 = (const uint32_t*)(A.gray + (size_t)GRAY_PIX * A.np);
-    if (pw & 2) { const uint32_t* t = g0; g0 = g1; g1 = t; }
-    area_columns4(g0, g1, A.np, e, (pw & 1) != 0, chunk, A.T, out, row_stride, dy0, dy1);
+    const bool pool = (pw & 1) != 0;
+    const uint32_t* gl = (const uint32_t*)(A.gray + ((pw & 2) ? (size_t)GRAY_PIX * A.np : 0));   // the last frame
+    const uint32_t* gp = (const uint32_t*)(A.gray + ((pw & 2) ? 0 : (size_t)GRAY_PIX * A.np));   // its partner
+    // the loads land in la / lb and are max-pooled only when stored, so that they stay in flight while the
+    // previous row is summed
+    // (both buffers hold np lanes whether or not the env pools, so the wave loads both when any lane pools)
+    uint32_t la[16], lb[16];
+    const bool any_pool = __any(pool);
+    auto load_row = [&](int sy) {
+        const size_t w0 = (size_t)((uint32_t)sy * 64 + 16 * g) * A.np + e;
+        if (any_pool) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) { la[i] = gl[w0 + (size_t)i * A.np]; lb[i] = gp[w0 + (size_t)i * A.np]; }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) { la[i] = gl[w0 + (size_t)i * A.np]; lb[i] = 0u; }
+        }
+    };
+    auto store_row = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) srow[buf][(16 * g + i) * 64 + lane] = pool ? max_u8x4(la[i], lb[i]) : la[i];
+    };
+    // every wave sums 24 columns from 20 g (waves 0-2 also sum the next wave's first 4, and do not store them)
+    const int c0 = 20 * g, nw = g == 3 ? 6 : 5;
+    float acc[OBS_COLS], rs[OBS_COLS];
+#pragma unroll
+    for (int q = 0; q < OBS_COLS; q++) { acc[q] = 0.f; rs[q] = 0.f; }
+    const int sy_lo = T->ys[dy0 * TAPS], sy_hi = T->ys[(dy1 - 1) * TAPS + T->yn[dy1 - 1] - 1];
+    load_row(sy_lo);
+    store_row(0);
+    __syncthreads();
+    const bool boot = A.ev[(size_t)E_SHOWS_BOOT * A.np + e] != 0;
+    const uint8_t* bsrc = A.boot_obs + (size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX;
+    int dy = dy0, j = 0;
+    for (int sy = sy_lo; sy <= sy_hi; sy++) {
+        const int buf = (sy - sy_lo) & 1;
+        if (sy < sy_hi) load_row(sy + 1);
+        // the row's horizontal sums of this wave's columns, then the output rows that take the row
+        obs_row_sums(g, srow[buf], 64, lane, s_xw, rs);
+        obs_rows_take(sy, dy, j, dy1, s_ys, s_yw, s_yn, rs, acc, [&](int d) {
+            // the output row's words of this wave's columns: word (d, c / 4) of env e at [(d * 21 + c / 4) * np + e]
+            if (e >= (uint32_t)A.n) return;
+            uint32_t* out = (uint32_t*)A.out + ((size_t)d * 21 + c0 / 4) * A.np + e;
+#pragma unroll
+            for (int wq = 0; wq < OBS_COLS / 4; wq++) {
+                if (wq < nw) {
+                    uint32_t v;
+                    if (boot) {
+                        const uint8_t* b = bsrc + d * 84 + c0 + 4 * wq;
+                        v = (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24;
+                    } else {
+                        v = obs_word(acc, wq);
+                    }
+                    out[(size_t)wq * A.np] = v;
+                }
+            }
+        });
+        if (sy < sy_hi) store_row(buf ^ 1);
+        __syncthreads();
+    }
 }
 
 struct StackArgs {
@@ -498,6 +560,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     if (!good) return fail();
     AreaTables T;
     area_tables(&T);
+    if (!x_cols_match(T)) { g_err = "INTER_AREA column taps differ from the compiled-in positions"; return fail(); }
     // per-env words: level, RNG, lives = -1 (reset() installs the real start state)
     std::vector<uint32_t> ev((size_t)E_COUNT * h->np, 0);
     for (int i = 0; i < n; i++) {
@@ -614,7 +677,7 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
     ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
-    hipLaunchKernelGGL(k_obs, dim3(7, h->np / 64, 84 / OBS_BAND_ROWS), dim3(192), 0, s, oa);
+    hipLaunchKernelGGL(k_obs, dim3(h->np / 64, 84 / OBS_BAND_ROWS), dim3(256), 0, s, oa);
     CK(hipGetLastError());
     if (mark(h, s, 2)) return -1;
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(0));

@@ -274,24 +274,40 @@ int run_env(const char* cfg_file) {
             }
         }
     };
-    // k_obs: the boot observation right after a reset, else INTER_AREA of the last frame, max-pooled
+    // k_obs: the boot observation right after a reset, else INTER_AREA of the last frame, max-pooled; the
+    // kernel's row sums and vertical steps, each source row staged as 64 words (stride 1) instead of in LDS
+    float xw[84][4];
+    for (int c = 0; c < 84; c++)
+        for (int k = 0; k < 4; k++) xw[c][k] = v.T.xw[c * TAPS + k];
     auto do_obs = [&]() {
         for (int e = 0; e < n; e++) {
-            for (int chunk = 0; chunk < 21; chunk++) {
-                uint32_t* out = (uint32_t*)v.fresh.data() + (size_t)chunk * np + e;
-                const size_t row_stride = (size_t)21 * np;
-                if (v.ev[(size_t)E_SHOWS_BOOT * np + e]) {
-                    const uint8_t* src = v.boot_obs.data() + (size_t)v.ev[(size_t)E_LEVEL * np + e] * OBS_PIX + 4 * chunk;
-                    for (int dy = 0; dy < 84; dy++)
-                        out[(size_t)dy * row_stride] = (uint32_t)src[dy * 84] | (uint32_t)src[dy * 84 + 1] << 8 |
-                                                       (uint32_t)src[dy * 84 + 2] << 16 | (uint32_t)src[dy * 84 + 3] << 24;
-                    continue;
+            uint32_t* fresh = (uint32_t*)v.fresh.data();
+            if (v.ev[(size_t)E_SHOWS_BOOT * np + e]) {
+                const uint8_t* src = v.boot_obs.data() + (size_t)v.ev[(size_t)E_LEVEL * np + e] * OBS_PIX;
+                for (int w = 0; w < OBS_PIX / 4; w++) {
+                    const uint8_t* b = src + 4 * w;
+                    fresh[(size_t)w * np + e] = (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24;
                 }
-                const uint32_t pw = v.ev[(size_t)E_POOLED * np + e];
-                const uint32_t* g0 = (const uint32_t*)v.gray.data();
-                const uint32_t* g1 = (const uint32_t*)(v.gray.data() + (size_t)GRAY_PIX * np);
-                if (pw & 2) { const uint32_t* t = g0; g0 = g1; g1 = t; }
-                area_columns4(g0, g1, np, (uint32_t)e, (pw & 1) != 0, chunk, &v.T, out, row_stride, 0, 84);
+                continue;
+            }
+            const uint32_t pw = v.ev[(size_t)E_POOLED * np + e];
+            const uint32_t* gl = (const uint32_t*)(v.gray.data() + ((pw & 2) ? (size_t)GRAY_PIX * np : 0));
+            const uint32_t* gp = (const uint32_t*)(v.gray.data() + ((pw & 2) ? 0 : (size_t)GRAY_PIX * np));
+            for (int g = 0; g < 4; g++) {
+                float acc[OBS_COLS] = {}, rs[OBS_COLS];
+                int dy = 0, j = 0;
+                const int c0 = 20 * g, nw = g == 3 ? 6 : 5;
+                for (int sy = 0; sy < 240; sy++) {
+                    uint32_t row[64];
+                    for (int i = 0; i < 64; i++) {
+                        const size_t wi = (size_t)(sy * 64 + i) * np + e;
+                        row[i] = (pw & 1) ? max_u8x4(gl[wi], gp[wi]) : gl[wi];
+                    }
+                    obs_row_sums(g, row, 1, 0, xw, rs);
+                    obs_rows_take(sy, dy, j, 84, v.T.ys, v.T.yw, v.T.yn, rs, acc, [&](int d) {
+                        for (int wq = 0; wq < nw; wq++) fresh[((size_t)d * 21 + c0 / 4 + wq) * np + e] = obs_word(acc, wq);
+                    });
+                }
             }
         }
     };
