@@ -1497,10 +1497,10 @@ struct Console {
             {   // one console left to run instructions and no catch-up asked for: its run of lone instructions
                 const uint64_t go = __ballot(act);
                 const uint64_t env = PART_LANES << (__builtin_ctzll(go | (1ull << 63)) & (ENVS_PER_WAVE - 1));
+                // (a run of at least one instruction is this iteration's action: no early `continue`, whose
+                // extra path into the loop top would make the compiler merge the console state there)
                 if (go && !(go & ~env) && !__any(want >= 0)) {
-                    uint32_t ran = 0;
-                    if (act) ran = lone_run(end, slice);
-                    if (__any(ran != 0)) continue;
+                    if (act && lone_run(end, slice) != 0) act = false;
                 }
             }
             // PRG bytes pc .. pc + 6 for the fast paths, from three aligned LDS words and two byte-aligns (the
