@@ -199,6 +199,7 @@ struct RomArgs {
 __device__ __forceinline__ Cart make_cart(const RomArgs& R, const uint8_t* s_rom, const uint32_t* s_dec) {
     Cart c;
     c.prg = s_rom;
+    c.gprg = R.rom;
     c.chr = s_rom + 0x8000;
     c.dec = s_dec;
     c.nt_bits = R.nt_bits;

@@ -210,8 +210,15 @@ struct Table {
 __device__ __constant__ static const dec::Table kDecode{};
 
 // Read-only cartridge view: PRG/CHR in LDS, name-table offsets in registers (uniform).
+// Pointers through which wave-uniform addresses of read-only data are loaded with scalar loads (the constant
+// address space): the PRG image in device memory, which no kernel writes.
+#ifndef MH_SCALAR_CONST
+#define MH_SCALAR_CONST __attribute__((address_space(4)))
+#endif
+
 struct Cart {
     const uint8_t* prg;      // 0x8000 bytes (16 KB images mirrored)
+    const uint8_t* gprg;     // the same PRG image in device memory (scalar loads of wave-uniform addresses)
     const uint8_t* chr;      // 0x2000 bytes
     const uint32_t* dec;     // decode words (LDS copy of kDecode)
     uint32_t nt_bits;        // bit k set: name table k ($2000 + k * $400) maps to VRAM $400, else to $000
@@ -1223,12 +1230,13 @@ struct Console {
             if (tgt >= nmi && calls < tgt) break;               // frame() catches up first
             if (upc < 0x8000u || upc > 0xfffdu) break;          // opcode or operands through the bus
             const uint32_t pa = upc & 0x7fffu;
-            const uint32_t* pw = (const uint32_t*)cart.prg + (pa >> 2);
-            const uint64_t w = (uint64_t)uniform(pw[1]) << 32 | uniform(pw[0]);
+            // opcode, operands and decode word by scalar loads (a wave-uniform address; no LDS round trip)
+            const MH_SCALAR_CONST uint32_t* pw = (const MH_SCALAR_CONST uint32_t*)(const void*)cart.gprg + (pa >> 2);
+            const uint64_t w = (uint64_t)pw[1] << 32 | pw[0];
             const uint32_t b0 = (uint32_t)(w >> (8 * (pa & 3u)));                // bytes pc .. pc + 3
             const uint32_t op = b0 & 0xffu, b1 = (b0 >> 8) & 0xffu, b2 = (b0 >> 16) & 0xffu, absv = b1 | b2 << 8;
             if (op == 0x4cu && absv == upc) break;               // JMP *: frame()'s idle fast-forward
-            const uint32_t D = uniform(cart.dec[op]);
+            const uint32_t D = kDecode.w[op];
             if (!(D & OK)) break;                               // invalid opcode: frame() counts it
             const uint32_t am = D & 15u, alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, dst = (D >> DST_SH) & 7u;
             const uint32_t xop = (D >> X_SH) & 15u, fl = (D >> FL_SH) & 7u;

@@ -15,6 +15,8 @@
 #define __global__
 #define __constant__
 #define __forceinline__ inline __attribute__((always_inline))
+// host memory has one address space
+#define MH_SCALAR_CONST
 
 // a one-lane wave
 static inline unsigned __lane_id() { return 0u; }
