@@ -386,6 +386,47 @@ static bool load_cart(const uint8_t* d, int64_t n, std::vector<uint8_t>& img, ui
     return true;
 }
 
+// ---- the PPO policy's input (the rollout harness's observation -> bf16 channels-last scaling)
+// Observation stacks (n, k, 84, 84) u8 -> the bf16 (n, k, 84, 84) tensor in channels-last memory, i.e. element
+// (b, c, h, w) at ((b * 84 + h) * 84 + w) * k + c, of value bf16(float(v) * float(1 / 255)) rounded to nearest
+// even: what torch's float32 scaling followed by the bf16 cast gives. Thread: 4 consecutive pixels of one row of
+// one image, all k channels (k u32 loads of 4 pixels, then 4 k bf16 values stored as 32-bit pairs).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {   // f finite and >= 0
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+template <int K>
+__global__ void __launch_bounds__(256) k_policy_input(const uint8_t* obs, uint32_t* out, int64_t groups) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= groups) return;
+    const int64_t b = t / (OBS_PIX / 4);
+    const int r = (int)(t - b * (OBS_PIX / 4));          // pixel group in the image: pixels 4 r .. 4 r + 3
+    const float s = (float)(1.0 / 255.0);
+    uint32_t v[K];
+#pragma unroll
+    for (int c = 0; c < K; c++) v[c] = ((const uint32_t*)obs)[(b * K + c) * (OBS_PIX / 4) + r];
+    // pixel q of the group: its K channels at out halves (4 r + q) * K .. + K - 1 of image b
+    uint32_t* o = out + (b * OBS_PIX + 4 * r) * K / 2;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int c = 0; c < K; c += 2) {
+            const uint32_t lo = bf16_rne((float)((v[c] >> (8 * q)) & 0xffu) * s);
+            const uint32_t hi = c + 1 < K ? bf16_rne((float)((v[c + 1] >> (8 * q)) & 0xffu) * s) : 0u;
+            o[(q * K + c) / 2] = lo | hi << 16;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) k_policy_input_k1(const uint8_t* obs, uint32_t* out, int64_t groups) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= groups) return;
+    const float s = (float)(1.0 / 255.0);
+    const uint32_t v = ((const uint32_t*)obs)[t];
+    out[2 * t] = bf16_rne((float)(v & 0xffu) * s) | bf16_rne((float)((v >> 8) & 0xffu) * s) << 16;
+    out[2 * t + 1] = bf16_rne((float)((v >> 16) & 0xffu) * s) | bf16_rne((float)(v >> 24) * s) << 16;
+}
+
 }  // namespace
 
 // compute units of a device (the emulator kernels' launch shape depends on it)
@@ -911,6 +952,29 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
         }
     }
     hipLaunchKernelGGL(k_resize_images, dim3((OBS_PIX + 255) / 256, n), dim3(256), 0, (hipStream_t)stream, d_src, d_dst, n, d_T);
+    CK(hipGetLastError());
+    return 0;
+}
+
+int mh_policy_input(const uint8_t* d_obs, void* d_out, int64_t n, int k, void* stream) {
+    if (!d_obs || !d_out || n < 1 || (k != 1 && k != 2 && k != 4 && k != 8)) {
+        g_err = "invalid arguments (n >= 1, k in 1, 2, 4, 8)";
+        return -1;
+    }
+    if ((((uintptr_t)d_obs) & 3) || (((uintptr_t)d_out) & 3)) { g_err = "obs and out must be 4-byte aligned"; return -1; }
+    const int64_t groups = n * (OBS_PIX / 4);
+    const dim3 grid((unsigned)((groups + 255) / 256));
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t* o = (uint32_t*)d_out;
+    if (k == 1) {   // one channel: two pixels per 32-bit word
+        hipLaunchKernelGGL(k_policy_input_k1, grid, dim3(256), 0, s, d_obs, o, groups);
+    } else if (k == 2) {
+        hipLaunchKernelGGL(k_policy_input<2>, grid, dim3(256), 0, s, d_obs, o, groups);
+    } else if (k == 4) {
+        hipLaunchKernelGGL(k_policy_input<4>, grid, dim3(256), 0, s, d_obs, o, groups);
+    } else {
+        hipLaunchKernelGGL(k_policy_input<8>, grid, dim3(256), 0, s, d_obs, o, groups);
+    }
     CK(hipGetLastError());
     return 0;
 }

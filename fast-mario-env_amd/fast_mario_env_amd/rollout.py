@@ -32,6 +32,21 @@ def _torch():
     return torch
 
 
+def policy_input(obs_u8, out):
+    """Scale uint8 (B, k, 84, 84) observation stacks into `out`, a bf16 (B, k, 84, 84) channels-last tensor on the
+    same GPU: bf16(float(v) * float(1/255)), rounded to nearest even, by the library's HIP kernel."""
+    torch = _torch()
+    from ._native import check, lib
+    if (obs_u8.dtype != torch.uint8 or out.dtype != torch.bfloat16 or tuple(obs_u8.shape) != tuple(out.shape)
+            or obs_u8.dim() != 4 or tuple(obs_u8.shape[2:]) != (84, 84) or not obs_u8.is_contiguous()
+            or not out.is_contiguous(memory_format=torch.channels_last) or obs_u8.device != out.device):
+        raise ValueError("policy_input: needs a contiguous uint8 (B, k, 84, 84) tensor and a bf16 channels-last "
+                         "tensor of the same shape on the same GPU")
+    check(lib().mh_policy_input(obs_u8.data_ptr(), out.data_ptr(), obs_u8.shape[0], obs_u8.shape[1],
+                                torch.cuda.current_stream(obs_u8.device).cuda_stream), "mh_policy_input")
+    return out
+
+
 def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="cuda"):
     """The Nature-CNN actor-critic with the reference's architecture and initialisation, random weights."""
     torch = _torch()
@@ -66,12 +81,13 @@ def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="
         def forward(self, obs_u8):
             """uint8 (B, 4, 84, 84) -> logits f32 (B, A), value f32 (B,).
 
-            On the GPU the observation is scaled in one op straight into a bf16 channels-last buffer:
-            bf16(float(v) * float(1/255)), the value autocast gives the float32 scaling of the CPU path, without
-            the float32 intermediate (4x the observation's bytes). Calls of one batch shape share the buffer."""
+            On the GPU the observation is scaled by one HIP kernel straight into a bf16 channels-last buffer
+            (mh_policy_input): bf16(float(v) * float(1/255)), the value autocast gives the float32 scaling of the
+            CPU path, without the float32 intermediate (4x the observation's bytes). Calls of one batch shape
+            share the buffer."""
             if obs_u8.is_cuda:
                 x = self._input(obs_u8.shape, obs_u8.device)
-                torch.mul(obs_u8, 1.0 / 255.0, out=x)
+                policy_input(obs_u8, x)
             else:
                 x = obs_u8.float().mul_(1.0 / 255.0)
             with torch.autocast("cuda", dtype=torch.bfloat16, enabled=x.is_cuda):

@@ -152,6 +152,15 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
  * A call on another stream that overlaps the first call on the same GPU races with the tables' set-up. */
 int mh_resize_noalloc(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
+/* ---- the PPO rollout harness's policy input
+ * No counterpart in the reference's C ABI: the device step of its PPO trainer scales the observation with torch
+ * (ppo/backends.py:127-162, ppo/model.py:13-38: obs.float() / 255 feeding a Nature CNN); this is that scaling
+ * written for the bf16 channels-last input the harness's convolutions take.
+ * d_obs: (n, k, 84, 84) uint8 stacks, contiguous; d_out: the (n, k, 84, 84) bf16 tensor in channels-last
+ * memory (element (b, c, h, w) at ((b * 84 + h) * 84 + w) * k + c), of value bf16(float(v) * float(1 / 255))
+ * rounded to nearest even. k in 1, 2, 4, 8; both pointers 4-byte aligned; -1 otherwise. */
+int mh_policy_input(const uint8_t* d_obs, void* d_out, int64_t n, int k, void* stream);
+
 /* ---- frame-deduplicating replay ring (device storage owned by the caller)
  * The ring of FrameReplay (src/fast_mario_env/replay.py:43-60) for n_envs envs and `capacity` slots each,
  * all device memory, slot s of env e at index e * capacity + s:

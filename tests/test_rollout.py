@@ -126,6 +126,24 @@ def test_rollout_vs_oracle():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("k,n", [(4, 97), (1, 5), (2, 3), (8, 2)])
+def test_policy_input_kernel_matches_torch_scaling(k, n):
+    # mh_policy_input against torch's own float32 scaling cast to bf16 (round to nearest even), bit for bit,
+    # into a channels-last buffer; every byte value occurs
+    from fast_mario_env_amd.rollout import policy_input
+    g = torch.Generator(device="cuda").manual_seed(k)
+    obs = torch.randint(0, 256, (n, k, 84, 84), dtype=torch.uint8, device="cuda", generator=g)
+    obs.view(-1)[:256] = torch.arange(256, dtype=torch.uint8, device="cuda")
+    out = torch.full((n, k, 84, 84), float("nan"), dtype=torch.bfloat16, device="cuda").to(memory_format=torch.channels_last)
+    policy_input(obs, out)
+    ref = (obs.float() * (1.0 / 255.0)).to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), ref.contiguous(memory_format=torch.channels_last).view(torch.int16))
+    assert torch.equal(out.contiguous().view(torch.int16), ref.view(torch.int16))
+    with pytest.raises(ValueError):
+        policy_input(obs, out.contiguous() if k > 1 else out.float())   # NCHW (or float) output refused
+
+
+@pytest.mark.gpu
 def test_policy_input_path_matches_float_scaling():
     # the GPU forward scales the uint8 observation straight into bf16 channels-last; it must give exactly what
     # the plain float32 scaling under bf16 autocast gives (plain PyTorch, NCHW)
