@@ -427,6 +427,73 @@ __global__ void __launch_bounds__(256) k_policy_input_k1(const uint8_t* obs, uin
     out[2 * t + 1] = bf16_rne((float)((v >> 16) & 0xffu) * s) | bf16_rne((float)(v >> 24) * s) << 16;
 }
 
+// ---- the PPO policy's first convolution (Nature CNN: 4 -> 32 channels, 8x8 kernel, stride 4, 84x84 -> 20x20)
+// fused with the input scaling, the bias and the ReLU, on the matrix cores: relu(conv(bf16(obs / 255), W) + b)
+// as an implicit GEMM, M = output pixels, N = 32 channels, K = 4 x 8 x 8 = 256 in the weight's own (ci, kh, kw)
+// order, one v_mfma_f32_32x32x16_bf16 per 16 of K with float32 accumulation.
+// A wave holds the whole weight matrix in registers (lane l: output channel l % 32, k = 16 s + 8 (l / 32) ..
+// + 7 of step s) and walks tiles of 32 output pixels: lane l's A operand of step s is input row 4 oy + kh of
+// channel ci, columns 4 ox .. 4 ox + 7 (two aligned u32 loads of 4 pixels) for pixel l % 32 of the tile,
+// scaled to bf16 as mh_policy_input scales it. Output: the (n, 32, 20, 20) bf16 tensor in channels-last memory
+// (pixel m's 32 channels at m * 32 ..), written as bf16(relu(acc + b)).
+typedef __bf16 mh_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float mh_f32x16 __attribute__((ext_vector_type(16)));
+constexpr int CONV1_OUT = 20 * 20;   // output pixels per image
+__global__ void __launch_bounds__(256) k_policy_conv1(const uint8_t* obs, const uint16_t* w, const uint16_t* bias,
+                                                      uint16_t* out, int64_t n) {
+    const int l = threadIdx.x & 63;
+    const int j = l & 31, kg = l >> 5;
+    // B operand of the 16 steps: W[j][16 s + 8 kg .. + 7] (OIHW, K = ci * 64 + kh * 8 + kw)
+    mh_bf16x8 wb[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const uint4 q = *(const uint4*)(w + (size_t)j * 256 + 16 * s + 8 * kg);
+        const uint32_t q4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) wb[s][e] = __builtin_bit_cast(__bf16, (uint16_t)(q4[e >> 1] >> (16 * (e & 1))));
+    }
+    const float bj = __uint_as_float((uint32_t)bias[j] << 16);
+    const float sc = (float)(1.0 / 255.0);
+    const int64_t M = n * CONV1_OUT, tiles = (M + 31) / 32;
+    const int64_t wave = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6, waves = (int64_t)gridDim.x * 4;
+    for (int64_t t = wave; t < tiles; t += waves) {
+        // this lane's A pixel: row l % 32 of the tile (clamped to the last pixel past the end; not stored)
+        int64_t m = t * 32 + j;
+        if (m >= M) m = M - 1;
+        const int64_t b = m / CONV1_OUT;
+        const int p = (int)(m - b * CONV1_OUT), oy = p / 20, ox = p - oy * 20;
+        const uint8_t* img = obs + (size_t)b * 4 * OBS_PIX + (size_t)(4 * oy) * 84 + 4 * ox;
+        uint32_t raw[16][2];
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const int k0 = 16 * s + 8 * kg, ci = k0 >> 6, kh = (k0 >> 3) & 7;
+            const uint32_t* r = (const uint32_t*)(img + (size_t)ci * OBS_PIX + kh * 84);
+            raw[s][0] = r[0];
+            raw[s][1] = r[1];
+        }
+        mh_f32x16 acc = {};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            mh_bf16x8 a;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t v = (raw[s][e >> 2] >> (8 * (e & 3))) & 0xffu;
+                a[e] = __builtin_bit_cast(__bf16, (uint16_t)bf16_rne((float)v * sc));
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, wb[s], acc, 0, 0, 0);
+        }
+        // D: register v holds output pixel 8 (v / 4) + 4 kg + v % 4 of the tile, channel j
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int64_t mo = t * 32 + 8 * (v >> 2) + 4 * kg + (v & 3);
+            if (mo < M) {
+                const float y = acc[v] + bj;
+                out[(size_t)mo * 32 + j] = (uint16_t)bf16_rne(y > 0.f ? y : 0.f);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // compute units of a device (the emulator kernels' launch shape depends on it)
@@ -952,6 +1019,23 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
         }
     }
     hipLaunchKernelGGL(k_resize_images, dim3((OBS_PIX + 255) / 256, n), dim3(256), 0, (hipStream_t)stream, d_src, d_dst, n, d_T);
+    CK(hipGetLastError());
+    return 0;
+}
+
+int mh_policy_conv1(const uint8_t* d_obs, const void* d_w, const void* d_b, void* d_out, int64_t n, void* stream) {
+    if (!d_obs || !d_w || !d_b || !d_out || n < 1) { g_err = "invalid arguments (n >= 1)"; return -1; }
+    if ((((uintptr_t)d_obs) & 3) || (((uintptr_t)d_w) & 15) || (((uintptr_t)d_out) & 1) || (((uintptr_t)d_b) & 1)) {
+        g_err = "obs must be 4-byte, weight 16-byte and bias / out 2-byte aligned";
+        return -1;
+    }
+    int dev = 0, cus = 0;
+    CK(hipGetDevice(&dev));
+    CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int64_t tiles = (n * CONV1_OUT + 31) / 32;
+    const int64_t blocks = std::min<int64_t>((tiles + 3) / 4, (int64_t)cus * 8);   // persistent: tiles per wave
+    hipLaunchKernelGGL(k_policy_conv1, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, d_obs,
+                       (const uint16_t*)d_w, (const uint16_t*)d_b, (uint16_t*)d_out, n);
     CK(hipGetLastError());
     return 0;
 }

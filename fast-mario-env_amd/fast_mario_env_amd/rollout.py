@@ -47,6 +47,29 @@ def policy_input(obs_u8, out):
     return out
 
 
+def policy_conv1(obs_u8, weight, bias, out=None):
+    """relu(conv2d(bf16(obs / 255), weight, bias, stride 4)) of the Nature CNN's first layer by the library's MFMA
+    kernel: obs uint8 (B, 4, 84, 84) contiguous on a GPU, weight (32, 4, 8, 8) and bias (32) in any float dtype
+    (taken as bf16, as autocast takes them); returns (or fills) a bf16 (B, 32, 20, 20) channels-last tensor."""
+    torch = _torch()
+    from ._native import check, lib
+    if (obs_u8.dtype != torch.uint8 or obs_u8.dim() != 4 or tuple(obs_u8.shape[1:]) != (4, 84, 84)
+            or not obs_u8.is_contiguous() or tuple(weight.shape) != (32, 4, 8, 8) or tuple(bias.shape) != (32,)):
+        raise ValueError("policy_conv1: needs a contiguous uint8 (B, 4, 84, 84) tensor, a (32, 4, 8, 8) weight and a "
+                         "(32,) bias")
+    w = weight.detach().to(device=obs_u8.device, dtype=torch.bfloat16).contiguous()
+    b = bias.detach().to(device=obs_u8.device, dtype=torch.bfloat16).contiguous()
+    n = obs_u8.shape[0]
+    if out is None:
+        out = torch.empty(n, 32, 20, 20, dtype=torch.bfloat16, device=obs_u8.device).to(memory_format=torch.channels_last)
+    if (out.dtype != torch.bfloat16 or tuple(out.shape) != (n, 32, 20, 20)
+            or not out.is_contiguous(memory_format=torch.channels_last)):
+        raise ValueError("policy_conv1: out must be a bf16 (B, 32, 20, 20) channels-last tensor")
+    check(lib().mh_policy_conv1(obs_u8.data_ptr(), w.data_ptr(), b.data_ptr(), out.data_ptr(), n,
+                                torch.cuda.current_stream(obs_u8.device).cuda_stream), "mh_policy_conv1")
+    return out
+
+
 def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="cuda"):
     """The Nature-CNN actor-critic with the reference's architecture and initialisation, random weights."""
     torch = _torch()
@@ -81,17 +104,30 @@ def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="
         def forward(self, obs_u8):
             """uint8 (B, 4, 84, 84) -> logits f32 (B, A), value f32 (B,).
 
-            On the GPU the observation is scaled by one HIP kernel straight into a bf16 channels-last buffer
-            (mh_policy_input): bf16(float(v) * float(1/255)), the value autocast gives the float32 scaling of the
-            CPU path, without the float32 intermediate (4x the observation's bytes). Calls of one batch shape
-            share the buffer."""
-            if obs_u8.is_cuda:
+            On the GPU the first layer is one HIP kernel on the matrix cores (mh_policy_conv1): the observation
+            scaled to bf16(float(v) * float(1/255)) (the value autocast gives the float32 scaling of the CPU
+            path), the 8x8 stride-4 convolution with float32 accumulation, the bias and the ReLU, written as the
+            bf16 channels-last input of the second layer. Other stack depths take mh_policy_input's scaling
+            into a bf16 channels-last buffer and the convolutions. Calls of one batch shape share the buffers.
+            With autograd on, the scaled input takes a buffer of its own and every layer is a torch layer."""
+            convs = list(self.convs)
+            grad = torch.is_grad_enabled()   # the fused layer has no backward, and a shared buffer must not be
+            if obs_u8.is_cuda and grad:      # overwritten while autograd holds it: the plain path, own buffers
+                x = torch.empty(obs_u8.shape, dtype=torch.bfloat16, device=obs_u8.device).to(
+                    memory_format=torch.channels_last)
+                policy_input(obs_u8.contiguous(), x)
+            elif obs_u8.is_cuda and obs_u8.shape[1] == 4 and obs_u8.is_contiguous():
+                # the first layer with its input scaling, bias and ReLU in one MFMA kernel (mh_policy_conv1)
+                x = policy_conv1(obs_u8, convs[0].weight, convs[0].bias, self._input((obs_u8.shape[0], 32, 20, 20),
+                                                                                     obs_u8.device))
+                convs = convs[1:]
+            elif obs_u8.is_cuda:
                 x = self._input(obs_u8.shape, obs_u8.device)
                 policy_input(obs_u8, x)
             else:
                 x = obs_u8.float().mul_(1.0 / 255.0)
             with torch.autocast("cuda", dtype=torch.bfloat16, enabled=x.is_cuda):
-                for c in self.convs:
+                for c in convs:
                     x = F.relu(c(x))
                 h = F.relu(self.fc(x.flatten(1)))
             h = h.float()

@@ -161,6 +161,13 @@ int mh_resize_noalloc(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream)
  * rounded to nearest even. k in 1, 2, 4, 8; both pointers 4-byte aligned; -1 otherwise. */
 int mh_policy_input(const uint8_t* d_obs, void* d_out, int64_t n, int k, void* stream);
 
+/* The harness's first policy layer fused with that scaling: relu(conv(bf16(obs / 255), W) + b) for the Nature
+ * CNN's first convolution (ppo/model.py:13-27: 4 -> 32 channels, 8x8 kernel, stride 4), on the matrix cores
+ * with float32 accumulation. d_obs: (n, 4, 84, 84) uint8 stacks, contiguous, 4-byte aligned; d_w: the bf16
+ * weight (32, 4, 8, 8) contiguous, 16-byte aligned; d_b: the bf16 bias (32); d_out: the (n, 32, 20, 20) bf16
+ * tensor in channels-last memory (pixel m's 32 channels at m * 32 ..), each value bf16(relu(sum + b)). */
+int mh_policy_conv1(const uint8_t* d_obs, const void* d_w, const void* d_b, void* d_out, int64_t n, void* stream);
+
 /* ---- frame-deduplicating replay ring (device storage owned by the caller)
  * The ring of FrameReplay (src/fast_mario_env/replay.py:43-60) for n_envs envs and `capacity` slots each,
  * all device memory, slot s of env e at index e * capacity + s:
