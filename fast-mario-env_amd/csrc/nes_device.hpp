@@ -1483,16 +1483,17 @@ struct Console {
             if (__all(parked)) {
                 // The whole wave is at the slice boundary: catch up together (next iteration), then
                 // open the next slice. `slice` and `synced` are wave-uniform, so every lane takes
-                // the same path here.
+                // the same path here. (No early `continue`: after the catch-up request every lane is still
+                // parked, so the rest of this iteration does nothing; after a new slice opens, this
+                // iteration's actions are those the next one would take.)
                 if (!synced) {
                     synced = true;
                     want = ppu_calls < slice ? slice : -1;
-                    continue;
+                } else {
+                    if (__all(slice >= last_call)) break;
+                    if (slice < last_call) { slice = next_slice(last_call); parked = false; }
+                    synced = false;
                 }
-                if (__all(slice >= last_call)) break;
-                if (slice < last_call) { slice = next_slice(last_call); parked = false; }
-                synced = false;
-                continue;
             }
             // One action per lane and iteration, chosen through `act` rather than early exits from the
             // loop body (each exit is a path whose state the next iteration must merge): park at the
