@@ -494,6 +494,87 @@ __global__ void __launch_bounds__(256) k_policy_conv1(const uint8_t* obs, const 
     }
 }
 
+// ---- the PPO policy's second and third convolutions (Nature CNN: 32 -> 64 channels 4x4 stride 2, 20x20 -> 9x9;
+// 64 -> 64 channels 3x3 stride 1, 9x9 -> 7x7), each fused with its bias and ReLU, on the matrix cores. Input and
+// output are bf16 in channels-last memory (pixel m's channels at m * C ..), the weight is (CO, KS, KS, CI)
+// (channels last), so K = (kh, kw, ci) and lane l's A operand of a step is 8 consecutive input channels of one
+// input pixel (one 16-byte load). A wave holds one half of the output channels' weights in registers (lane l:
+// channel 32 h + l % 32, K = 16 s + 8 (l / 32) .. + 7 of step s) and walks tiles of 32 output pixels; the two
+// halves are the block's even and odd waves. Output: bf16(relu(sum + b)) with float32 accumulation.
+template <int CI, int CO, int KS, int ST, int HI, int HO>
+__global__ void __launch_bounds__(256) k_policy_conv(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                                     uint16_t* y, int64_t n) {
+    static_assert(CI % 8 == 0 && CO == 64, "8-channel loads, two 32-channel halves");
+    constexpr int K = KS * KS * CI, STEPS = K / 16, PIX = HO * HO;
+    static_assert(K % 16 == 0, "whole MFMA steps");
+    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int j = l & 31, kg = l >> 5, half = wv & 1;
+    const int ch = 32 * half + j;
+    mh_bf16x8 wb[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+        const uint4 q = *(const uint4*)(w + (size_t)ch * K + 16 * s + 8 * kg);
+        const uint32_t q4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) wb[s][e] = __builtin_bit_cast(__bf16, (uint16_t)(q4[e >> 1] >> (16 * (e & 1))));
+    }
+    const float bj = __uint_as_float((uint32_t)bias[ch] << 16);
+    const int64_t M = n * PIX, tiles = (M + 31) / 32;
+    const int64_t pair = (int64_t)blockIdx.x * 2 + (wv >> 1), pairs = (int64_t)gridDim.x * 2;
+    // this lane's input pixel of tile t (past the end: a valid pixel, not stored)
+    auto pixel = [&](int64_t t) {
+        int64_t m = t * 32 + j;
+        if (m >= M) m = M - 1;
+        const int64_t b = m / PIX;
+        const int p = (int)(m - b * PIX), oy = p / HO, ox = p - oy * HO;
+        return x + ((size_t)(b * HI + ST * oy) * HI + ST * ox) * CI;
+    };
+    // the A operands of steps c .. c + CH - 1: 16-byte loads issued a chunk ahead of their MFMAs
+    constexpr int CH = STEPS % 8 == 0 ? 8 : 6, NCH = STEPS / CH;
+    static_assert(STEPS % CH == 0, "whole chunks");
+    auto load_chunk = [&](const uint16_t* px, int c, uint4 (&q)[CH]) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int k0 = 16 * (CH * c + i) + 8 * kg, kh = k0 / (KS * CI), kw = (k0 / CI) % KS, ci = k0 % CI;
+            q[i] = *(const uint4*)(px + ((size_t)kh * HI + kw) * CI + ci);
+        }
+    };
+    uint4 qa[CH], qb[CH];
+    const uint16_t* px = pixel(pair);
+    if (pair < tiles) load_chunk(px, 0, qa);
+    for (int64_t t = pair; t < tiles; t += pairs) {
+        mh_f32x16 acc = {};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            uint4 (&cur)[CH] = (c & 1) ? qb : qa;
+            uint4 (&nxt)[CH] = (c & 1) ? qa : qb;
+            if (c + 1 < NCH) load_chunk(px, c + 1, nxt);
+            else if (t + pairs < tiles) load_chunk(pixel(t + pairs), 0, nxt);   // the next tile's first chunk
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                const uint32_t q4[4] = {cur[i].x, cur[i].y, cur[i].z, cur[i].w};
+                mh_bf16x8 a;
+#pragma unroll
+                for (int e = 0; e < 8; e++) a[e] = __builtin_bit_cast(__bf16, (uint16_t)(q4[e >> 1] >> (16 * (e & 1))));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, wb[CH * c + i], acc, 0, 0, 0);
+            }
+        }
+        if constexpr (NCH & 1) {   // the next tile's first chunk landed in qb: move it to qa
+#pragma unroll
+            for (int i = 0; i < CH; i++) qa[i] = qb[i];
+        }
+        if (t + pairs < tiles) px = pixel(t + pairs);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int64_t mo = t * 32 + 8 * (v >> 2) + 4 * kg + (v & 3);
+            if (mo < M) {
+                const float r = acc[v] + bj;
+                y[(size_t)mo * CO + ch] = (uint16_t)bf16_rne(r > 0.f ? r : 0.f);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // compute units of a device (the emulator kernels' launch shape depends on it)
@@ -1036,6 +1117,29 @@ int mh_policy_conv1(const uint8_t* d_obs, const void* d_w, const void* d_b, void
     const int64_t blocks = std::min<int64_t>((tiles + 3) / 4, (int64_t)cus * 8);   // persistent: tiles per wave
     hipLaunchKernelGGL(k_policy_conv1, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, d_obs,
                        (const uint16_t*)d_w, (const uint16_t*)d_b, (uint16_t*)d_out, n);
+    CK(hipGetLastError());
+    return 0;
+}
+
+int mh_policy_conv(const void* d_x, const void* d_w, const void* d_b, void* d_out, int64_t n, int layer, void* stream) {
+    if (!d_x || !d_w || !d_b || !d_out || n < 1 || (layer != 2 && layer != 3)) {
+        g_err = "invalid arguments (n >= 1, layer 2 or 3)";
+        return -1;
+    }
+    if ((((uintptr_t)d_x) & 15) || (((uintptr_t)d_w) & 15) || (((uintptr_t)d_out) & 1) || (((uintptr_t)d_b) & 1)) {
+        g_err = "input and weight must be 16-byte, bias and out 2-byte aligned";
+        return -1;
+    }
+    int dev = 0, cus = 0;
+    CK(hipGetDevice(&dev));
+    CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int64_t pix = layer == 2 ? 81 : 49, tiles = (n * pix + 31) / 32;
+    const int64_t blocks = std::min<int64_t>((tiles + 1) / 2, (int64_t)cus * 8);   // 2 tiles in flight per block
+    hipStream_t s = (hipStream_t)stream;
+    const uint16_t *x = (const uint16_t*)d_x, *w = (const uint16_t*)d_w, *b = (const uint16_t*)d_b;
+    uint16_t* y = (uint16_t*)d_out;
+    if (layer == 2) hipLaunchKernelGGL((k_policy_conv<32, 64, 4, 2, 20, 9>), dim3((unsigned)blocks), dim3(256), 0, s, x, w, b, y, n);
+    else hipLaunchKernelGGL((k_policy_conv<64, 64, 3, 1, 9, 7>), dim3((unsigned)blocks), dim3(256), 0, s, x, w, b, y, n);
     CK(hipGetLastError());
     return 0;
 }

@@ -70,6 +70,7 @@ def lib() -> ctypes.CDLL:
     L.mh_resize_noalloc.argtypes = [_P, _P, _i32, _P]
     L.mh_policy_input.argtypes = [_P, _P, _i64, _i32, _P]
     L.mh_policy_conv1.argtypes = [_P, _P, _P, _P, _i64, _P]
+    L.mh_policy_conv.argtypes = [_P, _P, _P, _P, _i64, _i32, _P]
     L.mh_reemulations.argtypes = [_P, _P]
     L.mh_replay_add.argtypes = [_P] * 7 + [_i32] * 4 + [_P] * 7
     L.mh_replay_gather.argtypes = [_P] * 5 + [_i32] * 4 + [_P, _P, _i32, _i32] + [_P] * 10

@@ -70,6 +70,33 @@ def policy_conv1(obs_u8, weight, bias, out=None):
     return out
 
 
+_CONV_SHAPES = {2: ((64, 32, 4, 4), (32, 20, 20), (64, 9, 9)), 3: ((64, 64, 3, 3), (64, 9, 9), (64, 7, 7))}
+
+
+def policy_conv(x, weight, bias, layer, out=None):
+    """relu(conv2d(x, weight, bias)) of the Nature CNN's second (layer=2: 4x4 stride 2) or third (layer=3: 3x3
+    stride 1) convolution by the library's MFMA kernel: x a bf16 channels-last (B, C, H, H) tensor on a GPU,
+    weight (64, C, k, k) and bias (64) in any float dtype (taken as bf16, as autocast takes them); returns (or
+    fills) the bf16 channels-last output."""
+    torch = _torch()
+    from ._native import check, lib
+    wshape, ishape, oshape = _CONV_SHAPES[layer]
+    n = x.shape[0]
+    if (x.dtype != torch.bfloat16 or tuple(x.shape[1:]) != ishape or not x.is_contiguous(memory_format=torch.channels_last)
+            or tuple(weight.shape) != wshape or tuple(bias.shape) != (64,)):
+        raise ValueError(f"policy_conv layer {layer}: needs a bf16 channels-last (B, {ishape[0]}, {ishape[1]}, {ishape[2]}) "
+                         f"input, a {wshape} weight and a (64,) bias")
+    w = weight.detach().to(device=x.device, dtype=torch.bfloat16).permute(0, 2, 3, 1).contiguous()
+    b = bias.detach().to(device=x.device, dtype=torch.bfloat16).contiguous()
+    if out is None:
+        out = torch.empty((n,) + oshape, dtype=torch.bfloat16, device=x.device).to(memory_format=torch.channels_last)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (n,) + oshape or not out.is_contiguous(memory_format=torch.channels_last):
+        raise ValueError(f"policy_conv layer {layer}: out must be a bf16 channels-last (B,) + {oshape} tensor")
+    check(lib().mh_policy_conv(x.data_ptr(), w.data_ptr(), b.data_ptr(), out.data_ptr(), n, layer,
+                               torch.cuda.current_stream(x.device).cuda_stream), "mh_policy_conv")
+    return out
+
+
 def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="cuda"):
     """The Nature-CNN actor-critic with the reference's architecture and initialisation, random weights."""
     torch = _torch()
@@ -104,10 +131,10 @@ def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="
         def forward(self, obs_u8):
             """uint8 (B, 4, 84, 84) -> logits f32 (B, A), value f32 (B,).
 
-            On the GPU the first layer is one HIP kernel on the matrix cores (mh_policy_conv1): the observation
-            scaled to bf16(float(v) * float(1/255)) (the value autocast gives the float32 scaling of the CPU
-            path), the 8x8 stride-4 convolution with float32 accumulation, the bias and the ReLU, written as the
-            bf16 channels-last input of the second layer. Other stack depths take mh_policy_input's scaling
+            On the GPU each convolution is one HIP kernel on the matrix cores with float32 accumulation, its bias
+            and its ReLU (mh_policy_conv1, mh_policy_conv): the first one scales the observation to
+            bf16(float(v) * float(1/255)) (the value autocast gives the float32 scaling of the CPU path); the
+            activations are bf16 channels-last. Other stack depths take mh_policy_input's scaling
             into a bf16 channels-last buffer and the convolutions. Calls of one batch shape share the buffers.
             With autograd on, the scaled input takes a buffer of its own and every layer is a torch layer."""
             convs = list(self.convs)
@@ -117,10 +144,18 @@ def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="
                     memory_format=torch.channels_last)
                 policy_input(obs_u8.contiguous(), x)
             elif obs_u8.is_cuda and obs_u8.shape[1] == 4 and obs_u8.is_contiguous():
-                # the first layer with its input scaling, bias and ReLU in one MFMA kernel (mh_policy_conv1)
-                x = policy_conv1(obs_u8, convs[0].weight, convs[0].bias, self._input((obs_u8.shape[0], 32, 20, 20),
-                                                                                     obs_u8.device))
-                convs = convs[1:]
+                # the three convolutions with their input scaling, biases and ReLUs as MFMA kernels
+                # (mh_policy_conv1, mh_policy_conv); the fully connected layer takes the last one's
+                # channels-last output as it lies, with its weight's columns permuted to (h, w, c) order
+                B, dev = obs_u8.shape[0], obs_u8.device
+                x = policy_conv1(obs_u8, convs[0].weight, convs[0].bias, self._input((B, 32, 20, 20), dev))
+                x = policy_conv(x, convs[1].weight, convs[1].bias, 2, self._input((B, 64, 9, 9), dev))
+                x = policy_conv(x, convs[2].weight, convs[2].bias, 3, self._input((B, 64, 7, 7), dev))
+                wfc = self.fc.weight.view(512, 64, 7, 7).permute(0, 2, 3, 1).reshape(512, 64 * 7 * 7)
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    h = F.relu(F.linear(x.permute(0, 2, 3, 1).reshape(B, 64 * 7 * 7), wfc, self.fc.bias))
+                h = h.float()
+                return self.pi(h), self.vf(h).squeeze(-1)
             elif obs_u8.is_cuda:
                 x = self._input(obs_u8.shape, obs_u8.device)
                 policy_input(obs_u8, x)

@@ -168,6 +168,13 @@ int mh_policy_input(const uint8_t* d_obs, void* d_out, int64_t n, int k, void* s
  * tensor in channels-last memory (pixel m's 32 channels at m * 32 ..), each value bf16(relu(sum + b)). */
 int mh_policy_conv1(const uint8_t* d_obs, const void* d_w, const void* d_b, void* d_out, int64_t n, void* stream);
 
+/* The Nature CNN's second (layer 2: 32 -> 64 channels, 4x4 kernel, stride 2, 20x20 -> 9x9) or third (layer 3:
+ * 64 -> 64 channels, 3x3, stride 1, 9x9 -> 7x7) convolution with its bias and ReLU (ppo/model.py:13-27), on the
+ * matrix cores with float32 accumulation: d_x the bf16 (n, CI, H, H) input in channels-last memory and d_out the
+ * bf16 (n, 64, HO, HO) output likewise, each value bf16(relu(sum + b)); d_w the bf16 weight as (64, KS, KS, CI)
+ * (channels last), d_b the bf16 bias (64). d_x and d_w 16-byte aligned. */
+int mh_policy_conv(const void* d_x, const void* d_w, const void* d_b, void* d_out, int64_t n, int layer, void* stream);
+
 /* ---- frame-deduplicating replay ring (device storage owned by the caller)
  * The ring of FrameReplay (src/fast_mario_env/replay.py:43-60) for n_envs envs and `capacity` slots each,
  * all device memory, slot s of env e at index e * capacity + s:

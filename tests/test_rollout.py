@@ -208,3 +208,27 @@ def test_policy_conv1_kernel_matches_torch(n):
     assert (yf > 0).float().mean() > 0.2          # the layer is not trivially zero
     with pytest.raises(ValueError):
         policy_conv1(obs[:, :3].contiguous(), c.weight, c.bias)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layer,n", [(2, 1), (2, 37), (3, 1), (3, 37)])
+def test_policy_conv_kernels_match_torch(layer, n):
+    # the fused MFMA second and third layers against torch's bf16 convolutions with bias under autocast and ReLU
+    import torch.nn.functional as F
+
+    from fast_mario_env_amd.rollout import make_net, policy_conv
+    net = make_net(seed=4)
+    c = net.convs[layer - 1]
+    ci, hi = (32, 20) if layer == 2 else (64, 9)
+    g = torch.Generator(device="cuda").manual_seed(layer * 100 + n)
+    x = torch.rand(n, ci, hi, hi, generator=g, device="cuda").to(torch.bfloat16).to(memory_format=torch.channels_last)
+    with torch.no_grad():
+        y = policy_conv(x, c.weight, c.bias, layer)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            ref = F.relu(F.conv2d(x, c.weight, c.bias, stride=c.stride))
+    assert y.shape == ref.shape and y.is_contiguous(memory_format=torch.channels_last)
+    yf, rf = y.float(), ref.float()
+    assert torch.allclose(yf, rf, rtol=1.6e-2, atol=4e-3), (yf - rf).abs().max().item()
+    assert (yf > 0).float().mean() > 0.2
+    with pytest.raises(ValueError):
+        policy_conv(x.contiguous() if ci > 1 else x, c.weight, c.bias, layer)   # NCHW input refused
