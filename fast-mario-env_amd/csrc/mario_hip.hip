@@ -293,6 +293,53 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
     }
 }
 
+// k_stack with 16-byte accesses, for obs / fin buffers (and the reset cache) 16-byte aligned: the same block
+// (64 envs x 64 words of a frame, the fresh words transposed through LDS), but a thread moves 4 consecutive
+// words of one env per access (16 threads per env, 16 envs per pass, 4 passes), and reads the env's slot and
+// reset index once per pass.
+__global__ void __launch_bounds__(256) k_stack4(StackArgs A) {
+    __shared__ uint32_t tile[64][65];
+    const uint32_t e0 = blockIdx.x * 64;
+    const int w0 = blockIdx.y * 64;
+    const int nw = OBS_PIX / 4;
+    if (A.mode == 0) {
+        for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
+            const int wl = idx >> 6, j = idx & 63;
+            const uint32_t e = e0 + j;
+            uint32_t val = 0;
+            if (w0 + wl < nw && e < (uint32_t)A.n) val = ((const uint32_t*)A.fresh)[(size_t)(w0 + wl) * A.np + e];
+            tile[wl][j] = val;
+        }
+    }
+    __syncthreads();
+    const size_t fw = (size_t)nw * A.K;   // words per env stack
+    const int g = threadIdx.x & 15, w = w0 + 4 * g;   // this thread's 4 words: w .. w + 3 (nw is a multiple of 4)
+    for (int pass = 0; pass < 4; pass++) {
+        const int j = 16 * pass + (threadIdx.x >> 4);
+        const uint32_t e = e0 + j;
+        if (w >= nw || e >= (uint32_t)A.n) continue;
+        const size_t env = (size_t)A.slot_env[e];
+        uint4* st = (uint4*)((uint32_t*)A.obs + env * fw + w);          // frame s of the stack at st + s * nw / 4
+        const uint32_t ri = A.ev[(size_t)E_RESET_IDX * A.np + e];
+        const size_t fq = (size_t)nw / 4;
+        if (A.mode == 1) {
+            for (int s = 0; s < A.K - 1; s++) st[s * fq] = make_uint4(0, 0, 0, 0);
+            st[(A.K - 1) * fq] = *(const uint4*)((const uint32_t*)A.cobs + (size_t)ri * nw + w);
+            continue;
+        }
+        const uint4 fresh = make_uint4(tile[4 * g][j], tile[4 * g + 1][j], tile[4 * g + 2][j], tile[4 * g + 3][j]);
+        if (ri != 0xffffffffu) {
+            uint4* fo = (uint4*)((uint32_t*)A.fin + env * fw + w);
+            for (int s = 0; s < A.K - 1; s++) { fo[s * fq] = st[(s + 1) * fq]; st[s * fq] = make_uint4(0, 0, 0, 0); }
+            fo[(A.K - 1) * fq] = fresh;
+            st[(A.K - 1) * fq] = *(const uint4*)((const uint32_t*)A.cobs + (size_t)ri * nw + w);
+        } else {
+            for (int s = 0; s < A.K - 1; s++) st[s * fq] = st[(s + 1) * fq];
+            st[(A.K - 1) * fq] = fresh;
+        }
+    }
+}
+
 // slot_env (nullable): the output row of each console slot
 __global__ void k_canon(const uint8_t* mem, const uint32_t* sc, uint32_t np, int n, const int32_t* slot_env, uint8_t* out) {
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
@@ -624,6 +671,14 @@ struct MhEnv {
     StackArgs stack_args(int mode) const { return StackArgs{n, np, K, obs, fin, slot_env, fresh, ev, cobs, mode}; }
 };
 
+// k_stack4 when the stacks (and the reset cache) allow 16-byte accesses, else k_stack
+static void launch_stack(const MhEnv* h, hipStream_t s, int mode) {
+    const dim3 grid(h->np / 64, (OBS_PIX / 4 + 63) / 64);
+    const bool al = ((((uintptr_t)h->obs) | ((uintptr_t)h->fin) | ((uintptr_t)h->cobs)) & 15) == 0;
+    if (al) hipLaunchKernelGGL(k_stack4, grid, dim3(256), 0, s, h->stack_args(mode));
+    else hipLaunchKernelGGL(k_stack, grid, dim3(256), 0, s, h->stack_args(mode));
+}
+
 struct MhRaw {
     int n = 0, device = 0, cus = 0;
     uint32_t np = 0;
@@ -836,7 +891,7 @@ int mh_reset(MhEnv* h, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(1));
     CK(hipGetLastError());
-    hipLaunchKernelGGL(k_stack, dim3(h->np / 64, (OBS_PIX / 4 + 63) / 64), dim3(256), 0, s, h->stack_args(1));
+    launch_stack(h, s, 1);
     CK(hipGetLastError());
     return 0;
 }
@@ -872,7 +927,7 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(0));
     CK(hipGetLastError());
     if (mark(h, s, 3)) return -1;
-    hipLaunchKernelGGL(k_stack, dim3(h->np / 64, (OBS_PIX / 4 + 63) / 64), dim3(256), 0, s, h->stack_args(0));
+    launch_stack(h, s, 0);
     CK(hipGetLastError());
     if (mark(h, s, 4)) return -1;
     if (h->timing) h->timed_steps++;

@@ -160,6 +160,41 @@ def test_set_buffers_device_and_refusals():
     v.close()
 
 
+def test_stack_kernels_on_4_byte_aligned_buffers():
+    """Observation and final-observation stacks that are 4-byte but not 16-byte aligned take the 4-byte frame-stack
+    kernel (16-byte aligned ones take the 16-byte one): the same observations, final observations and resets as the
+    oracle over 40 steps with episode ends (max_steps=9)."""
+    import fast_mario_env_amd as fme
+    n = 3
+    v = fme.FastVecEnv("1-1", n, seed=2, rom=MINI, max_steps=9)
+    z = lambda *s, dt: torch.zeros(*s, dtype=dt, device="cuda")  # noqa: E731
+    big = z(2 * n * 4 * 84 * 84 + 64, dt=torch.uint8)
+    obs = big[4:4 + n * 4 * 84 * 84].view(n, 4, 84, 84)             # 4 bytes past a 16-byte boundary
+    fin = big[n * 4 * 84 * 84 + 8:2 * n * 4 * 84 * 84 + 8].view(n, 4, 84, 84)
+    assert obs.data_ptr() % 16 == 4 and fin.data_ptr() % 16 == 8
+    rest = [z(n, dt=torch.float32), z(n, dt=torch.uint8), z(n, dt=torch.uint8), z(n, 10, dt=torch.int32),
+            z(n, dt=torch.float64), z(n, dt=torch.int32)]
+    v.set_buffers(obs, fin, *rest)
+    ref = OracleVec(MINI, _levels(["1-1"] * n), n, seed=2, max_steps=9)
+    v.reset()
+    ref.reset()
+    torch.cuda.synchronize()
+    assert np.array_equal(obs.cpu().numpy(), ref.obs)
+    ends = 0
+    for t in range(40):
+        a = np.array([t % 7, (3 * t) % 7, (5 * t + 1) % 7])
+        v.step(a)
+        ref.step(a)
+        torch.cuda.synchronize()
+        assert np.array_equal(obs.cpu().numpy(), ref.obs), t
+        d = np.flatnonzero(ref.term | ref.trunc)
+        ends += len(d)
+        for i in d:
+            assert np.array_equal(fin[i].cpu().numpy(), ref.fin[i]), (t, i)
+    assert ends >= 6
+    v.close()
+
+
 class _StackLikeSb3:
     """SB3's VecFrameStack rule for channels-last Box observations, restated for this test (SB3 is not installed):
     reset zero-fills the stack and puts the frame last; each step shifts the stack one frame towards the front,
