@@ -1159,12 +1159,27 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream) {
     return 0;
 }
 
+// The policy entry points' buffers: memory of the current GPU (device, or pinned host memory it maps); anything
+// else (pageable host memory, another GPU's memory) is refused before a kernel could fault on it.
+static bool on_gpu(const void* p, const char* name) {
+    int dev = 0;
+    if (!ok(hipGetDevice(&dev), "hipGetDevice")) return false;
+    hipPointerAttribute_t at;
+    const hipError_t e = hipPointerGetAttributes(&at, p);
+    (void)hipGetLastError();   // a refused pointer must not surface as the error of a later launch
+    const bool good = e == hipSuccess && ((at.type == hipMemoryTypeDevice && at.device == dev) ||
+                                          at.type == hipMemoryTypeHost || at.type == hipMemoryTypeManaged);
+    if (!good) g_err = std::string(name) + ": not memory of GPU " + std::to_string(dev);
+    return good;
+}
+
 int mh_policy_conv1(const uint8_t* d_obs, const void* d_w, const void* d_b, void* d_out, int64_t n, void* stream) {
     if (!d_obs || !d_w || !d_b || !d_out || n < 1) { g_err = "invalid arguments (n >= 1)"; return -1; }
     if ((((uintptr_t)d_obs) & 3) || (((uintptr_t)d_w) & 15) || (((uintptr_t)d_out) & 1) || (((uintptr_t)d_b) & 1)) {
         g_err = "obs must be 4-byte, weight 16-byte and bias / out 2-byte aligned";
         return -1;
     }
+    if (!on_gpu(d_obs, "obs") || !on_gpu(d_w, "weight") || !on_gpu(d_b, "bias") || !on_gpu(d_out, "out")) return -1;
     int dev = 0, cus = 0;
     CK(hipGetDevice(&dev));
     CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
@@ -1185,6 +1200,7 @@ int mh_policy_conv(const void* d_x, const void* d_w, const void* d_b, void* d_ou
         g_err = "input and weight must be 16-byte, bias and out 2-byte aligned";
         return -1;
     }
+    if (!on_gpu(d_x, "input") || !on_gpu(d_w, "weight") || !on_gpu(d_b, "bias") || !on_gpu(d_out, "out")) return -1;
     int dev = 0, cus = 0;
     CK(hipGetDevice(&dev));
     CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
@@ -1205,6 +1221,7 @@ int mh_policy_input(const uint8_t* d_obs, void* d_out, int64_t n, int k, void* s
         return -1;
     }
     if ((((uintptr_t)d_obs) & 3) || (((uintptr_t)d_out) & 3)) { g_err = "obs and out must be 4-byte aligned"; return -1; }
+    if (!on_gpu(d_obs, "obs") || !on_gpu(d_out, "out")) return -1;
     const int64_t groups = n * (OBS_PIX / 4);
     const dim3 grid((unsigned)((groups + 255) / 256));
     hipStream_t s = (hipStream_t)stream;

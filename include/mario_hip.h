@@ -158,7 +158,8 @@ int mh_resize_noalloc(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream)
  * written for the bf16 channels-last input the harness's convolutions take.
  * d_obs: (n, k, 84, 84) uint8 stacks, contiguous; d_out: the (n, k, 84, 84) bf16 tensor in channels-last
  * memory (element (b, c, h, w) at ((b * 84 + h) * 84 + w) * k + c), of value bf16(float(v) * float(1 / 255))
- * rounded to nearest even. k in 1, 2, 4, 8; both pointers 4-byte aligned; -1 otherwise. */
+ * rounded to nearest even. k in 1, 2, 4, 8; both pointers 4-byte aligned and memory of the current GPU (device
+ * memory, or pinned host memory); -1 otherwise. The two layer entry points below check their pointers alike. */
 int mh_policy_input(const uint8_t* d_obs, void* d_out, int64_t n, int k, void* stream);
 
 /* The harness's first policy layer fused with that scaling: relu(conv(bf16(obs / 255), W) + b) for the Nature

@@ -141,6 +141,11 @@ def test_policy_input_kernel_matches_torch_scaling(k, n):
     assert torch.equal(out.contiguous().view(torch.int16), ref.view(torch.int16))
     with pytest.raises(ValueError):
         policy_input(obs, out.contiguous() if k > 1 else out.float())   # NCHW (or float) output refused
+    # a pageable host buffer is refused by the library before any kernel could touch it
+    from fast_mario_env_amd._native import lib
+    host = np.zeros(obs.numel() * 2, np.uint8)
+    assert lib().mh_policy_input(obs.data_ptr(), host.ctypes.data, n, k, 0) == -1
+    assert lib().mh_policy_input(host.ctypes.data, out.data_ptr(), n, k, 0) == -1
 
 
 @pytest.mark.gpu
