@@ -108,12 +108,14 @@ def valu_roofline(workload_key):
 
 
 def kernel_source_sha1():
-    """sha1 of the HIP sources the library is built from (names the kernel build a profile measured)."""
+    """sha1 of the HIP sources the library is built from and of its build script (compiler flags): names the
+    kernel build a profile measured."""
     h = hashlib.sha1()
     d = os.path.join(ROOT, "fast-mario-env_amd", "csrc")
     for f in sorted(os.listdir(d)):
         if f.endswith((".hip", ".hpp")):
             h.update(open(os.path.join(d, f), "rb").read())
+    h.update(open(os.path.join(ROOT, "fast-mario-env_amd", "build_native.py"), "rb").read())
     return h.hexdigest()[:12]
 
 

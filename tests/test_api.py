@@ -1,6 +1,7 @@
 """Host-side API and boundary checks that need no GPU (mirrors the reference's tests/test_api.py)."""
 import ctypes
 import os
+import sys
 import re
 import subprocess
 
@@ -135,8 +136,11 @@ def test_resize_kernel_has_no_fma(tmp_path):
     -ffp-contract=off build): compile the device code to gfx950 assembly and inspect the obs kernels."""
     src = os.path.join(ROOT, "fast-mario-env_amd", "csrc", "mario_hip.hip")
     out = tmp_path / "dev.s"
-    cmd = ["hipcc", "--offload-arch=gfx950", "--cuda-device-only", "-S", "-O3", "-std=c++17", "-ffp-contract=off",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", src, "-o", str(out)]
+    sys.path.insert(0, os.path.join(ROOT, "fast-mario-env_amd"))
+    import build_native                                  # the library's own flags
+    flags = [f for f in build_native.FLAGS if f not in ("-shared", "-fPIC", "-Wall")]
+    assert "-ffp-contract=off" in flags
+    cmd = ["hipcc", "--offload-arch=gfx950", "--cuda-device-only", "-S", *flags, src, "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
     asm = out.read_text()
