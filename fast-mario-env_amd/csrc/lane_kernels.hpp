@@ -47,36 +47,102 @@ __host__ __device__ inline void area_tables(AreaTables* T) {
     area_taps(240, 84, T->ys, T->yw, T->yn);
 }
 
-// The first source column of each output column's taps, at compile time: area_taps(256, 84)'s steps for the
-// start index (the same double operations; ceil and floor of non-negative values by truncation), so that a
-// kernel can address a column's pixels with constant word and byte indices. The library checks at start-up that
-// they equal the run-time tables' (x_cols_match()); the taps of a column are at most 4 consecutive pixels.
-struct XCols { int x0[84]; };
-constexpr XCols x_cols() {
-    XCols r{};
-    const double scale = 1.0 / ((double)84 / 256);
-    for (int d = 0; d < 84; d++) {
-        const double f1 = d * scale, f2 = f1 + scale;
-        int s1 = (int)f1;
-        if ((double)s1 < f1) s1++;
-        int s2 = (int)f2;
-        if (s2 > 255) s2 = 255;
-        if (s1 > s2) s1 = s2;
-        r.x0[d] = s1 - f1 > 1e-3 ? s1 - 1 : s1;
+// ---- The INTER_AREA tables by periods
+// 256 -> 84 columns and 240 -> 84 rows are ratios 64 : 21 and 20 : 7, and the tables repeat with them: output
+// column 21 g + q takes source pixels 64 g + (those of column q) with column q's weights, output row 7 p + q
+// source rows 20 p + (those of row q) with row q's weights, and no source pixel or row is shared across a
+// period boundary. AreaPeriod holds one period of each, computed at compile time by area_taps's steps (the same
+// double operations; ceil and floor of non-negative values by truncation), so that a kernel can take every
+// tap's position and weight as a constant. The library checks at start-up that the run-time tables are these
+// periods repeated (area_period_match()).
+struct AreaPeriod {
+    int x0[21], xn[21];    // output column q: source pixels x0 .. x0 + xn - 1 of its 64-pixel period
+    float xw[21][4];
+    int y0[7], yn[7];      // output row q: source rows y0 .. y0 + yn - 1 of its 20-row period
+    float yw[7][4];
+};
+constexpr void area_taps_cx(int ssize, int dsize, int d, int* idx, float* w, int& cnt) {
+    const double scale = 1.0 / ((double)dsize / ssize);
+    const double f1 = d * scale, f2 = f1 + scale;
+    const double cell = scale < ssize - f1 ? scale : ssize - f1;
+    int s1 = (int)f1;
+    if ((double)s1 < f1) s1++;
+    int s2 = (int)f2;
+    if (s2 > ssize - 1) s2 = ssize - 1;
+    if (s1 > s2) s1 = s2;
+    cnt = 0;
+    if (s1 - f1 > 1e-3) { idx[cnt] = s1 - 1; w[cnt] = (float)((s1 - f1) / cell); cnt++; }
+    for (int s = s1; s < s2; s++) { idx[cnt] = s; w[cnt] = (float)(1.0 / cell); cnt++; }
+    if (f2 - s2 > 1e-3) {
+        double ww = f2 - s2 < 1.0 ? f2 - s2 : 1.0;
+        if (cell < ww) ww = cell;
+        idx[cnt] = s2; w[cnt] = (float)(ww / cell); cnt++;
+    }
+}
+constexpr AreaPeriod area_period() {
+    AreaPeriod r{};
+    for (int q = 0; q < 21; q++) {
+        int idx[TAPS] = {}, n = 0;
+        float w[TAPS] = {};
+        area_taps_cx(256, 84, q, idx, w, n);
+        r.x0[q] = idx[0]; r.xn[q] = n;
+        for (int k = 0; k < n && k < 4; k++) r.xw[q][k] = w[k];
+    }
+    for (int q = 0; q < 7; q++) {
+        int idx[TAPS] = {}, n = 0;
+        float w[TAPS] = {};
+        area_taps_cx(240, 84, q, idx, w, n);
+        r.y0[q] = idx[0]; r.yn[q] = n;
+        for (int k = 0; k < n && k < 4; k++) r.yw[q][k] = w[k];
     }
     return r;
 }
-constexpr XCols kXCols = x_cols();
-inline bool x_cols_match(const AreaTables& T) {
+constexpr AreaPeriod kArea = area_period();
+constexpr bool area_period_shape() {
+    for (int q = 0; q < 21; q++)
+        if (kArea.xn[q] != 4 || kArea.x0[q] < 0 || kArea.x0[q] + 4 > 64) return false;
+    for (int q = 0; q < 7; q++) {
+        if (kArea.yn[q] < 1 || kArea.yn[q] > 4 || kArea.y0[q] < 0 || kArea.y0[q] + kArea.yn[q] > 20) return false;
+        // consecutive rows share at most their boundary row
+        if (q > 0 && kArea.y0[q] < kArea.y0[q - 1] + kArea.yn[q - 1] - 1) return false;
+    }
+    return kArea.y0[0] == 0 && kArea.y0[6] + kArea.yn[6] == 20;
+}
+static_assert(area_period_shape(), "every column takes 4 pixels of its period, every row 1-4 rows of its period");
+
+inline bool area_period_match(const AreaTables& T) {
     for (int d = 0; d < 84; d++) {
-        if (T.xs[d * TAPS] != kXCols.x0[d] || T.xn[d] < 1 || T.xn[d] > 4) return false;
-        for (int k = 1; k < T.xn[d]; k++)
-            if (T.xs[d * TAPS + k] != kXCols.x0[d] + k) return false;
-        for (int k = T.xn[d]; k < 4; k++)
-            if (T.xw[d * TAPS + k] != 0.f) return false;
+        const int q = d % 21, g = d / 21;
+        if (T.xn[d] != kArea.xn[q]) return false;
+        for (int k = 0; k < T.xn[d]; k++)
+            if (T.xs[d * TAPS + k] != 64 * g + kArea.x0[q] + k || T.xw[d * TAPS + k] != kArea.xw[q][k]) return false;
+        const int r = d % 7, p = d / 7;
+        if (T.yn[d] != kArea.yn[r]) return false;
+        for (int j = 0; j < T.yn[d]; j++)
+            if (T.ys[d * TAPS + j] != 20 * p + kArea.y0[r] + j || T.yw[d * TAPS + j] != kArea.yw[r][j]) return false;
     }
     return true;
 }
+
+// What source row r of a 20-row period does: its sums, times `wa`, are added to the open output row (row q of
+// the period); if `last`, that row is then complete, and the next one opens with the row's sums times `wb`
+// (+0 when the next row starts at the following source row).
+struct RowStep { float wa, wb; int q; int last; };
+struct RowSteps { RowStep s[20]; };
+constexpr RowSteps row_steps() {
+    RowSteps t{};
+    for (int r = 0; r < 20; r++) {
+        int q = 0;
+        while (!(kArea.y0[q] <= r && r < kArea.y0[q] + kArea.yn[q])) q++;
+        const int j = r - kArea.y0[q];
+        t.s[r].wa = kArea.yw[q][j];
+        t.s[r].q = q;
+        t.s[r].last = j == kArea.yn[q] - 1;
+        t.s[r].wb = (t.s[r].last && q + 1 < 7 && kArea.y0[q + 1] == r) ? kArea.yw[q + 1][0] : 0.f;
+    }
+    return t;
+}
+constexpr RowSteps kRows = row_steps();
 
 __device__ __forceinline__ uint8_t round_sat(float v) {
     float r = __builtin_rintf(v);           // round half to even, like lrintf
@@ -116,74 +182,53 @@ __device__ __forceinline__ uint8_t area_pixel(const Image& g0, const Image& g1, 
     return round_sat(acc);
 }
 
-// bytewise max of two words (in 16-bit lanes: 256 + a - b has bit 8 set exactly when a >= b)
-__device__ __forceinline__ uint32_t max_u8x4(uint32_t a, uint32_t b) {
-    const uint32_t a0 = a & 0x00ff00ffu, b0 = b & 0x00ff00ffu, a1 = (a >> 8) & 0x00ff00ffu, b1 = (b >> 8) & 0x00ff00ffu;
-    const uint32_t t0 = ((a0 | 0x01000100u) - b0) & 0x01000100u, t1 = ((a1 | 0x01000100u) - b1) & 0x01000100u;
-    const uint32_t k0 = t0 - (t0 >> 8), k1 = t1 - (t1 >> 8);
-    return ((a0 & k0) | (b0 & ~k0)) | (((a1 & k1) | (b1 & ~k1)) << 8);
+// Bytewise max of two words by packed 16-bit maxima: max_even_bytes holds the maxima of bytes 0 and 2 in bytes
+// 0 and 2 (the other bytes masked to 0 first); max_odd_bytes those of bytes 1 and 3 in bytes 1 and 3 (the high
+// byte of a 16-bit maximum is the maximum of the high bytes, whatever the low bytes are).
+typedef unsigned short mh_u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t max_even_bytes(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(mh_u16x2, a & 0x00ff00ffu),
+                                                                  __builtin_bit_cast(mh_u16x2, b & 0x00ff00ffu)));
 }
-// ---- INTER_AREA of a staged source row, by column groups (k_obs)
-constexpr int OBS_COLS = 24;   // output columns one row-sum call covers: 20 G .. 20 G + 23
-
-// The horizontal sums of one source row for output columns 20 G .. 20 G + 23 of one env: word i of the row
-// (pixels 4 i .. 4 i + 3, max-pooled if the env pools) at rw[i * stride + lane]; xw[c]: column c's 4 tap
-// weights (+0 past its tap count). The words these columns' taps cover are read once, and every tap is a
-// constant byte of one of them (kXCols). Always 4 taps: adding +0 * pixel leaves the non-negative sum
-// unchanged, bit for bit, and the pixel is still inside the row.
-template <int G>
-__device__ __forceinline__ void obs_row_sums(const uint32_t* rw, uint32_t stride, uint32_t lane, const float (*xw)[4],
-                                             float (&rs)[OBS_COLS]) {
-    constexpr int c0 = 20 * G, wlo = kXCols.x0[c0] >> 2, whi = (kXCols.x0[c0 + OBS_COLS - 1] + 3) >> 2;
-    constexpr int NW = whi - wlo + 1;
-    static_assert(G >= 0 && G <= 3 && c0 + OBS_COLS <= 84 && whi < 64, "columns and taps inside the row");
-    uint32_t wv[NW];
+__device__ __forceinline__ uint32_t max_odd_bytes(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(mh_u16x2, a),
+                                                                  __builtin_bit_cast(mh_u16x2, b)));
+}
+// ---- INTER_AREA by periods (the step kernel's observation)
+// The horizontal sums of source row pixels 64 g .. 64 g + 63 for output columns 21 g .. 21 g + 20: per column
+// its 4 taps in order, as area_pixel's row sum (whose first step, +0 + a non-negative product, is the product
+// itself). Pixel 4 i + j (max-pooled if the env pools) is byte j of ev[i] for even j and of od[i] for odd j, so
+// that a max-pooled row needs no merge of the two packed maxima (both arrays are the row's words otherwise).
+__device__ __forceinline__ void obs_period_sums(const uint32_t (&ev)[16], const uint32_t (&od)[16], float (&rs)[21]) {
 #pragma unroll
-    for (int i = 0; i < NW; i++) wv[i] = rw[(uint32_t)(wlo + i) * stride + lane];
-#pragma unroll
-    for (int q = 0; q < OBS_COLS; q++) {
-        const int c = c0 + q;
+    for (int q = 0; q < 21; q++) {
         float row = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int px = kXCols.x0[c] + k;
-            row += (float)((wv[(px >> 2) - wlo] >> (8 * (px & 3))) & 0xffu) * xw[c][k];
+            const int px = kArea.x0[q] + k;
+            const uint32_t w = (px & 1) ? od[px >> 2] : ev[px >> 2];
+            const float t = (float)((w >> (8 * (px & 3))) & 0xffu) * kArea.xw[q][k];
+            row = k == 0 ? t : row + t;
         }
         rs[q] = row;
     }
 }
-__device__ __forceinline__ void obs_row_sums(int g, const uint32_t* rw, uint32_t stride, uint32_t lane,
-                                             const float (*xw)[4], float (&rs)[OBS_COLS]) {
-    switch (g) {
-        case 0: obs_row_sums<0>(rw, stride, lane, xw, rs); break;
-        case 1: obs_row_sums<1>(rw, stride, lane, xw, rs); break;
-        case 2: obs_row_sums<2>(rw, stride, lane, xw, rs); break;
-        default: obs_row_sums<3>(rw, stride, lane, xw, rs); break;
-    }
-}
 
-// The vertical step for source row sy: every (output row dy, tap j) from the current (dy, j) on, up to output
-// row dy_end, that takes row sy, in order (consecutive output rows take consecutive source rows, the one they
-// share summed once); emit(dy, acc) when output row dy is complete.
+// The vertical step for source row sy (0 .. 239) with its sums rs: adds them to the open output row `acc`
+// (which starts at +0: +0 + the first non-negative term is that term, as area_pixel's first step), and when the
+// row is complete calls emit(output row, acc) and opens the next one. The step is the same for every lane
+// (sy is uniform in the kernel), so its weights come from one table entry.
 template <class Emit>
-__device__ __forceinline__ void obs_rows_take(int sy, int& dy, int& j, int dy_end, const int32_t* ys, const float* yw,
-                                              const int32_t* yn, const float (&rs)[OBS_COLS], float (&acc)[OBS_COLS],
-                                              Emit&& emit) {
-    while (dy < dy_end && ys[dy * TAPS + j] == sy) {
-        const float w = yw[dy * TAPS + j];
+__device__ __forceinline__ void obs_period_take(int sy, const float (&rs)[21], float (&acc)[21], Emit&& emit) {
+    const int p = sy / 20;
+    const RowStep st = kRows.s[sy - 20 * p];
 #pragma unroll
-        for (int q = 0; q < OBS_COLS; q++) {
-            const float term = w * rs[q];
-            acc[q] = j == 0 ? term : acc[q] + term;
-        }
-        if (++j == yn[dy]) { emit(dy); dy++; j = 0; }
+    for (int q = 0; q < 21; q++) acc[q] = acc[q] + st.wa * rs[q];
+    if (st.last) {
+        emit(7 * p + st.q, acc);
+#pragma unroll
+        for (int q = 0; q < 21; q++) acc[q] = st.wb * rs[q];
     }
-}
-
-// output pixels 4 wq .. 4 wq + 3 of a column group as one word (pixel 4 wq + i in byte i)
-__device__ __forceinline__ uint32_t obs_word(const float (&acc)[OBS_COLS], int wq) {
-    return (uint32_t)round_sat(acc[4 * wq]) | (uint32_t)round_sat(acc[4 * wq + 1]) << 8 |
-           (uint32_t)round_sat(acc[4 * wq + 2]) << 16 | (uint32_t)round_sat(acc[4 * wq + 3]) << 24;
 }
 
 // ------------------------------------------------------------------ arguments
@@ -266,6 +311,12 @@ struct StepArgs {
     float* rew; uint8_t* term; uint8_t* trunc; int32_t* info; double* ep_ret_out; int32_t* ep_len_out;
     const uint8_t* key_bank;      // CHR bank of each (level, ROM) key (E_LEVEL)
     const int32_t* slot_env;      // env of each console slot (actions in and outputs out are in env order)
+    uint8_t* fresh;               // new observation of each slot: [e * OBS_PIX + o]
+    const uint8_t* boot_obs;      // boot observation of each level: [level * OBS_PIX + o]
+    uint32_t* obs_order;          // [0]: waves that finished their frame loop (0 at launch); [1 + k]: the first
+                                  // slot of the wave whose ticket is obs_late_from + k
+    uint32_t obs_late_from;       // waves with a ticket in [obs_late_from, obs_late_to) leave their
+    uint32_t obs_late_to;         // observations to k_obs_late (obs_late_to: the waves with live envs)
 };
 
 struct ResetArgs {
@@ -381,10 +432,13 @@ __device__ inline void cache_lane(const CacheArgs& A, const LaneCtx& x, int ci) 
 }
 
 // One agent step of the env in console slot e (fastmario.cpp:403-411 + 336-374).
-__device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e) {
+// Returns what the env's new observation needs: bit 0 pool, bit 1 the last frame is in frame buffer 1, bit 2
+// the boot observation, bits 8.. the level.
+__device__ inline uint32_t step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e) {
     const uint32_t o = (uint32_t)A.slot_env[e];   // the env's index in the action and output arrays
     Console c;
-    attach(c, x, A.mem, A.np, e, A.key_bank[A.ev[(size_t)E_LEVEL * A.np + e]]);
+    const uint32_t level = A.ev[(size_t)E_LEVEL * A.np + e];
+    attach(c, x, A.mem, A.np, e, A.key_bank[level]);
     c.load(A.sc, e);
     EnvRegs ev;
     load_env(ev, A.ev, A.np, e);
@@ -416,6 +470,7 @@ __device__ inline void step_lane(const StepArgs& A, const LaneCtx& x, uint32_t e
     for (int k = 0; k < 3; k++)
         if ((ev.reemu >> k) & 1u) A.ev[(size_t)(E_REEMU_ONE + k) * A.np + e] += 1;
     A.ev[(size_t)E_HACK_REDRAWS * A.np + e] += ev.hack_redraws;
+    return (ev.pooled ? 1u : 0u) | (ev.slot_swap ? 2u : 0u) | (ev.shows_boot ? 4u : 0u) | level << 8;
 }
 
 // Auto-reset (fastmario.cpp:389-401): k = integers(noop_max + 1) from the env's stream, the draws of

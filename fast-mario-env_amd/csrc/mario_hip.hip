@@ -1,11 +1,11 @@
 // mario_hip: batched Super Mario Bros env stepping on gfx950 — kernels and the C-ABI (include/mario_hip.h).
 //
-// One agent step of N envs is four kernels on the caller's stream:
-//   k_step          one lane per env: sticky draw, K frames of 6502 + catch-up PPU, reward/done/info,
-//                   hack frames, gray rendering of every frame into two alternating frame buffers
-//   k_obs           one thread per (env, 4 output columns, band of 21 output rows): 2-frame max + INTER_AREA
+// One agent step of N envs is three kernels on the caller's stream:
+//   k_step          4 lanes per env: sticky draw, K frames of 6502 + catch-up PPU, reward/done/info,
+//                   hack frames, gray rendering of every frame into two alternating frame buffers; then, per
+//                   wave, the 2-frame max + INTER_AREA of its envs' last frames (obs_tail)
 //   k_reset         one lane per env: finished envs take a cached (level, no-op count) start state
-//   k_stack         LDS-transposed frame-stack shift, final_obs, reset observation
+//   k_stack         frame-stack shift, final_obs, reset observation
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -77,6 +77,103 @@ static inline EmuLaunch emu_launch(int count, int cus) {
 // first console slot of this block (blocks of blockDim.x / 64 waves)
 __device__ __forceinline__ uint32_t block_base() { return blockIdx.x * ((blockDim.x >> 6) * ENVS_PER_WAVE); }
 
+// The new observation of a lane's env, output columns 21 g .. 21 g + 20 (g: the lane's part), into
+// fresh[e * OBS_PIX + o]: the boot observation right after a reset, else INTER_AREA of the last frame,
+// max-pooled with its partner frame (fastmario.cpp:377-386); `bits` as step_lane returns them; the output rows of
+// NP row periods from p0 (7 rows from 20 source rows each). k_step runs it for all 12 periods once the wave's
+// frame loop is over, on the frames the wave has just drawn, except in the waves that finish last, whose envs
+// k_obs_late takes with a wave per period. The 4 lanes of an env take the 4
+// column periods of the tables (AreaPeriod), so every lane runs the same code with constant taps and weights,
+// and the wave reads every frame byte once: a load takes word 16 g + i of a source row for the 16 envs of each
+// part (4 x 64 contiguous bytes). The loads of the next source row are in flight while a row is summed. The
+// float operations and their order are area_pixel's. Not inlined, so that its registers stay out of the frame
+// loop's allocation.
+typedef __attribute__((address_space(1))) uint8_t gbyte;       // global memory, addressed as such
+constexpr int kBufferWord3 = 0x00020000;   // buffer resource word 3 on gfx9: 32-bit raw (untyped) accesses
+// a wave-uniform 64-bit value, as such (the builtin returns a signed int: each half is taken as unsigned before
+// it is widened, so that the low half's bit 31 does not spread into the high half)
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (uint64_t)lo | (uint64_t)hi << 32;
+}
+template <int NP>
+__device__ __attribute__((noinline)) void obs_tail(const uint8_t* gray_, uint32_t np_, uint8_t* fresh_,
+                                                   const uint8_t* boot_obs, uint32_t e, uint32_t g, uint32_t bits,
+                                                   int p0) {
+    // The frames were stored by the env's lanes of this wave (streaming stores, and read-modify-writes whose loads
+    // may have left lines in this CU's L1): wait for the stores, and drop the L1's lines, before reading them.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // the arguments a call passes in vector registers: the buffers and np are the kernel's, the same in every lane
+    const gbyte* gray = (const gbyte*)uniform64((uint64_t)gray_);
+    gbyte* fresh = (gbyte*)uniform64((uint64_t)fresh_);
+    const uint32_t np = __builtin_amdgcn_readfirstlane(np_);
+    p0 = __builtin_amdgcn_readfirstlane(p0);          // the same in every lane of both callers' waves
+    gbyte* out = fresh + (size_t)e * OBS_PIX + 21 * g;
+    if (bits & 4) {
+        const uint8_t* b = boot_obs + (size_t)(bits >> 8) * OBS_PIX + 21 * g;
+        for (int d = 7 * p0; d < 7 * (p0 + NP); d++)
+            for (int q = 0; q < 21; q++) out[d * 84 + q] = b[d * 84 + q];
+        return;
+    }
+    const bool pool = (bits & 1) != 0, swap = (bits & 2) != 0, all_pool = __all(pool);
+    const size_t fb = (size_t)GRAY_PIX * np, rowb = (size_t)256 * np;   // bytes per frame buffer, per source row
+    const uint32_t lo = (16 * g * np + e) * 4, step = 4 * np;           // word 16 g of the row, the next word
+    uint32_t a0[16], b0[16], a1[16], b1[16];
+    // Source row sy of both frame buffers as buffer resources (base: the row, size: the row's 256 np bytes, so
+    // that no offset reaches past it), loaded with the lane's 32-bit word offsets: no 64-bit address per lane
+    // and word.
+    auto load = [&](int sy, uint32_t (&a)[16], uint32_t (&b)[16]) {
+        const __amdgpu_buffer_rsrc_t r0 =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(gray + (size_t)sy * rowb), 0, (int)rowb, kBufferWord3);
+        const __amdgpu_buffer_rsrc_t r1 =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(gray + fb + (size_t)sy * rowb), 0, (int)rowb, kBufferWord3);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            a[i] = __builtin_amdgcn_raw_buffer_load_b32(r0, (int)(lo + (uint32_t)i * step), 0, 0);
+            b[i] = __builtin_amdgcn_raw_buffer_load_b32(r1, (int)(lo + (uint32_t)i * step), 0, 0);
+        }
+    };
+    float acc[21];
+#pragma unroll
+    for (int q = 0; q < 21; q++) acc[q] = 0.f;
+    auto row = [&](int sy, const uint32_t (&a)[16], const uint32_t (&b)[16]) {
+        uint32_t ev[16], od[16];
+        if (all_pool) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) { ev[i] = max_even_bytes(a[i], b[i]); od[i] = max_odd_bytes(a[i], b[i]); }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t w = swap ? b[i] : a[i];
+                ev[i] = pool ? max_even_bytes(a[i], b[i]) : w;
+                od[i] = pool ? max_odd_bytes(a[i], b[i]) : w;
+            }
+        }
+        float rs[21];
+        obs_period_sums(ev, od, rs);
+        obs_period_take(sy, rs, acc, [&](int dy, const float (&v)[21]) {
+            gbyte* o = out + dy * 84;
+#pragma unroll
+            for (int q = 0; q < 21; q++) o[q] = round_sat(v[q]);
+        });
+    };
+    // the 20 source rows of each of periods p0 .. p0 + NP - 1 (output rows 7 p .. 7 p + 6); acc is +0 at every
+    // period's start
+    for (int pi = 0; pi < NP; pi++) {
+        const int sy0 = 20 * (p0 + pi);
+        load(sy0, a0, b0);
+#pragma nounroll
+        for (int r = 0; r < 20; r += 2) {
+            load(sy0 + r + 1, a1, b1);
+            row(sy0 + r, a0, b0);
+            if (r + 2 < 20) load(sy0 + r + 2, a0, b0);
+            row(sy0 + r + 1, a1, b1);
+        }
+    }
+}
+
 __global__ void EMU_BOUNDS k_boot(BootArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
@@ -96,9 +193,49 @@ __global__ void EMU_BOUNDS k_cache(CacheArgs A) {
 __global__ void EMU_BOUNDS k_step(StepArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
+    // The frame loop issues ahead of the observations of the waves that have finished it (on a SIMD, the two
+    // waves' instructions are arbitrated by this priority first).
+    __builtin_amdgcn_s_setprio(2);
     const int slot = lane_slot();
     const uint32_t e = block_base() + (uint32_t)slot;
-    if (e < (uint32_t)A.n) step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
+    const bool live = e < (uint32_t)A.n;
+    uint32_t bits = 0;
+    if (live) bits = step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
+    if (!__any(live)) return;
+    // The wave's ticket: its place in the order in which the waves finish their frame loops (a vector atomic
+    // from one lane). The waves that finish last would hold the kernel's end with their observations; they
+    // leave them to k_obs_late, which spreads an env's rows over 12 waves.
+    uint32_t ticket = 0;
+    if (__lane_id() == 0) ticket = atomicAdd(A.obs_order, 1u);
+    ticket = (uint32_t)__builtin_amdgcn_readfirstlane(ticket);
+    if (ticket >= A.obs_late_from && ticket < A.obs_late_to) {
+        if (__lane_id() == 0) A.obs_order[1 + ticket - A.obs_late_from] = e;   // lane 0 holds the wave's first slot
+    } else if (live) {
+        __builtin_amdgcn_s_setprio(0);
+        obs_tail<12>(A.gray, A.np, A.fresh, A.boot_obs, e, lane_part(), bits, 0);
+    }
+}
+
+// The observations of the envs of the waves that finished k_step's frame loop last (obs_tail, one wave per
+// (deferred wave, row period): 12 waves per env group instead of one), then k_step's counter back to 0.
+struct ObsLateArgs {
+    int n; uint32_t np; int waves;       // deferred waves (their first slots at order[1 ..])
+    const uint32_t* ev;
+    const uint8_t* gray; uint8_t* fresh; const uint8_t* boot_obs;
+    uint32_t* order;
+};
+constexpr int OBS_LATE_MAX = 64;         // waves that may defer
+__global__ void __launch_bounds__(256) k_obs_late(ObsLateArgs A) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) A.order[0] = 0;   // k_step is over: no ticket is taken any more
+    const int u = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));   // (deferred wave u / 12, row period u % 12)
+    if (u >= A.waves * 12) return;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t e = A.order[1 + u / 12] + (lane & (ENVS_PER_WAVE - 1));   // k_step's lanes: env slot, part
+    if (e >= (uint32_t)A.n) return;
+    const uint32_t pw = A.ev[(size_t)E_POOLED * A.np + e];
+    const uint32_t bits = (pw & 3u) | (A.ev[(size_t)E_SHOWS_BOOT * A.np + e] ? 4u : 0u) |
+                          A.ev[(size_t)E_LEVEL * A.np + e] << 8;
+    obs_tail<1>(A.gray, A.np, A.fresh, A.boot_obs, e, lane / ENVS_PER_WAVE, bits, u % 12);
 }
 
 __global__ void EMU_BOUNDS k_raw(RawArgs A) {
@@ -143,129 +280,21 @@ __global__ void k_small_obs(SmallObsArgs A) {
     A.out[(size_t)i * OBS_PIX + o] = v;
 }
 
-struct ObsArgs {
-    int n; uint32_t np;
-    const uint32_t* ev;
-    const uint8_t* gray;          // 2 frame buffers of np lanes (4-pixel words)
-    const uint8_t* boot_obs;      // [level * OBS_PIX + o]
-    uint8_t* out;                 // word w (pixels 4w .. 4w+3) of env e at 32-bit word [w * np + e]
-    const AreaTables* T;
-};
-// New observation of every env: the boot observation right after a reset, else INTER_AREA of the last
-// frame, max-pooled with its partner frame (fastmario.cpp:377-386). E_POOLED bit 0: pool; bit 1: the
-// last frame is in frame buffer 1 (the episode ended at an agent frame of the other parity than K-1).
-// Block: 64 envs (a wave's lanes) x a band of OBS_BAND_ROWS output rows; wave g sums output columns
-// 20 g .. 20 g + 23 and stores 20 g .. 20 g + 19 (wave 3: all 24, 60 .. 83). The band's source rows are staged in LDS one at a time, double
-// buffered: all 256 threads load a row's 64 words of the 64 envs (each load 64 consecutive envs' word, 256
-// contiguous bytes), max-pool them and store them, and while row sy is summed from LDS the loads of row
-// sy + 1 are in flight. Every source byte is read from HBM once. The float operations and their order are
-// area_pixel's: per source row and column the taps in order, per output row the source rows in order, a
-// source row shared by two output rows summed once.
-constexpr int OBS_BAND_ROWS = 21;   // output rows per block: 4 bands
-__global__ void __launch_bounds__(256) k_obs(ObsArgs A) {
-    __shared__ uint32_t srow[2][64 * 64];          // [buffer][word * 64 + env]: one source row of the 64 envs
-    __shared__ int32_t s_ys[84 * TAPS], s_yn[84];
-    __shared__ __attribute__((aligned(16))) float s_xw[84][4];   // a column's 4 tap weights (+0 past its tap count)
-    __shared__ float s_yw[84 * TAPS];   // (in LDS: a table load from memory would wait for the row loads)
-    const int lane = threadIdx.x & 63, g = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t e = blockIdx.x * 64 + lane;       // < np: the buffers hold np lanes
-    const int dy0 = OBS_BAND_ROWS * blockIdx.y, dy1 = dy0 + OBS_BAND_ROWS;
-    const AreaTables* T = A.T;
-    for (int i = threadIdx.x; i < 84; i += 256) {
-        s_yn[i] = T->yn[i];
-        for (int k = 0; k < 4; k++) s_xw[i][k] = T->xw[i * TAPS + k];
-    }
-    for (int i = threadIdx.x; i < 84 * TAPS; i += 256) { s_ys[i] = T->ys[i]; s_yw[i] = T->yw[i]; }
-    // this thread's loads: words 16 g .. 16 g + 15 of a row of env e
-    const uint32_t pw = A.ev[(size_t)E_POOLED * A.np + e];
-    const bool pool = (pw & 1) != 0;
-    const uint32_t* gl = (const uint32_t*)(A.gray + ((pw & 2) ? (size_t)GRAY_PIX * A.np : 0));   // the last frame
-    const uint32_t* gp = (const uint32_t*)(A.gray + ((pw & 2) ? 0 : (size_t)GRAY_PIX * A.np));   // its partner
-    // the loads land in la / lb and are max-pooled only when stored, so that they stay in flight while the
-    // previous row is summed
-    // (both buffers hold np lanes whether or not the env pools, so the wave loads both when any lane pools)
-    uint32_t la[16], lb[16];
-    const bool any_pool = __any(pool);
-    auto load_row = [&](int sy) {
-        const size_t w0 = (size_t)((uint32_t)sy * 64 + 16 * g) * A.np + e;
-        if (any_pool) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) { la[i] = gl[w0 + (size_t)i * A.np]; lb[i] = gp[w0 + (size_t)i * A.np]; }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) { la[i] = gl[w0 + (size_t)i * A.np]; lb[i] = 0u; }
-        }
-    };
-    auto store_row = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) srow[buf][(16 * g + i) * 64 + lane] = pool ? max_u8x4(la[i], lb[i]) : la[i];
-    };
-    // every wave sums 24 columns from 20 g (waves 0-2 also sum the next wave's first 4, and do not store them)
-    const int c0 = 20 * g, nw = g == 3 ? 6 : 5;
-    float acc[OBS_COLS], rs[OBS_COLS];
-#pragma unroll
-    for (int q = 0; q < OBS_COLS; q++) { acc[q] = 0.f; rs[q] = 0.f; }
-    const int sy_lo = T->ys[dy0 * TAPS], sy_hi = T->ys[(dy1 - 1) * TAPS + T->yn[dy1 - 1] - 1];
-    load_row(sy_lo);
-    store_row(0);
-    __syncthreads();
-    const bool boot = A.ev[(size_t)E_SHOWS_BOOT * A.np + e] != 0;
-    const uint8_t* bsrc = A.boot_obs + (size_t)A.ev[(size_t)E_LEVEL * A.np + e] * OBS_PIX;
-    int dy = dy0, j = 0;
-    for (int sy = sy_lo; sy <= sy_hi; sy++) {
-        const int buf = (sy - sy_lo) & 1;
-        if (sy < sy_hi) load_row(sy + 1);
-        // the row's horizontal sums of this wave's columns, then the output rows that take the row
-        obs_row_sums(g, srow[buf], 64, lane, s_xw, rs);
-        obs_rows_take(sy, dy, j, dy1, s_ys, s_yw, s_yn, rs, acc, [&](int d) {
-            // the output row's words of this wave's columns: word (d, c / 4) of env e at [(d * 21 + c / 4) * np + e]
-            if (e >= (uint32_t)A.n) return;
-            uint32_t* out = (uint32_t*)A.out + ((size_t)d * 21 + c0 / 4) * A.np + e;
-#pragma unroll
-            for (int wq = 0; wq < OBS_COLS / 4; wq++) {
-                if (wq < nw) {
-                    uint32_t v;
-                    if (boot) {
-                        const uint8_t* b = bsrc + d * 84 + c0 + 4 * wq;
-                        v = (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24;
-                    } else {
-                        v = obs_word(acc, wq);
-                    }
-                    out[(size_t)wq * A.np] = v;
-                }
-            }
-        });
-        if (sy < sy_hi) store_row(buf ^ 1);
-        __syncthreads();
-    }
-}
-
 struct StackArgs {
     int n; uint32_t np; int K;
     uint8_t* obs; uint8_t* fin;   // [env][K][OBS_PIX]
     const int32_t* slot_env;      // env of each console slot
-    const uint8_t* fresh;         // word w (pixels 4w .. 4w+3) of env e at 32-bit word [w * np + e]
+    const uint8_t* fresh;         // new observation of slot e at [e * OBS_PIX + o]
     const uint32_t* ev;
     const uint8_t* cobs;          // [ci * OBS_PIX + o]
     int mode;                     // 0 step, 1 reset
 };
 // Frame stack, final_obs, reset observation (fastmario.cpp:477-504). Block: 64 envs x 64 words of one
-// frame; the fresh frame is read lane-interleaved and transposed through LDS.
+// frame; consecutive threads take consecutive words of one env.
 __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
-    __shared__ uint32_t tile[64][65];
-    const uint32_t e0 = blockIdx.x * 64;   // env groups vary fastest: neighbouring workgroups read adjacent fresh words
+    const uint32_t e0 = blockIdx.x * 64;   // env groups vary fastest: neighbouring workgroups read adjacent envs
     const int w0 = blockIdx.y * 64;        // word index within a frame (OBS_PIX / 4 = 1764 words)
     const int nw = OBS_PIX / 4;
-    if (A.mode == 0) {
-        for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
-            const int wl = idx >> 6, j = idx & 63;
-            const uint32_t e = e0 + j;
-            uint32_t val = 0;
-            if (w0 + wl < nw && e < (uint32_t)A.n) val = ((const uint32_t*)A.fresh)[(size_t)(w0 + wl) * A.np + e];
-            tile[wl][j] = val;
-        }
-    }
-    __syncthreads();
     const size_t fw = (size_t)nw * A.K;   // words per env stack
     for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
         const int j = idx >> 6, wl = idx & 63;
@@ -280,7 +309,7 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
             st[(size_t)(A.K - 1) * nw + w] = ((const uint32_t*)A.cobs)[(size_t)ri * nw + w];
             continue;
         }
-        const uint32_t fresh = tile[wl][j];
+        const uint32_t fresh = ((const uint32_t*)A.fresh)[(size_t)e * nw + w];
         if (ri != 0xffffffffu) {
             uint32_t* fo = (uint32_t*)A.fin + env * fw;
             for (int s = 0; s < A.K - 1; s++) { fo[(size_t)s * nw + w] = st[(size_t)(s + 1) * nw + w]; st[(size_t)s * nw + w] = 0; }
@@ -294,24 +323,12 @@ __global__ void __launch_bounds__(256) k_stack(StackArgs A) {
 }
 
 // k_stack with 16-byte accesses, for obs / fin buffers (and the reset cache) 16-byte aligned: the same block
-// (64 envs x 64 words of a frame, the fresh words transposed through LDS), but a thread moves 4 consecutive
-// words of one env per access (16 threads per env, 16 envs per pass, 4 passes), and reads the env's slot and
-// reset index once per pass.
+// (64 envs x 64 words of a frame), but a thread moves 4 consecutive words of one env per access (16 threads per
+// env, 16 envs per pass, 4 passes), and reads the env's slot and reset index once per pass.
 __global__ void __launch_bounds__(256) k_stack4(StackArgs A) {
-    __shared__ uint32_t tile[64][65];
     const uint32_t e0 = blockIdx.x * 64;
     const int w0 = blockIdx.y * 64;
     const int nw = OBS_PIX / 4;
-    if (A.mode == 0) {
-        for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
-            const int wl = idx >> 6, j = idx & 63;
-            const uint32_t e = e0 + j;
-            uint32_t val = 0;
-            if (w0 + wl < nw && e < (uint32_t)A.n) val = ((const uint32_t*)A.fresh)[(size_t)(w0 + wl) * A.np + e];
-            tile[wl][j] = val;
-        }
-    }
-    __syncthreads();
     const size_t fw = (size_t)nw * A.K;   // words per env stack
     const int g = threadIdx.x & 15, w = w0 + 4 * g;   // this thread's 4 words: w .. w + 3 (nw is a multiple of 4)
     for (int pass = 0; pass < 4; pass++) {
@@ -327,7 +344,7 @@ __global__ void __launch_bounds__(256) k_stack4(StackArgs A) {
             st[(A.K - 1) * fq] = *(const uint4*)((const uint32_t*)A.cobs + (size_t)ri * nw + w);
             continue;
         }
-        const uint4 fresh = make_uint4(tile[4 * g][j], tile[4 * g + 1][j], tile[4 * g + 2][j], tile[4 * g + 3][j]);
+        const uint4 fresh = *(const uint4*)((const uint32_t*)A.fresh + (size_t)e * nw + w);
         if (ri != 0xffffffffu) {
             uint4* fo = (uint4*)((uint32_t*)A.fin + env * fw + w);
             for (int s = 0; s < A.K - 1; s++) { fo[s * fq] = st[(s + 1) * fq]; st[s * fq] = make_uint4(0, 0, 0, 0); }
@@ -638,6 +655,7 @@ struct MhEnv {
     RomArgs R{};
     AreaTables* T = nullptr;
     uint8_t *mem = nullptr, *gray = nullptr, *fresh = nullptr;
+    uint32_t* obs_order = nullptr;     // k_step's finish counter and the deferred waves (k_obs_late)
     uint32_t *sc = nullptr, *ev = nullptr;
     uint8_t* snap_mem = nullptr;     // 2 snapshot slots of the live consoles (early-termination re-emulation)
     uint32_t* snap_sc = nullptr;
@@ -783,6 +801,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     h->snap_mem = B.alloc<uint8_t>((size_t)2 * MEM_ROWS * h->np, good);
     h->snap_sc = B.alloc<uint32_t>((size_t)2 * S_COUNT * h->np, good);
     h->fresh = B.alloc<uint8_t>((size_t)OBS_PIX * h->np, good);
+    h->obs_order = B.alloc<uint32_t>(1 + OBS_LATE_MAX, good);
     h->boot_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->nlp, good);
     h->boot_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->nlp, good);
     h->boot_gray = B.alloc<uint8_t>((size_t)GRAY_PIX * h->nlp, good);
@@ -804,7 +823,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     if (!good) return fail();
     AreaTables T;
     area_tables(&T);
-    if (!x_cols_match(T)) { g_err = "INTER_AREA column taps differ from the compiled-in positions"; return fail(); }
+    if (!area_period_match(T)) { g_err = "INTER_AREA tables differ from the compiled-in periods"; return fail(); }
     // per-env words: level, RNG, lives = -1 (reset() installs the real start state)
     std::vector<uint32_t> ev((size_t)E_COUNT * h->np, 0);
     for (int i = 0; i < n; i++) {
@@ -914,14 +933,17 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
     CK(hipSetDevice(h->device));
     hipStream_t s = (hipStream_t)stream;
     if (mark(h, s, 0)) return -1;
+    // waves with live envs, and how many of the last to finish defer their observations
+    const int waves = (h->n + ENVS_PER_WAVE - 1) / ENVS_PER_WAVE, late = std::min(waves, OBS_LATE_MAX);
     StepArgs sa{h->R, h->cfg, h->n, h->np, h->mem, h->sc, h->ev, h->gray, h->snap_mem, h->snap_sc, d_actions,
-                h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len, h->key_bank, h->slot_env};
+                h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len, h->key_bank, h->slot_env, h->fresh,
+                h->boot_obs, h->obs_order, (uint32_t)(waves - late), (uint32_t)waves};
     const EmuLaunch ls = emu_launch(h->n, h->cus);
     hipLaunchKernelGGL(k_step, ls.grid, ls.block, 0, s, sa);
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
-    ObsArgs oa{h->n, h->np, h->ev, h->gray, h->boot_obs, h->fresh, h->T};
-    hipLaunchKernelGGL(k_obs, dim3(h->np / 64, 84 / OBS_BAND_ROWS), dim3(256), 0, s, oa);
+    const ObsLateArgs la{h->n, h->np, late, h->ev, h->gray, h->fresh, h->boot_obs, h->obs_order};
+    hipLaunchKernelGGL(k_obs_late, dim3((unsigned)((late * 12 + 3) / 4)), dim3(256), 0, s, la);
     CK(hipGetLastError());
     if (mark(h, s, 2)) return -1;
     hipLaunchKernelGGL(k_reset, dim3(h->np / 64), dim3(64), 0, s, h->reset_args(0));

@@ -288,7 +288,7 @@ class HipVecEnv:
     def bytes_per_env(self) -> int:
         return int(lib().mh_env_bytes(self.h))
 
-    STAGES = ("k_step", "k_obs", "k_reset", "k_stack")
+    STAGES = ("k_step", "k_obs_late", "k_reset", "k_stack")
 
     def timing(self, enable: bool = True):
         """Start (or stop) per-stage HIP-event timing of step(); read it with timing_read()."""

@@ -79,8 +79,9 @@ int mh_step_wait(MhEnv* h, void* stream);
 void mh_destroy(MhEnv* h);
 
 /* Per-stage timing of mh_step_async with HIP events recorded on the step's own stream (no counterpart
- * in the reference; used by the benchmark). Stages: 0 k_step (emulation + render), 1 k_obs (max-pool +
- * INTER_AREA), 2 k_reset, 3 k_stack. mh_timing(h, 1) clears and starts
+ * in the reference; used by the benchmark). Stages: 0 k_step (emulation, render, and the max-pool +
+ * INTER_AREA observation of most envs), 1 k_obs_late (the observation of the envs of the waves that finish
+ * k_step last), 2 k_reset, 3 k_stack. mh_timing(h, 1) clears and starts
  * recording; mh_timing_read synchronizes and returns the summed milliseconds per stage and the number
  * of timed steps. */
 #define MH_STAGES 4

@@ -257,7 +257,7 @@ int run_env(const char* cfg_file) {
                 uint8_t* st0 = word(v.obs, e * fw);
                 auto st = [&](size_t s) { return st0 + 4 * (s * nw + w); };
                 uint8_t fresh[4];
-                for (int b = 0; b < 4; b++) fresh[b] = v.fresh[(w * np + e) * 4 + b];
+                for (int b = 0; b < 4; b++) fresh[b] = v.fresh[(size_t)e * OBS_PIX + 4 * w + b];
                 const uint8_t* cw = v.cobs.data() + 4 * ((size_t)ri * nw + w);
                 if (mode == 1) {
                     for (int s = 0; s < stack - 1; s++) memset(st(s), 0, 4);
@@ -274,38 +274,32 @@ int run_env(const char* cfg_file) {
             }
         }
     };
-    // k_obs: the boot observation right after a reset, else INTER_AREA of the last frame, max-pooled; the
-    // kernel's row sums and vertical steps, each source row staged as 64 words (stride 1) instead of in LDS
-    float xw[84][4];
-    for (int c = 0; c < 84; c++)
-        for (int k = 0; k < 4; k++) xw[c][k] = v.T.xw[c * TAPS + k];
-    auto do_obs = [&]() {
+    // k_step's obs_tail: the boot observation right after a reset, else INTER_AREA of the last frame,
+    // max-pooled; per env its 4 column periods one after another, with the kernel's row sums and vertical steps
+    // (bits: what step_lane returned for the env)
+    auto do_obs = [&](const std::vector<uint32_t>& bits) {
         for (int e = 0; e < n; e++) {
-            uint32_t* fresh = (uint32_t*)v.fresh.data();
-            if (v.ev[(size_t)E_SHOWS_BOOT * np + e]) {
-                const uint8_t* src = v.boot_obs.data() + (size_t)v.ev[(size_t)E_LEVEL * np + e] * OBS_PIX;
-                for (int w = 0; w < OBS_PIX / 4; w++) {
-                    const uint8_t* b = src + 4 * w;
-                    fresh[(size_t)w * np + e] = (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24;
-                }
+            uint8_t* out = v.fresh.data() + (size_t)e * OBS_PIX;
+            const uint32_t b = bits[e];
+            if (b & 4) {
+                memcpy(out, v.boot_obs.data() + (size_t)(b >> 8) * OBS_PIX, OBS_PIX);
                 continue;
             }
-            const uint32_t pw = v.ev[(size_t)E_POOLED * np + e];
-            const uint32_t* gl = (const uint32_t*)(v.gray.data() + ((pw & 2) ? (size_t)GRAY_PIX * np : 0));
-            const uint32_t* gp = (const uint32_t*)(v.gray.data() + ((pw & 2) ? 0 : (size_t)GRAY_PIX * np));
+            const uint32_t* g0 = (const uint32_t*)v.gray.data();
+            const uint32_t* g1 = (const uint32_t*)(v.gray.data() + (size_t)GRAY_PIX * np);
             for (int g = 0; g < 4; g++) {
-                float acc[OBS_COLS] = {}, rs[OBS_COLS];
-                int dy = 0, j = 0;
-                const int c0 = 20 * g, nw = g == 3 ? 6 : 5;
+                float acc[21] = {}, rs[21];
                 for (int sy = 0; sy < 240; sy++) {
-                    uint32_t row[64];
-                    for (int i = 0; i < 64; i++) {
-                        const size_t wi = (size_t)(sy * 64 + i) * np + e;
-                        row[i] = (pw & 1) ? max_u8x4(gl[wi], gp[wi]) : gl[wi];
+                    uint32_t ev[16], od[16];
+                    for (int i = 0; i < 16; i++) {
+                        const size_t wi = (size_t)(sy * 64 + 16 * g + i) * np + e;
+                        const uint32_t w = (b & 2) ? g1[wi] : g0[wi];
+                        ev[i] = (b & 1) ? max_even_bytes(g0[wi], g1[wi]) : w;
+                        od[i] = (b & 1) ? max_odd_bytes(g0[wi], g1[wi]) : w;
                     }
-                    obs_row_sums(g, row, 1, 0, xw, rs);
-                    obs_rows_take(sy, dy, j, 84, v.T.ys, v.T.yw, v.T.yn, rs, acc, [&](int d) {
-                        for (int wq = 0; wq < nw; wq++) fresh[((size_t)d * 21 + c0 / 4 + wq) * np + e] = obs_word(acc, wq);
+                    obs_period_sums(ev, od, rs);
+                    obs_period_take(sy, rs, acc, [&](int dy, const float (&a)[21]) {
+                        for (int q = 0; q < 21; q++) out[dy * 84 + 21 * g + q] = round_sat(a[q]);
                     });
                 }
             }
@@ -323,9 +317,11 @@ int run_env(const char* cfg_file) {
             get(actions.data(), actions.size() * 8);
             StepArgs sa{L.R, v.cfg, n, np, v.mem.data(), v.sc.data(), v.ev.data(), v.gray.data(), v.snap_mem.data(),
                         v.snap_sc.data(), actions.data(), v.rew.data(), v.term.data(), v.trunc.data(), v.info.data(),
-                        v.ep_ret.data(), v.ep_len.data(), v.key_bank.data(), v.slot_env.data()};
-            for (int e = 0; e < n; e++) step_lane(sa, L.ctx(e), (uint32_t)e);
-            do_obs();
+                        v.ep_ret.data(), v.ep_len.data(), v.key_bank.data(), v.slot_env.data(), v.fresh.data(),
+                        v.boot_obs.data()};
+            std::vector<uint32_t> bits(n);
+            for (int e = 0; e < n; e++) bits[e] = step_lane(sa, L.ctx(e), (uint32_t)e);
+            do_obs(bits);
             do_reset(0);
             do_stack(0);
             std::vector<int64_t> info64(v.info.begin(), v.info.end()), epl64(v.ep_len.begin(), v.ep_len.end());

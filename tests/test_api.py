@@ -133,7 +133,8 @@ def test_no_cpu_fallback():
 
 def test_resize_kernel_has_no_fma(tmp_path):
     """The INTER_AREA float sums must not be contracted into FMAs (bit-exactness with the reference's
-    -ffp-contract=off build): compile the device code to gfx950 assembly and inspect the obs kernels."""
+    -ffp-contract=off build): compile the device code to gfx950 assembly and inspect the obs code (k_step's
+    obs_tail, a function of its own, and the kernels for reset-cache entries and images)."""
     src = os.path.join(ROOT, "fast-mario-env_amd", "csrc", "mario_hip.hip")
     out = tmp_path / "dev.s"
     sys.path.insert(0, os.path.join(ROOT, "fast-mario-env_amd"))
@@ -145,8 +146,8 @@ def test_resize_kernel_has_no_fma(tmp_path):
     assert r.returncode == 0, r.stderr[-2000:]
     asm = out.read_text()
     checked = 0
-    for name in ("k_obs", "k_small_obs", "k_resize_images"):
-        m = re.search(rf"^(_Z\w*{name}\w*):[^\n]*$(.*?)^\s*s_endpgm", asm, re.S | re.M)
+    for name in ("obs_tail", "k_small_obs", "k_resize_images"):
+        m = re.search(rf"^(_Z\w*{name}\w*):[^\n]*$(.*?)^\s*(s_endpgm|s_setpc_b64)", asm, re.S | re.M)
         assert m, name
         body = m.group(2)
         assert "v_mul_f32" in body and "v_add_f32" in body
