@@ -15,8 +15,8 @@ raw: the raw-emulator configuration: 4,096 consoles, skip 1, no wrappers, every 
 ppo / replay: the PPO rollout feeding a Nature CNN, and the GPU FrameReplay.
 
 The ROM is the real one when the reference's lookup finds it, else this repository's synthetic NROM stand-in
-(tests/golden/roms/mini_smb_*.nes); the JSON line names which. One step is one mh_step_async (k_step, k_obs,
-k_reset, k_stack) or, for raw, one frame and its outputs, on torch's current stream with inputs resident in
+(tests/golden/roms/mini_smb_*.nes); the JSON line names which. One step is one mh_step_async (k_step,
+k_obs_late, k_reset, k_stack) or, for raw, one frame and its outputs, on torch's current stream with inputs resident in
 HBM. Before the W warm-up steps, --preroll untimed steps carry the envs past their first episodes so that the
 timed window has episode ends, resets and early-termination re-emulations in it (the first steps after a
 reset are the cheapest ones). K steps are timed between two device synchronizations; per-kernel times come
@@ -42,12 +42,13 @@ for _p in (os.path.join(ROOT, "fast-mario-env_amd"), os.path.join(ROOT, "tests")
 METRIC = "agent env-steps/sec (skip=4) at 32768 envs on 1 MI355X; % HBM/VALU roofline"
 HBM_PEAK_GBS = 8000.0
 # bytes k_step must move per env and agent step: console state read + write,
-# env words read + write, action, reward / term / trunc / info out; ep stats on episode end.
+# env words read + write, action, reward / term / trunc / info out, the new 84x84 observation out;
+# ep stats on episode end.
 STATE_BYTES = 4384 + 4 * 41
 ENV_WORD_BYTES = 4 * 30
-K_STEP_BYTES = 2 * STATE_BYTES + 2 * ENV_WORD_BYTES + 8 + 4 + 1 + 1 + 40
-K_STEP_DONE_BYTES = 12
 OBS = 84 * 84
+K_STEP_BYTES = 2 * STATE_BYTES + 2 * ENV_WORD_BYTES + 8 + 4 + 1 + 1 + 40 + OBS
+K_STEP_DONE_BYTES = 12
 SIMPLE_BUTTONS = (0x00, 0x80, 0x81, 0x82, 0x83, 0x01, 0x40)
 
 
@@ -422,8 +423,8 @@ def env_line(args, metric, n, m, workload_key, config, dtype="u8"):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
                      "traffic": traffic_from_profiles(workload_key), "algorithmic_bytes_per_launch": round(k_bytes),
                      "note": "the live HBM figure of k_step's algorithmic bytes (console state, env words, action, "
-                             "outputs); k_step is bound by VALU issue and dependent latency, not by HBM: see "
-                             "valu_roofline"},
+                             "outputs, new observation); k_step is bound by VALU issue and dependent latency, not "
+                             "by HBM: see valu_roofline"},
         "valu_roofline": valu_roofline(workload_key),
         "stages_ms_per_step": {k: round(v, 3) for k, v in m["stages"].items()},
         "p_done": round(m["p_done"], 5),
