@@ -123,7 +123,8 @@ __device__ __attribute__((noinline)) void obs_tail(const uint8_t* gray_, uint32_
     uint32_t a0[16], b0[16], a1[16], b1[16];
     // Source row sy of both frame buffers as buffer resources (base: the row, size: the row's 256 np bytes, so
     // that no offset reaches past it), loaded with the lane's 32-bit word offsets: no 64-bit address per lane
-    // and word.
+    // and word. The loads are streaming (cache policy nt, aux bit 1): the frames are read once, and the
+    // console state of the waves still in their frame loops stays in the L2.
     auto load = [&](int sy, uint32_t (&a)[16], uint32_t (&b)[16]) {
         const __amdgpu_buffer_rsrc_t r0 =
             __builtin_amdgcn_make_buffer_rsrc((void*)(gray + (size_t)sy * rowb), 0, (int)rowb, kBufferWord3);
@@ -131,8 +132,8 @@ __device__ __attribute__((noinline)) void obs_tail(const uint8_t* gray_, uint32_
             __builtin_amdgcn_make_buffer_rsrc((void*)(gray + fb + (size_t)sy * rowb), 0, (int)rowb, kBufferWord3);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            a[i] = __builtin_amdgcn_raw_buffer_load_b32(r0, (int)(lo + (uint32_t)i * step), 0, 0);
-            b[i] = __builtin_amdgcn_raw_buffer_load_b32(r1, (int)(lo + (uint32_t)i * step), 0, 0);
+            a[i] = __builtin_amdgcn_raw_buffer_load_b32(r0, (int)(lo + (uint32_t)i * step), 0, 2);
+            b[i] = __builtin_amdgcn_raw_buffer_load_b32(r1, (int)(lo + (uint32_t)i * step), 0, 2);
         }
     };
     float acc[21];
