@@ -207,6 +207,8 @@ int run_env(const char* cfg_file) {
     v.obs.assign(stack_bytes, 0); v.fin.assign(stack_bytes, 0); v.term.assign(n, 0); v.trunc.assign(n, 0);
     v.rew.assign(n, 0.f); v.info.assign((size_t)10 * n, 0); v.ep_ret.assign(n, 0.0); v.ep_len.assign(n, 0);
     area_tables(&v.T);
+    // the library creates an env only if the run-time tables are the compiled-in periods that obs_tail uses
+    if (!area_period_match(v.T)) die("INTER_AREA tables differ from the compiled-in periods");
     for (int i = 0; i < n; i++) {
         auto w = [&](int k) -> uint32_t& { return v.ev[(size_t)k * np + i]; };
         w(E_LEVEL) = (uint32_t)env_level[i];
