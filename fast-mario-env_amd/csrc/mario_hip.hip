@@ -352,8 +352,12 @@ __global__ void __launch_bounds__(256) k_stack4(StackArgs A) {
             fo[(A.K - 1) * fq] = fresh;
             st[(A.K - 1) * fq] = *(const uint4*)((const uint32_t*)A.cobs + (size_t)ri * nw + w);
         } else {
-            for (int s = 0; s < A.K - 1; s++) st[s * fq] = st[(s + 1) * fq];
-            st[(A.K - 1) * fq] = fresh;
+            // streaming stores: the stacks are read next by the caller, not by a kernel of this step
+            // (0.453 -> 0.422 ms at 32,768 envs)
+            typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+            v4u* sv = (v4u*)st;
+            for (int s = 0; s < A.K - 1; s++) __builtin_nontemporal_store(sv[(s + 1) * fq], &sv[s * fq]);
+            __builtin_nontemporal_store(*(const v4u*)&fresh, &sv[(A.K - 1) * fq]);
         }
     }
 }
