@@ -110,6 +110,37 @@ constexpr bool area_period_shape() {
 }
 static_assert(area_period_shape(), "every column takes 4 pixels of its period, every row 1-4 rows of its period");
 
+// The whole tables at compile time: area_taps_cx for every output index (the same double operations as
+// area_taps), for kernels that take the tables from a statically initialised device array.
+constexpr AreaTables area_tables_cx() {
+    AreaTables T{};
+    for (int d = 0; d < 84; d++) {
+        int idx[TAPS] = {}, n = 0;
+        float w[TAPS] = {};
+        area_taps_cx(256, 84, d, idx, w, n);
+        T.xn[d] = n;
+        for (int k = 0; k < n; k++) { T.xs[d * TAPS + k] = idx[k]; T.xw[d * TAPS + k] = w[k]; }
+        int jdx[TAPS] = {}, m = 0;
+        float v[TAPS] = {};
+        area_taps_cx(240, 84, d, jdx, v, m);
+        T.yn[d] = m;
+        for (int k = 0; k < m; k++) { T.ys[d * TAPS + k] = jdx[k]; T.yw[d * TAPS + k] = v[k]; }
+    }
+    return T;
+}
+constexpr AreaTables kAreaTables = area_tables_cx();
+
+// Two tables equal entry for entry (weights compared as bit patterns).
+inline bool area_tables_equal(const AreaTables& a, const AreaTables& b) {
+    for (int i = 0; i < 84 * TAPS; i++)
+        if (a.xs[i] != b.xs[i] || a.ys[i] != b.ys[i] || __builtin_bit_cast(uint32_t, a.xw[i]) != __builtin_bit_cast(uint32_t, b.xw[i]) ||
+            __builtin_bit_cast(uint32_t, a.yw[i]) != __builtin_bit_cast(uint32_t, b.yw[i]))
+            return false;
+    for (int d = 0; d < 84; d++)
+        if (a.xn[d] != b.xn[d] || a.yn[d] != b.yn[d]) return false;
+    return true;
+}
+
 inline bool area_period_match(const AreaTables& T) {
     for (int d = 0; d < 84; d++) {
         const int q = d % 21, g = d / 21;

@@ -1267,31 +1267,35 @@ int mh_policy_input(const uint8_t* d_obs, void* d_out, int64_t n, int k, void* s
 }
 
 // ---- the allocation-free resize (mh_resize_noalloc)
-// Its filter tables live in `scratch`, a file-scope device array: every GPU the library runs on holds one
-// copy, at its own address, until the process ends. The first call on a device looks up that device's
-// address of the array (hipGetSymbolAddress; the array's name in host code is only a host-side stand-in)
-// and writes the tables there with one kernel on the caller's stream; later calls only read them.
-constexpr size_t MH_SCRATCH_BYTES = 16384;
-static_assert(sizeof(AreaTables) <= MH_SCRATCH_BYTES, "the area tables must fit the scratch array");
-static __device__ __align__(256) uint8_t scratch[MH_SCRATCH_BYTES];
+// Its filter tables live in `scratch`, a file-scope device array statically initialised with the tables the
+// compiler computes (kAreaTables, area_taps's double operations at compile time): every GPU the library runs on
+// holds one copy, loaded with the code object, at its own address, until the process ends. No kernel writes it
+// and every call only reads it, so calls on one GPU never race over it and a first call under stream capture
+// records nothing but the resize. The first call on a device looks up that device's address of the array
+// (hipGetSymbolAddress; the array's name in host code is only a host-side stand-in, not a device address); the
+// first call in the process checks once that the compile-time tables are, bit for bit, the run-time tables that
+// mh_resize copies to the device (area_tables()).
+static_assert(sizeof(AreaTables) == 8736, "the scratch array holds 8,736 B on every GPU");
+static __device__ __align__(256) AreaTables scratch[1] = {kAreaTables};
 constexpr int MH_MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
+static int g_scratch_checked;                          // 0 not yet, 1 the tables match, -1 they differ
 static AreaTables* g_scratch_tables[MH_MAX_DEVICES];   // the device address of `scratch`, per device
 
-__global__ void k_area_tables(AreaTables* T) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) area_tables(T);
-}
-
-static AreaTables* scratch_tables(hipStream_t s) {
+static AreaTables* scratch_tables() {
     int dev = 0;
     if (!ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
     if (dev < 0 || dev >= MH_MAX_DEVICES) { g_err = "device index beyond the allocation-free path's table"; return nullptr; }
     std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_checked) {
+        AreaTables host;
+        area_tables(&host);
+        g_scratch_checked = area_tables_equal(host, kAreaTables) ? 1 : -1;
+    }
+    if (g_scratch_checked < 0) { g_err = "compile-time INTER_AREA tables differ from the run-time ones"; return nullptr; }
     if (!g_scratch_tables[dev]) {
         void* p = nullptr;
         if (!ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return nullptr;
-        hipLaunchKernelGGL(k_area_tables, dim3(1), dim3(64), 0, s, (AreaTables*)p);
-        if (!ok(hipGetLastError(), "k_area_tables launch")) return nullptr;
         g_scratch_tables[dev] = (AreaTables*)p;
     }
     return g_scratch_tables[dev];
@@ -1304,7 +1308,7 @@ int mh_resize_noalloc(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream)
         return -1;
     }
     hipStream_t s = (hipStream_t)stream;
-    AreaTables* T = scratch_tables(s);
+    AreaTables* T = scratch_tables();
     if (!T) return -1;
     hipLaunchKernelGGL(k_resize_images, dim3((OBS_PIX + 255) / 256, n), dim3(256), 0, s, d_src, d_dst, n, (const AreaTables*)T);
     CK(hipGetLastError());

@@ -147,10 +147,11 @@ int mh_resize(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
 /* mh_resize without any device allocation: no counterpart in the reference. For callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same
- * kernel and results as mh_resize; its filter tables (8.7 KB) sit in a 16 KB file-scope device array the
- * library holds on every GPU it runs on until the process ends, written by the first call on a device (one
- * kernel on that call's stream). At most MH_RESIZE_MAX_IMAGES images per call; more is refused (-1).
- * A call on another stream that overlaps the first call on the same GPU races with the tables' set-up. */
+ * kernel and results as mh_resize; its filter tables (8,736 B) sit in a file-scope device array that is
+ * statically initialised with them, which the library holds on every GPU it runs on until the process ends.
+ * No call writes the array, so calls on one GPU, overlapping or not, never race over it, and a first call
+ * made under stream capture enqueues nothing but the resize itself. At most MH_RESIZE_MAX_IMAGES images per
+ * call; more, fewer than 1, or a null buffer is refused (-1). */
 int mh_resize_noalloc(const uint8_t* d_src, uint8_t* d_dst, int n, void* stream);
 
 /* ---- the PPO rollout harness's policy input

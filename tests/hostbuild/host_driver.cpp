@@ -209,6 +209,8 @@ int run_env(const char* cfg_file) {
     area_tables(&v.T);
     // the library creates an env only if the run-time tables are the compiled-in periods that obs_tail uses
     if (!area_period_match(v.T)) die("INTER_AREA tables differ from the compiled-in periods");
+    // and the allocation-free resize takes the whole tables from a device array initialised at compile time
+    if (!area_tables_equal(v.T, kAreaTables)) die("INTER_AREA tables differ from the compile-time tables");
     for (int i = 0; i < n; i++) {
         auto w = [&](int k) -> uint32_t& { return v.ev[(size_t)k * np + i]; };
         w(E_LEVEL) = (uint32_t)env_level[i];
