@@ -358,6 +358,21 @@ def run_replay(args):
     print(json.dumps(out), flush=True)
 
 
+def headline_actions(n, preroll, timed, device="cuda:0"):
+    """The headline workload's actions on the device: `preroll` rows drawn one step at a time from a seed-0
+    torch.Generator (the untimed preroll), then `timed` rows drawn at once from a second seed-0 generator (the
+    warm-up and timed steps), each uniform in {0..6}, int64 (rows, n). The GPU parity test of the headline
+    shape replays exactly this stream."""
+    import torch
+    gen = torch.Generator(device=device)
+    gen.manual_seed(0)
+    pre = [torch.randint(0, 7, (n,), generator=gen, device=device, dtype=torch.int64) for _ in range(preroll)]
+    gen_t = torch.Generator(device=device)
+    gen_t.manual_seed(0)
+    acts = torch.randint(0, 7, (timed, n), generator=gen_t, device=device, dtype=torch.int64)
+    return (torch.stack(pre) if pre else acts[:0]), acts
+
+
 def step_loop(env, args, next_actions, timed_actions):
     """--preroll untimed steps (fresh actions from next_actions()), W warm-up and K timed steps over the rows of
     timed_actions (pre-generated on the device). Returns the measurements of the K timed steps."""
@@ -454,12 +469,9 @@ def run_headline(args):
     env.reset()
     torch.cuda.synchronize()
     log(f"boot + reset cache + reset: {time.perf_counter() - t0:.1f} s")
-    gen = torch.Generator(device="cuda:0")
-    gen.manual_seed(0)
-    pre = lambda: torch.randint(0, 7, (n,), generator=gen, device="cuda:0", dtype=torch.int64)  # noqa: E731
-    gen_t = torch.Generator(device="cuda:0")
-    gen_t.manual_seed(0)
-    acts = torch.randint(0, 7, (args.warmup + args.steps, n), generator=gen_t, device="cuda:0", dtype=torch.int64)
+    pre_rows, acts = headline_actions(n, args.preroll, args.warmup + args.steps)
+    pre_it = iter(pre_rows)
+    pre = lambda: next(pre_it)  # noqa: E731
     if args.probe_copy_mib:
         src = torch.ones(args.probe_copy_mib << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)

@@ -157,8 +157,9 @@ def make_net(n_actions: int = N_ACTIONS, in_ch: int = 4, seed: int = 0, device="
                 h = h.float()
                 return self.pi(h), self.vf(h).squeeze(-1)
             elif obs_u8.is_cuda:
+                # other stack depths, and views that are not contiguous (policy_input takes contiguous stacks)
                 x = self._input(obs_u8.shape, obs_u8.device)
-                policy_input(obs_u8, x)
+                policy_input(obs_u8.contiguous(), x)
             else:
                 x = obs_u8.float().mul_(1.0 / 255.0)
             with torch.autocast("cuda", dtype=torch.bfloat16, enabled=x.is_cuda):

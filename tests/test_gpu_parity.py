@@ -72,8 +72,8 @@ def test_raw_program_fuzz(seed):
 
 
 def test_raw_program_fuzz_two_waves():
-    # 40 consoles: a full 32-env wave and a partial one, so catch-ups that one lane forces on the others of
-    # its wave (PPU register accesses at different points) are compared across many lanes
+    # 40 consoles: two full 16-console waves and a partial one, so catch-ups that one lane forces on the others
+    # of its wave (PPU register accesses at different points) are compared across many lanes
     _raw_run(fuzz.program_rom(3), 40, scaled(40), seed=3, backup_p=0.05)
 
 
@@ -149,7 +149,7 @@ def test_env_rom_modes_per_env():
 
 
 def test_env_vs_oracle_two_waves():
-    # 40 envs (a full 32-env wave and a partial one) with the headline wrappers
+    # 40 envs (two full 16-env waves and a partial one) with the headline wrappers
     names = ["1-1", "4-1", "8-4", "2-3", "1-2", "5-2", "3-3", "7-1"] * 5
     _env_run(names, "headline", scaled(60))
 
@@ -194,7 +194,9 @@ def _env_run(names, config, steps):
     assert gpu.frames == cpu.frames()
     assert gpu.bad_ops() == 0 and cpu.bad_ops() == 0
     assert gpu.instructions() == cpu.instructions()
-    assert 0 <= gpu.ff_instructions() < gpu.instructions()
+    # the sprite-0 poll fast-forward (state-identical, so the counts above cannot show it) must have fired: the
+    # synthetic game polls sprite 0 every frame of a level
+    assert 0 < gpu.ff_instructions() < gpu.instructions()
     re_gpu, re_cpu = gpu.reemulations(), cpu.reemulations()
     assert re_gpu == re_cpu, (re_gpu, re_cpu)
     if steps >= 150:
@@ -244,6 +246,48 @@ def test_hack_frames_redrawn_vs_oracle():
     assert gpu.instructions() == sum(c.instructions() for c in cpu)
     assert gpu.bad_ops() == 0
     assert gpu.hack_redraws() > 0, "no busy run after a drawn frame: the redraw path was not exercised"
+
+
+def test_env_2048_in_kernel_observations():
+    """2,048 envs (128 waves) with the headline wrappers, every env every step against the oracle. k_step's waves
+    take tickets in the order they finish their frame loops; the first 64 compute their envs' observations inside
+    k_step (obs_tail after the frame loop, behind its release / acquire fences) and only the last 64 leave them
+    to k_obs_late. With 64 waves or fewer every wave defers, so the smaller parity tests cover k_obs_late alone.
+    The oracle runs as 16 instances of 128 envs (their own PCG64 streams by env_offset) on a thread pool."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    import torch
+
+    from fast_mario_env_amd import HipVecEnv
+    kw = CONFIGS["headline"]
+    names = ["1-1", "4-1", "8-4", "2-3", "1-2", "5-2", "3-3", "7-1"] * 256
+    n, m = len(names), 128
+    assert n // 16 > 64      # waves of 16 envs beyond the 64 that defer
+    pool = ThreadPoolExecutor(min(16, os.cpu_count() or 1))
+    cpu = list(pool.map(lambda k: OracleVec(MINI, _levels(names[k:k + m]), m, seed=3, env_offset=k, **kw),
+                        range(0, n, m)))
+    gpu = HipVecEnv(names, n, seed=3, rom=MINI, **kw)
+    o1 = np.concatenate(list(pool.map(lambda c: c.reset().copy(), cpu)))
+    assert np.array_equal(o1, gpu.reset().cpu().numpy()), "reset obs"
+    rng = np.random.default_rng(23)
+    for t in range(scaled(60)):
+        a = rng.integers(0, 7, n)
+        outs = list(pool.map(lambda kc: [x.copy() for x in kc[1].step(a[kc[0]:kc[0] + m])], zip(range(0, n, m), cpu)))
+        o1, r1, te1, tr1, i1 = (np.concatenate(z) for z in zip(*outs))
+        o2, r2, te2, tr2, _ = gpu.step(torch.from_numpy(a).cuda())
+        o2, r2, te2, tr2, i2 = (x.cpu().numpy() for x in (o2, r2, te2, tr2, gpu.info_t))
+        assert np.array_equal(r1, r2) and np.array_equal(te1, te2) and np.array_equal(tr1, tr2), (t, "reward/done")
+        assert np.array_equal(i1, i2), (t, "info")
+        bad = np.flatnonzero((o1 != o2).reshape(n, -1).any(1))
+        assert bad.size == 0, (t, "obs of envs", bad[:8].tolist())
+    pool.shutdown()
+    ram = gpu.ram().cpu().numpy()
+    for i in range(n):
+        assert np.array_equal(cpu[i // m].ram(i % m), ram[i]), (i, "ram")
+    assert gpu.frames == sum(c.frames() for c in cpu)
+    assert gpu.instructions() == sum(c.instructions() for c in cpu)
+    assert gpu.bad_ops() == 0
 
 
 def test_config1_golden_trace_on_gpu():

@@ -149,15 +149,18 @@ def test_policy_input_kernel_matches_torch_scaling(k, n):
 
 
 @pytest.mark.gpu
-def test_policy_forward_as_accurate_as_plain_bf16():
+@pytest.mark.parametrize("n", [96, 4096])
+def test_policy_forward_as_accurate_as_plain_bf16(n):
     # the GPU forward (the fused first layer, then channels-last bf16 convolutions) against the float32 network:
     # its error must be of the size of plain PyTorch's own bf16 forward (float32 scaling, NCHW, autocast), the two
-    # bf16 pipelines rounding at different points; with autograd on it takes torch layers throughout
+    # bf16 pipelines rounding at different points; with autograd on it takes torch layers throughout. At 4,096
+    # samples every convolution kernel's waves walk several tiles each (their launches are capped at 8 blocks
+    # per CU), the shape of the rollout workload
     import torch.nn.functional as F
 
     from fast_mario_env_amd.rollout import make_net
     net = make_net(seed=1)
-    obs = torch.randint(0, 256, (96, 4, 84, 84), dtype=torch.uint8, device="cuda",
+    obs = torch.randint(0, 256, (n, 4, 84, 84), dtype=torch.uint8, device="cuda",
                         generator=torch.Generator(device="cuda").manual_seed(5))
 
     def plain(bf16):
@@ -180,6 +183,9 @@ def test_policy_forward_as_accurate_as_plain_bf16():
         assert torch.allclose(got, ref, rtol=5e-2, atol=1e-2)
     # (the library's layers may pick other kernels, with other summation orders, for another batch size)
     assert torch.allclose(logits[:64], logits2, rtol=2e-2, atol=2e-3)
+    with torch.no_grad():
+        logits4, _ = net(obs[::2])               # a view that is not contiguous: the scaling kernel + torch layers
+    assert torch.allclose(logits[::2], logits4, rtol=2e-2, atol=2e-3)
     logits3, value3 = net(obs)
     assert logits3.requires_grad
     for got, ref, bf in ((logits3.detach(), ref_logits, bf_logits), (value3.detach(), ref_value, bf_value)):
@@ -187,11 +193,12 @@ def test_policy_forward_as_accurate_as_plain_bf16():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [1, 3, 50])
+@pytest.mark.parametrize("n", [1, 3, 50, 4096])
 def test_policy_conv1_kernel_matches_torch(n):
     # the fused MFMA first layer against torch's: bf16 input (mh_policy_input), bf16 convolution with its bias
     # under autocast, ReLU. Both accumulate in float32 in different orders and torch rounds the convolution to
-    # bf16 before adding the bias, so they agree to a bf16 rounding or two
+    # bf16 before adding the bias, so they agree to a bf16 rounding or two. At 4,096 samples (1.6M output pixels,
+    # 51,200 tiles of 32) each wave of the persistent kernel walks several tiles, with the next tile's prefetch
     import torch.nn.functional as F
 
     from fast_mario_env_amd.rollout import make_net, policy_conv1, policy_input
@@ -216,9 +223,10 @@ def test_policy_conv1_kernel_matches_torch(n):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("layer,n", [(2, 1), (2, 37), (3, 1), (3, 37)])
+@pytest.mark.parametrize("layer,n", [(2, 1), (2, 37), (2, 4096), (3, 1), (3, 37), (3, 4096)])
 def test_policy_conv_kernels_match_torch(layer, n):
-    # the fused MFMA second and third layers against torch's bf16 convolutions with bias under autocast and ReLU
+    # the fused MFMA second and third layers against torch's bf16 convolutions with bias under autocast and ReLU;
+    # at 4,096 samples each wave of the persistent kernels walks several tiles, with the next tile's prefetch
     import torch.nn.functional as F
 
     from fast_mario_env_amd.rollout import make_net, policy_conv
