@@ -216,6 +216,218 @@ __device__ __constant__ static const dec::Table kDecode{};
 #define MH_SCALAR_CONST __attribute__((address_space(4)))
 #endif
 
+// ---------------------------------------------------------------- long lone runs
+// A console that is the only one of its wave with instructions to run (Console::lone_run()) runs them in
+// lone_long(): out of line, in registers of its own (not the frame loop's), wave-uniform, with one body per
+// opcode whose decode word is known at compile time, so that the addressing, the operation, its flags and its
+// control flow fold to the few scalar instructions the opcode needs. Measured on one console running a loop of
+// register instructions: 0.33 us per instruction, against 0.67 us for a body that takes the decode word's
+// fields at run time (inline, as a switch per field).
+// The registers of a lone run, wave-uniform: pc, a, x, y, sp, p, exec_at (ex) and zero_skip (zs).
+struct LoneRegs { uint32_t pc, a, x, y, sp, p; int32_t ex; uint32_t zs, n; };   // n: instructions run (output)
+struct LoneCore {
+    LoneRegs r;
+    uint8_t* mem;                              // the console's RAM row 0 (row stride np), the same in every active lane
+    uint32_t np;
+    const MH_SCALAR_CONST uint32_t* gprg;      // PRG image (read only): scalar loads
+    __device__ __forceinline__ uint32_t ram(uint32_t ad) const {
+        return __builtin_amdgcn_readfirstlane(mem[(size_t)((ad & 0x7ffu) * np)]);
+    }
+    __device__ __forceinline__ void set_ram(uint32_t ad, uint32_t v) { mem[(size_t)((ad & 0x7ffu) * np)] = (uint8_t)v; }
+    __device__ __forceinline__ uint32_t prg(uint32_t ad) const {
+        ad &= 0x7fffu;
+        return (gprg[ad >> 2] >> (8u * (ad & 3u))) & 0xffu;
+    }
+    // the bus reads and writes a lone run may make: RAM, PRG, and $4000-$7FFF but the joypads (reads) or OAM
+    // DMA and the joypad strobe (writes), which read 0 and ignore writes; anything else (the PPU registers above
+    // all) is left to frame()
+    __device__ __forceinline__ static bool reads_ok(uint32_t ad) { return (ad - 0x2000u) >= 0x2000u && (ad | 1u) != 0x4017u; }
+    __device__ __forceinline__ static bool writes_ok(uint32_t ad) { return (ad - 0x2000u) >= 0x2000u && (ad & ~2u) != 0x4014u; }
+    __device__ __forceinline__ uint32_t read(uint32_t ad) const { return ad < 0x2000u ? ram(ad) : ad >= 0x8000u ? prg(ad) : 0u; }
+};
+
+// One instruction of opcode OP (operand bytes b1, b2) on a lone console; false, with no effect, if it needs
+// frame() (an invalid opcode, a bus access lone runs do not make). instruction()'s rules and the reference's
+// results (nes_core.hpp:619-1163), with every choice on the decode word resolved at compile time.
+template <uint32_t OP>
+__device__ __forceinline__ bool lone_op(LoneCore& c, uint32_t b1, uint32_t b2) {
+    using namespace dec;
+    constexpr uint32_t D = entry((int)OP);
+    constexpr uint32_t am = D & 15u, alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, dst = (D >> DST_SH) & 7u;
+    constexpr uint32_t xop = (D >> X_SH) & 15u, fl = (D >> FL_SH) & 7u, fop = (D >> FOP_SH) & 7u;
+    constexpr bool rd = (D & RD) != 0, wr = dst == D_MEM, pen = (D & PEN) != 0;
+    constexpr bool zpm = am == M_ZP || am == M_ZPX || am == M_ZPY;   // zero-page modes touch RAM only
+    if constexpr (!(D & OK)) {
+        return false;
+    } else {
+        LoneRegs& r = c.r;
+        const uint32_t absv = b1 | b2 << 8;
+        const uint32_t p2 = (absv & 0xff00u) | ((absv + 1u) & 0xffu);   // JMP (ind): high byte, page wrap
+        uint32_t ea = 0, base = absv;
+        int32_t sk = 0;
+        if constexpr (am == M_IMM) ea = (r.pc + 1u) & 0xffffu;
+        if constexpr (am == M_ZP) ea = b1;
+        if constexpr (am == M_ZPX) ea = (b1 + r.x) & 0xffu;
+        if constexpr (am == M_ZPY) ea = (b1 + r.y) & 0xffu;
+        if constexpr (am == M_ABS) ea = absv;
+        if constexpr (am == M_ABSX) ea = (absv + r.x) & 0xffffu;
+        if constexpr (am == M_ABSY) ea = (absv + r.y) & 0xffffu;
+        if constexpr (am == M_INDX) { const uint32_t z = (b1 + r.x) & 0xffu; ea = c.ram(z) | c.ram((z + 1u) & 0xffu) << 8; }
+        if constexpr (am == M_INDY) { base = c.ram(b1) | c.ram((b1 + 1u) & 0xffu) << 8; ea = (base + r.y) & 0xffffu; }
+        if constexpr (xop == X_JMPI) {
+            if (!LoneCore::reads_ok(absv) || !LoneCore::reads_ok(p2)) return false;
+        } else {
+            if constexpr (rd && am != M_IMM && !zpm) if (!LoneCore::reads_ok(ea)) return false;
+            if constexpr (wr && !zpm) if (!LoneCore::writes_ok(ea)) return false;
+        }
+        if constexpr (pen && (am == M_ABSX || am == M_ABSY || am == M_INDY)) sk = ((base ^ ea) & 0xff00u) ? 1 : 0;
+        uint32_t m = b1;
+        if constexpr (rd && am != M_IMM) m = zpm ? c.ram(ea) : c.read(ea);
+        // the operation (alu_op()'s results): result, carry out, overflow
+        const uint32_t rv = src == R_A ? r.a : src == R_X ? r.x : src == R_Y ? r.y : src == R_SP ? r.sp : m;
+        const uint32_t sv = rd ? m : rv, cin = (r.p >> 7) & 1u;   // FC is bit 7
+        uint32_t res = sv, c_out = 0, v_out = 0;
+        if constexpr (alu == OP_ORA) res = r.a | m;
+        if constexpr (alu == OP_AND) res = r.a & m;
+        if constexpr (alu == OP_EOR) res = r.a ^ m;
+        if constexpr (alu == OP_ADC || alu == OP_SBC || alu == OP_CMP) {
+            const uint32_t ax = alu == OP_CMP ? rv : r.a, m2 = alu == OP_ADC ? m : m ^ 0xffu;
+            const uint32_t t = ax + m2 + (alu == OP_CMP ? 1u : cin);
+            res = t & 0xffu; c_out = t >> 8; v_out = (ax ^ t) & (m2 ^ t) & 0x80u;
+        }
+        if constexpr (alu == OP_ASL) { res = (sv << 1) & 0xffu; c_out = sv >> 7; }
+        if constexpr (alu == OP_ROL) { res = ((sv << 1) | cin) & 0xffu; c_out = sv >> 7; }
+        if constexpr (alu == OP_LSR) { res = sv >> 1; c_out = sv & 1u; }
+        if constexpr (alu == OP_ROR) { res = (sv >> 1) | cin << 7; c_out = sv & 1u; }
+        if constexpr (alu == OP_INC) res = (sv + 1u) & 0xffu;
+        if constexpr (alu == OP_DEC) res = (sv - 1u) & 0xffu;
+        const uint32_t nz = (res ? 0u : (uint32_t)FZ) | (res >> 7);   // FN is bit 0
+        if constexpr (fl == FL_NZ) r.p = (r.p & ~(uint32_t)(FZ | FN)) | nz;
+        if constexpr (fl == FL_NZC) r.p = (r.p & ~(uint32_t)(FZ | FN | FC)) | nz | (c_out ? (uint32_t)FC : 0u);
+        if constexpr (fl == FL_NZCV)
+            r.p = (r.p & ~(uint32_t)(FZ | FN | FC | FV)) | nz | (c_out ? (uint32_t)FC : 0u) | (v_out ? (uint32_t)FV : 0u);
+        if constexpr (fl == FL_BIT)
+            r.p = (r.p & ~(uint32_t)(FZ | FV | FN)) | ((r.a & m) ? 0u : (uint32_t)FZ) | ((m & 0x40u) ? (uint32_t)FV : 0u) | (m >> 7);
+        if constexpr (fl == FL_OP) {   // CLC SEC CLI SEI CLV CLD SED
+            constexpr uint32_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;
+            constexpr uint32_t fset = (fop == 1 || fop == 3 || fop == 6) ? fm : 0u;
+            r.p = (r.p & ~fm) | fset;
+        }
+        if constexpr (dst == D_A) r.a = res;
+        if constexpr (dst == D_X) r.x = res;
+        if constexpr (dst == D_Y) r.y = res;
+        if constexpr (dst == D_SP) r.sp = res;
+        if constexpr (wr) { if (zpm || ea < 0x2000u) c.set_ram(ea, res); }   // writes elsewhere are ignored
+        // control flow
+        const uint32_t ret = (r.pc + 2u) & 0xffffu;
+        uint32_t npc = (r.pc + (am == M_NONE ? 1u : (am == M_ABS || am == M_ABSX || am == M_ABSY) ? 3u : 2u)) & 0xffffu;
+        if constexpr (xop == X_BRANCH) {   // on N, V, C, Z (op bits 6-7) equal to op bit 5
+            constexpr uint32_t fbit = (0x40800201u >> (8 * (OP >> 6))) & 0xffu;   // FN FV FC FZ
+            if (((r.p & fbit) != 0) == ((OP & 0x20u) != 0)) {
+                npc = (ret + (uint32_t)(int32_t)(int8_t)b1) & 0xffffu;
+                sk += ((ret ^ npc) & 0xff00u) ? 3 : 1;
+            } else {
+                npc = ret;
+            }
+        }
+        if constexpr (xop == X_JMP) npc = absv;
+        if constexpr (xop == X_JMPI) npc = c.read(absv) | c.read(p2) << 8;
+        if constexpr (xop == X_JSR) {
+            c.set_ram(0x100u | r.sp, ret >> 8);
+            c.set_ram(0x100u | ((r.sp - 1u) & 0xffu), ret & 0xffu);
+            r.sp = (r.sp - 2u) & 0xffu;
+            npc = absv;
+        }
+        if constexpr (xop == X_BRK) {
+            c.set_ram(0x100u | r.sp, ret >> 8);
+            c.set_ram(0x100u | ((r.sp - 1u) & 0xffu), ret & 0xffu);
+            c.set_ram(0x100u | ((r.sp - 2u) & 0xffu), r.p | 0x30u);
+            r.sp = (r.sp - 3u) & 0xffu;
+            r.p |= FI;
+            npc = c.prg(0xfffe) | c.prg(0xffff) << 8;
+            sk += 7;
+        }
+        if constexpr (xop == X_PHA || xop == X_PHP) {
+            c.set_ram(0x100u | r.sp, xop == X_PHA ? r.a : r.p);
+            r.sp = (r.sp - 1u) & 0xffu;
+        }
+        if constexpr (xop == X_PLA || xop == X_PLP) {
+            const uint32_t u = c.ram(0x100u | ((r.sp + 1u) & 0xffu));
+            r.sp = (r.sp + 1u) & 0xffu;
+            if constexpr (xop == X_PLA) { r.a = u; r.p = (r.p & ~(uint32_t)(FZ | FN)) | (u ? 0u : (uint32_t)FZ) | (u >> 7); }
+            else r.p = u;
+        }
+        if constexpr (xop == X_RTS) {
+            const uint32_t lo = c.ram(0x100u | ((r.sp + 1u) & 0xffu)), hi = c.ram(0x100u | ((r.sp + 2u) & 0xffu));
+            r.sp = (r.sp + 2u) & 0xffu;
+            npc = ((lo | hi << 8) + 1u) & 0xffffu;
+        }
+        if constexpr (xop == X_RTI) {
+            const uint32_t f = c.ram(0x100u | ((r.sp + 1u) & 0xffu)), lo = c.ram(0x100u | ((r.sp + 2u) & 0xffu)),
+                           hi = c.ram(0x100u | ((r.sp + 3u) & 0xffu));
+            r.sp = (r.sp + 3u) & 0xffu;
+            r.p = f; npc = lo | hi << 8;
+        }
+        r.pc = npc;
+        sk += (int32_t)((D >> CYC_SH) & 7u);
+        r.ex += sk >= 1 ? sk : 1;
+        r.zs = sk <= 0 ? 1u : 0u;   // opcodes the cycle table gives 0 cycles (and no penalty)
+        return true;
+    }
+}
+
+// A wave-uniform 64-bit value (a pointer): the builtin returns a signed int, so each half is taken as unsigned
+// before it is widened (else the low half's bit 31 would spread into the high half).
+__device__ __forceinline__ uint64_t lone_uniform64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (uint64_t)lo | (uint64_t)hi << 32;
+}
+
+// Runs lone instructions from r until one needs frame(): its catch-up point 3 (ex + 1) past lim, its opcode or
+// operands outside PRG, the idle `JMP *`, or what lone_op() refuses. Returns the registers after the last one
+// run and, in n, how many ran. Not inlined: its registers are its own, not the frame loop's.
+__device__ __attribute__((noinline)) LoneRegs lone_long(LoneRegs in, int32_t lim, uint8_t* mem, uint32_t np,
+                                                        const uint8_t* gprg) {
+    LoneCore c;
+    c.r.pc = __builtin_amdgcn_readfirstlane(in.pc); c.r.a = __builtin_amdgcn_readfirstlane(in.a);
+    c.r.x = __builtin_amdgcn_readfirstlane(in.x); c.r.y = __builtin_amdgcn_readfirstlane(in.y);
+    c.r.sp = __builtin_amdgcn_readfirstlane(in.sp); c.r.p = __builtin_amdgcn_readfirstlane(in.p);
+    c.r.ex = (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)in.ex);
+    c.r.zs = __builtin_amdgcn_readfirstlane(in.zs);
+    lim = (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)lim);
+    c.mem = (uint8_t*)lone_uniform64((uint64_t)mem);
+    c.np = __builtin_amdgcn_readfirstlane(np);
+    c.gprg = (const MH_SCALAR_CONST uint32_t*)(const void*)lone_uniform64((uint64_t)gprg);
+    uint32_t n = 0;
+    for (;;) {
+        if (3 * c.r.ex + 3 > lim) break;                   // parks or catches up in frame()
+        if (c.r.pc - 0x8000u > 0x7ffdu) break;             // opcode or operands through the bus
+        const uint32_t pa = c.r.pc & 0x7fffu;
+        const uint64_t w = (uint64_t)c.gprg[(pa >> 2) + 1] << 32 | c.gprg[pa >> 2];
+        const uint32_t b0 = (uint32_t)(w >> (8 * (pa & 3u)));   // bytes pc .. pc + 3
+        const uint32_t op = b0 & 0xffu, b1 = (b0 >> 8) & 0xffu, b2 = (b0 >> 16) & 0xffu;
+        if (op == 0x4cu && (b1 | b2 << 8) == c.r.pc) break;  // JMP *: frame()'s idle fast-forward
+        bool ran = false;
+        switch (op) {
+#define MH_LONE_CASE(i) case i: ran = lone_op<i>(c, b1, b2); break;
+#define MH_LONE_CASE4(i) MH_LONE_CASE(i) MH_LONE_CASE(i + 1) MH_LONE_CASE(i + 2) MH_LONE_CASE(i + 3)
+#define MH_LONE_CASE16(i) MH_LONE_CASE4(i) MH_LONE_CASE4(i + 4) MH_LONE_CASE4(i + 8) MH_LONE_CASE4(i + 12)
+#define MH_LONE_CASE64(i) MH_LONE_CASE16(i) MH_LONE_CASE16(i + 16) MH_LONE_CASE16(i + 32) MH_LONE_CASE16(i + 48)
+            MH_LONE_CASE64(0) MH_LONE_CASE64(64) MH_LONE_CASE64(128) MH_LONE_CASE64(192)
+#undef MH_LONE_CASE64
+#undef MH_LONE_CASE16
+#undef MH_LONE_CASE4
+#undef MH_LONE_CASE
+            default: break;
+        }
+        if (!ran) break;
+        n++;
+    }
+    c.r.n = n;
+    return c.r;
+}
+
 struct Cart {
     const uint8_t* prg;      // 0x8000 bytes (16 KB images mirrored)
     const uint8_t* gprg;     // the same PRG image in device memory (scalar loads of wave-uniform addresses)
@@ -1196,196 +1408,34 @@ struct Console {
     // While a console is the only one of its wave with an instruction to run (the others parked at their slice
     // end, or out of the frame loop), an iteration of frame()'s loop costs about what it costs a full wave: every
     // opcode's work as selects, the wave votes and the catch-up checks. lone_run() runs that console's
-    // instructions back to back instead, with its registers and decode word wave-uniform, so that the compiler
-    // branches over the work an opcode does not need. It runs the instructions whose opcode and operands are in
-    // PRG and whose bus accesses touch only RAM, PRG, or addresses that read as 0 or ignore writes ($4000-$7FFF
-    // but the joypads and OAM DMA), as instruction() would; it stops before any other instruction (PPU register,
-    // joypad or DMA access, invalid opcode), before the idle loop `JMP *` (fast-forwarded by frame()), before an
-    // instruction at the NMI check, and at the slice or frame end, leaving that instruction to frame()'s own
-    // iteration. Returns the number of instructions run. Called by this console's lanes only (its parts, with
-    // identical values), while no lane of the wave waits for a catch-up.
+    // instructions back to back instead, in lone_long(), with its registers wave-uniform and one body per opcode.
+    // It runs the instructions whose opcode and operands are in PRG and whose bus accesses touch only RAM, PRG,
+    // or addresses that read as 0 or ignore writes ($4000-$7FFF but the joypads and OAM DMA), as instruction()
+    // would; it stops before any other instruction (PPU register, joypad or DMA access, invalid opcode), before
+    // the idle loop `JMP *` (fast-forwarded by frame()), before an instruction at the NMI check, and at the
+    // slice or frame end, leaving that instruction to frame()'s own iteration. Returns the number of instructions
+    // run. Called by this console's lanes only (its parts, with identical values), while no lane of the wave
+    // waits for a catch-up.
     __device__ __forceinline__ static uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
-    __device__ __forceinline__ static bool lone_reads(uint32_t ad) {
-        return ad < 0x2000u || ad >= 0x8000u || (ad >= 0x4000u && ad != 0x4016u && ad != 0x4017u);
-    }
-    __device__ __forceinline__ static bool lone_writes(uint32_t ad) {
-        return ad < 0x2000u || (ad >= 0x4000u && ad != 0x4014u && ad != 0x4016u);
-    }
-    // read() for the addresses lone_reads() admits
-    __device__ __forceinline__ uint32_t lone_read(uint32_t ad) const {
-        if (ad < 0x2000u) return uniform(ram(ad));
-        if (ad >= 0x8000u) return uniform(prg((uint16_t)ad));
-        return 0u;
-    }
     __device__ __forceinline__ uint32_t lone_run(int32_t end, int32_t slice) {
-        using namespace dec;
-        uint32_t upc = uniform(pc), ua = uniform(a), ux = uniform(x), uy = uniform(y), us = uniform(sp), up = uniform(p);
-        int32_t ex = (int32_t)uniform((uint32_t)exec_at);
+        // frame()'s stopping rules as one limit on the catch-up point 3 (j + 1) of instruction j: at most the slice
+        // end, at most 3 end (j < end), and no NMI check that needs a catch-up first (below nmi_thresh, or
+        // already caught up to it)
         const int32_t calls = (int32_t)uniform((uint32_t)ppu_calls), nmi = (int32_t)uniform((uint32_t)nmi_thresh);
         const int32_t last = (int32_t)uniform((uint32_t)slice);
-        uint32_t n = 0, zs = 0;
-        for (;;) {
-            const int32_t j = ex, tgt = 3 * (j + 1);
-            if (j >= end || tgt > last) break;                  // parks in frame()
-            if (tgt >= nmi && calls < tgt) break;               // frame() catches up first
-            if (upc < 0x8000u || upc > 0xfffdu) break;          // opcode or operands through the bus
-            const uint32_t pa = upc & 0x7fffu;
-            // opcode, operands and decode word by scalar loads (a wave-uniform address; no LDS round trip)
-            const MH_SCALAR_CONST uint32_t* pw = (const MH_SCALAR_CONST uint32_t*)(const void*)cart.gprg + (pa >> 2);
-            const uint64_t w = (uint64_t)pw[1] << 32 | pw[0];
-            const uint32_t b0 = (uint32_t)(w >> (8 * (pa & 3u)));                // bytes pc .. pc + 3
-            const uint32_t op = b0 & 0xffu, b1 = (b0 >> 8) & 0xffu, b2 = (b0 >> 16) & 0xffu, absv = b1 | b2 << 8;
-            if (op == 0x4cu && absv == upc) break;               // JMP *: frame()'s idle fast-forward
-            const uint32_t D = kDecode.w[op];
-            if (!(D & OK)) break;                               // invalid opcode: frame() counts it
-            const uint32_t am = D & 15u, alu = (D >> ALU_SH) & 15u, src = (D >> SRC_SH) & 7u, dst = (D >> DST_SH) & 7u;
-            const uint32_t xop = (D >> X_SH) & 15u, fl = (D >> FL_SH) & 7u;
-            const bool rd = (D & RD) != 0;
-            // addressing (instruction()'s rules): effective address, page-cross penalty, instruction length
-            uint32_t ea = 0, len = 2;
-            int32_t sk = 0;
-            switch (am) {
-                case M_NONE: len = 1; break;
-                case M_IMM: ea = (upc + 1u) & 0xffffu; break;
-                case M_ZP: ea = b1; break;
-                case M_ZPX: ea = (b1 + ux) & 0xffu; break;
-                case M_ZPY: ea = (b1 + uy) & 0xffu; break;
-                case M_ABS: ea = absv; len = 3; break;
-                case M_ABSX: case M_ABSY: {
-                    const uint32_t i = am == M_ABSX ? ux : uy;
-                    ea = (absv + i) & 0xffffu; len = 3;
-                    if ((D & PEN) && ((absv ^ (absv + i)) & 0xff00u)) sk = 1;
-                    break;
-                }
-                case M_INDX: {
-                    const uint32_t z = (b1 + ux) & 0xffu;
-                    ea = lone_read(z) | lone_read((z + 1u) & 0xffu) << 8;
-                    break;
-                }
-                default: {   // M_INDY
-                    const uint32_t base = lone_read(b1) | lone_read((b1 + 1u) & 0xffu) << 8;
-                    ea = (base + uy) & 0xffffu;
-                    if ((D & PEN) && ((base ^ (base + uy)) & 0xff00u)) sk = 1;
-                    break;
-                }
-            }
-            const uint32_t p2 = (absv & 0xff00u) | ((absv + 1u) & 0xffu);   // JMP (ind): high byte, page wrap
-            const bool wr = dst == D_MEM;
-            if (xop == X_JMPI ? !(lone_reads(absv) && lone_reads(p2))
-                              : ((rd && am != M_IMM && !lone_reads(ea)) || (wr && !lone_writes(ea)))) break;
-            const uint32_t m = rd && am != M_IMM ? lone_read(ea) : b1;
-            // the data operation (alu_op()'s results, by cases): result, carry out and overflow
-            const uint32_t rv = src == R_M ? m : src == R_A ? ua : src == R_X ? ux : src == R_Y ? uy : us;
-            const uint32_t sv = rd ? m : rv, cin = up & FC ? 1u : 0u;
-            uint32_t r = sv, c = 0, v = 0;
-            switch (alu) {
-                case OP_ORA: r = ua | m; break;
-                case OP_AND: r = ua & m; break;
-                case OP_EOR: r = ua ^ m; break;
-                case OP_ADC: { const uint32_t t = ua + m + cin; r = t & 0xffu; c = (t >> 8) & 1u; v = (ua ^ t) & (m ^ t) & 0x80u; break; }
-                case OP_SBC: { const uint32_t t = ua - m - (1u - cin); r = t & 0xffu; c = ((t >> 8) & 1u) ^ 1u; v = (ua ^ t) & (~m ^ t) & 0x80u; break; }
-                case OP_CMP: { const uint32_t t = rv - m; r = t & 0xffu; c = ((t >> 8) & 1u) ^ 1u; break; }
-                case OP_ASL: r = (sv << 1) & 0xffu; c = (sv >> 7) & 1u; break;
-                case OP_ROL: r = ((sv << 1) | cin) & 0xffu; c = (sv >> 7) & 1u; break;
-                case OP_LSR: r = sv >> 1; c = sv & 1u; break;
-                case OP_ROR: r = (sv >> 1) | cin << 7; c = sv & 1u; break;
-                case OP_INC: r = (sv + 1u) & 0xffu; break;
-                case OP_DEC: r = (sv - 1u) & 0xffu; break;
-                default: break;   // PASS, BIT, FLAG, NOP: the operand
-            }
-            const uint32_t nz = (r ? 0u : FZ) | (r >> 7);          // FN is bit 0
-            switch (fl) {
-                case FL_NZ: up = (up & ~(uint32_t)(FZ | FN)) | nz; break;
-                case FL_NZC: up = (up & ~(uint32_t)(FZ | FN | FC)) | nz | (c ? FC : 0u); break;
-                case FL_NZCV: up = (up & ~(uint32_t)(FZ | FN | FC | FV)) | nz | (c ? FC : 0u) | (v ? FV : 0u); break;
-                case FL_BIT: up = (up & ~(uint32_t)(FZ | FV | FN)) | ((ua & m) ? 0u : FZ) | (m & 0x40u ? FV : 0u) | (m >> 7); break;
-                case FL_OP: {   // CLC SEC CLI SEI CLV CLD SED
-                    const uint32_t fop = (D >> FOP_SH) & 7u;
-                    const uint32_t fm = fop < 2 ? FC : fop < 4 ? FI : fop == 4 ? FV : FD;
-                    up = (up & ~fm) | ((fop == 1 || fop == 3 || fop == 6) ? fm : 0u);
-                    break;
-                }
-                default: break;
-            }
-            switch (dst) {
-                case D_A: ua = r; break;
-                case D_X: ux = r; break;
-                case D_Y: uy = r; break;
-                case D_SP: us = r; break;
-                case D_MEM: if (ea < 0x2000u) st(ROW_RAM + (ea & 0x7ffu), (uint8_t)r); break;   // else ignored
-                default: break;
-            }
-            uint32_t npc = (upc + len) & 0xffffu;
-            const uint32_t ret = (upc + 2u) & 0xffffu;
-            switch (xop) {
-                case X_NONE: break;
-                case X_BRANCH: {   // on N, V, C, Z (op bits 6-7) equal to op bit 5
-                    const uint32_t fbit = (0x40800201u >> (8 * (op >> 6))) & 0xffu;   // FN FV FC FZ
-                    if (((up & fbit) != 0) == ((op & 0x20u) != 0)) {
-                        npc = (ret + (uint32_t)(int32_t)(int8_t)b1) & 0xffffu;
-                        sk += ((ret ^ npc) & 0xff00u) ? 3 : 1;
-                    } else {
-                        npc = ret;
-                    }
-                    break;
-                }
-                case X_JMP: npc = absv; break;
-                case X_JMPI: npc = lone_read(absv) | lone_read(p2) << 8; break;
-                case X_JSR:
-                    st(ROW_RAM + (0x100u | us), (uint8_t)(ret >> 8));
-                    st(ROW_RAM + (0x100u | ((us - 1u) & 0xffu)), (uint8_t)ret);
-                    us = (us - 2u) & 0xffu;
-                    npc = absv;
-                    break;
-                case X_BRK:
-                    st(ROW_RAM + (0x100u | us), (uint8_t)(ret >> 8));
-                    st(ROW_RAM + (0x100u | ((us - 1u) & 0xffu)), (uint8_t)ret);
-                    st(ROW_RAM + (0x100u | ((us - 2u) & 0xffu)), (uint8_t)(up | 0x30u));
-                    us = (us - 3u) & 0xffu;
-                    up |= FI;
-                    npc = uniform(prg(0xfffe)) | uniform(prg(0xffff)) << 8;
-                    sk += 7;
-                    break;
-                case X_PHA: case X_PHP:
-                    st(ROW_RAM + (0x100u | us), (uint8_t)(xop == X_PHA ? ua : up));
-                    us = (us - 1u) & 0xffu;
-                    break;
-                case X_RTS: {
-                    const uint32_t lo = lone_read(0x100u | ((us + 1u) & 0xffu)), hi = lone_read(0x100u | ((us + 2u) & 0xffu));
-                    us = (us + 2u) & 0xffu;
-                    npc = ((lo | hi << 8) + 1u) & 0xffffu;
-                    break;
-                }
-                case X_RTI: {
-                    const uint32_t f = lone_read(0x100u | ((us + 1u) & 0xffu)), lo = lone_read(0x100u | ((us + 2u) & 0xffu)),
-                                   hi = lone_read(0x100u | ((us + 3u) & 0xffu));
-                    us = (us + 3u) & 0xffu;
-                    up = f; npc = lo | hi << 8;
-                    break;
-                }
-                default: {   // PLA, PLP
-                    const uint32_t u = lone_read(0x100u | ((us + 1u) & 0xffu));
-                    us = (us + 1u) & 0xffu;
-                    if (xop == X_PLA) { ua = u; up = (up & ~(uint32_t)(FZ | FN)) | (u ? 0u : FZ) | (u >> 7); }
-                    else up = u;
-                    break;
-                }
-            }
-            upc = npc;
-            sk += (int32_t)((D >> CYC_SH) & 7u);
-            ex = j + (sk >= 1 ? sk : 1);
-            zs = sk <= 0;   // opcodes the cycle table gives 0 cycles (and no penalty)
-            n++;
+        int32_t lim = nmi - 1 > calls ? nmi - 1 : calls;
+        lim = lim < last ? lim : last;
+        lim = lim < 3 * end ? lim : 3 * end;
+        const LoneRegs o = lone_long(LoneRegs{pc, a, x, y, sp, p, exec_at, zero_skip, 0u}, lim, mem, np, cart.gprg);
+        if (o.n) {
+            pc = (uint16_t)o.pc;
+            a = o.a; x = o.x; y = o.y; sp = o.sp;
+            p = (uint8_t)o.p;
+            exec_at = o.ex;
+            zero_skip = o.zs;
+            instructions += o.n;
         }
-        if (n) {
-            pc = (uint16_t)upc;
-            a = ua; x = ux; y = uy; sp = us;
-            p = (uint8_t)up;
-            exec_at = ex;
-            zero_skip = zs;
-            instructions += n;
-        }
-        return n;
+        return o.n;
     }
 
     // PPU calls from the current PPU position to (line, dot) on the frame timeline of
