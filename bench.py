@@ -81,28 +81,50 @@ def profile_values(name, workload_key):
     return vals if wl == workload_key else {}
 
 
-def traffic_from_profiles(workload_key):
-    """HBM bytes per k_step launch from the committed rocprofv3 --pmc summary, if one exists for this workload."""
+def traffic_from_profiles(profile, workload_key):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if one exists for this workload."""
     try:
-        return float(profile_values("k_step_pmc_traffic.md", workload_key)["hbm_bytes_per_launch"])
+        return float(profile_values(profile, workload_key)["hbm_bytes_per_launch"])
     except (KeyError, ValueError):
         return None
 
 
-def valu_roofline(workload_key):
-    """k_step's VALU-issue roofline from the committed rocprofv3 SQ-counter summary of this workload: the
-    binding one for an interpreter (HBM is ~0.01 of peak). Counters cannot be read inside this run; the
-    summary names the command, the steady-state window it measured and the kernel build it measured."""
-    v = profile_values("k_step_sq_counters_headline.md", workload_key)
+# Peak wave64 VALU issue of the chip: 256 CUs x 4 SIMDs, one wave64 VALU instruction per SIMD every 4 cycles
+# (16 lanes wide), at the 2.4 GHz peak engine clock: 614.4 G wave-instructions/s.
+VALU_PEAK_G = 1024 * 2.4 / 4
+
+
+def valu_profile(profile, workload_key):
+    """The committed rocprofv3 SQ-counter summary of a kernel on this workload (profiles/<profile>): VALU
+    instructions per launch, its counter-based issue fraction, the window and the kernel build it measured.
+    Counters cannot be read inside this run; the summary names its command."""
+    v = profile_values(profile, workload_key)
     try:
+        valu = float(v["valu_per_launch"])
         frac = float(v["valu_issue_fraction"])
     except (KeyError, ValueError):
         return None
-    out = {"bound": "valu_issue", "kernel": "k_step", "frac": frac,
-           "unit": "VALU wave-instructions x 4 cycles / (1024 SIMDs x cycles)",
-           "source": "profiles/k_step_sq_counters_headline.md"}
-    for k in ("window", "active_lane_fraction", "occupancy_waves_per_simd", "lds_bank_conflict_per_lds_instr",
-              "kernel_source_sha1"):
+    v["_valu"], v["_frac"] = valu, frac
+    return v
+
+
+def valu_roofline(kernel, profile, workload_key, kernel_ms, executed_per_launch, traffic, hbm):
+    """The binding roofline of an interpreter kernel: VALU issue. achieved = the VALU wave-instructions of one
+    launch (the committed SQ profile of this workload, same window) / this run's average launch time from HIP
+    events on the launch stream, against VALU_PEAK_G. Falls back to the HBM figure when no profile exists."""
+    v = valu_profile(profile, workload_key)
+    if v is None:
+        return dict(hbm, note=f"no SQ-counter profile for this workload in profiles/{profile}: HBM figure only")
+    achieved = v["_valu"] / (kernel_ms * 1e-3) / 1e9
+    sha = v.get("kernel_source_sha1", "").split(" ")[0]
+    out = {"bound": "valu_issue", "kernel": kernel, "achieved": round(achieved, 2), "peak": VALU_PEAK_G,
+           "unit": "G VALU wave-instructions/s (wave64; 1024 SIMDs x 2.4 GHz / 4 cycles)",
+           "frac": round(achieved / VALU_PEAK_G, 4), "traffic": traffic,
+           "valu_per_launch": v["_valu"],
+           "valu_per_executed_instruction": round(v["_valu"] / max(1.0, executed_per_launch), 2),
+           "frac_counters": v["_frac"], "source": f"profiles/{profile}",
+           "profile_kernel_source_sha1": sha, "profile_matches_build": sha == kernel_source_sha1()}
+    for k in ("window", "active_lane_fraction", "occupancy_waves_per_simd", "lds_bank_conflict_per_lds_instr"):
         if k in v:
             out[k] = v[k]
     return out
@@ -161,11 +183,11 @@ def _timed_cpu_steps(envs_actions, seconds, min_steps=1):
     return steps, time.perf_counter() - t0
 
 
-def cpu_baseline_env(rom_by_mode, kw, levels, modes, seconds, n_req, action_fn, what):
+def cpu_baseline_env(rom_by_mode, kw, levels, modes, seconds, n_req, action_fn, what, preroll):
     """The reference C++ thread pool (oracle/_ref) on the host cores: one FastVecEnv per rom_mode (the reference
-    takes one rom_mode per instance), envs split by their mode, stepped one after the other each step."""
-    import numpy as np
-
+    takes one rom_mode per instance), envs split by their mode, stepped one after the other each step. Like the
+    GPU run, the envs first take `preroll` untimed steps (the steps right after a reset are the cheapest), then 3
+    warm-up steps; then steps are timed for `seconds`."""
     from cpu_libs import OracleVec, RefVec, have_ref
     from fast_mario_env_amd import decode_level
     cores = host_threads()
@@ -189,20 +211,26 @@ def cpu_baseline_env(rom_by_mode, kw, levels, modes, seconds, n_req, action_fn, 
         e.reset()
     build_s = time.perf_counter() - t_build
     pairs = [(e, action_fn) for e in envs]
+    t_pre = time.perf_counter()
+    _timed_cpu_steps(pairs, 0.0, min_steps=preroll) if preroll else None
+    pre_s = time.perf_counter() - t_pre
     _timed_cpu_steps(pairs, 0.0, min_steps=3)
     steps, dt = _timed_cpu_steps(pairs, seconds)
     for e in envs:
         e.close()
     model, load1 = host_info()
     return {"value": round(n * steps / dt, 1), "unit": "agent-steps/s", "cores": threads, "kind": kind,
-            "sample": f"{n} envs ({what}) x {steps} timed steps after 3 warm-up steps ({dt:.1f} s; construction "
-                      f"+ reset {build_s:.1f} s), {len(envs)} instance(s) by rom_mode; {model}; load1 {load1}{why}"}
+            "sample": f"{n} envs ({what}) x {steps} timed steps (steps {preroll + 4}..{preroll + 3 + steps} after the "
+                      f"reset: {preroll} untimed preroll steps and 3 warm-up steps first, as the GPU's window starts "
+                      f"after its preroll) in {dt:.1f} s; construction + reset {build_s:.1f} s, preroll {pre_s:.1f} s; "
+                      f"{len(envs)} instance(s) by rom_mode; {model}; load1 {load1}{why}"}
 
 
-def cpu_baseline_raw(rom, n, prologue, seconds):
+def cpu_baseline_raw(rom, n, prologue, button_rows, seconds_cap):
     """The reference's raw console (fm_raw_*, oracle/_ref): n consoles split over one Python thread per host
-    core (ctypes releases the GIL during each frame call), the same prologue, then random SIMPLE_MOVEMENT
-    frames, every frame rendered (palette screen + RAM in place; no RGB24 conversion)."""
+    core (ctypes releases the GIL during each frame call), the GPU run's prologue, then the GPU run's own button
+    rows for its first n consoles (its warm-up frames untimed, then its timed frames), every frame rendered
+    (palette screen + RAM in place; no RGB24 conversion). Stops early after seconds_cap."""
     import concurrent.futures as cf
 
     import numpy as np
@@ -213,9 +241,9 @@ def cpu_baseline_raw(rom, n, prologue, seconds):
     mk = RefRaw if have_ref() else OracleRaw
     if kind == "port":
         n, cores = 64, 1
+    warm, rows = button_rows
     cons = [mk(rom) for _ in range(n)]
     parts = [cons[t::cores] for t in range(cores)]
-    rng = np.random.default_rng(1)
 
     def run(part, buttons):
         for c, b in zip(part, buttons):
@@ -225,17 +253,22 @@ def cpu_baseline_raw(rom, n, prologue, seconds):
         for f in range(prologue):
             b = np.full(n, 8 if f % 2 == 0 else 0, np.uint8)
             list(pool.map(run, parts, [b[t::cores] for t in range(cores)]))
+        for b in warm:
+            list(pool.map(run, parts, [b[:n][t::cores] for t in range(cores)]))
         frames, t0 = 0, time.perf_counter()
-        tab = np.array(SIMPLE_BUTTONS, np.uint8)
-        while frames < 1 or time.perf_counter() - t0 < seconds:
-            b = tab[rng.integers(0, 7, n)]
-            list(pool.map(run, parts, [b[t::cores] for t in range(cores)]))
+        for b in rows:
+            list(pool.map(run, parts, [b[:n][t::cores] for t in range(cores)]))
             frames += 1
+            if time.perf_counter() - t0 > seconds_cap:
+                break
         dt = time.perf_counter() - t0
     model, load1 = host_info()
+    first = prologue + len(warm)
     return {"value": round(n * frames / dt, 1), "unit": "env-frames/s", "cores": cores, "kind": kind,
-            "sample": f"{n} consoles x {frames} timed frames after the {prologue}-frame prologue ({dt:.1f} s), "
-                      f"{cores} threads; {model}; load1 {load1}"}
+            "sample": f"{n} consoles x {frames} timed frames ({frames} of the GPU's {len(rows)} timed frames: frames "
+                      f"{first + 1}..{first + frames} after power-on, the GPU's first {n} consoles' buttons) in "
+                      f"{dt:.1f} s, after the {prologue}-frame prologue and {len(warm)} warm-up frames; {cores} "
+                      f"threads; {model}; load1 {load1}"}
 
 
 def run_ppo(args):
@@ -424,23 +457,25 @@ def step_loop(env, args, next_actions, timed_actions):
                 reemu={k: re1[k] - re0[k] for k in re1}, bad=env.bad_ops())
 
 
-def env_line(args, metric, n, m, workload_key, config, dtype="u8"):
+def env_line(args, metric, n, m, workload_key, config, sq_profile, dtype="u8"):
     """The JSON line of an env workload from the step_loop measurements."""
     value = n * args.steps / m["dt"]
     k_step_ms = m["stages"]["k_step"]
     k_bytes = n * (K_STEP_BYTES + K_STEP_DONE_BYTES * m["p_done"])
     achieved = k_bytes / (k_step_ms * 1e-3) / 1e9
+    traffic = traffic_from_profiles("k_step_pmc_traffic.md", workload_key)
+    hbm = {"bound": "hbm", "kernel": "k_step", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+           "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": traffic,
+           "algorithmic_bytes_per_launch": round(k_bytes),
+           "note": "k_step's algorithmic bytes (console state, env words, action, outputs, new observation) over its "
+                   "live launch time; traffic: rocprofv3 FETCH_SIZE + WRITE_SIZE per launch"}
+    executed = (m["instr"] - m["ff"]) * n
     return {
         "metric": metric, "value": round(value, 1), "unit": "agent-steps/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(m["dt"] * 1e3 / args.steps, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config,
-        "roofline": {"bound": "hbm", "kernel": "k_step", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
-                     "traffic": traffic_from_profiles(workload_key), "algorithmic_bytes_per_launch": round(k_bytes),
-                     "note": "the live HBM figure of k_step's algorithmic bytes (console state, env words, action, "
-                             "outputs, new observation); k_step is bound by VALU issue and dependent latency, not "
-                             "by HBM: see valu_roofline"},
-        "valu_roofline": valu_roofline(workload_key),
+        "roofline": valu_roofline("k_step", sq_profile, workload_key, k_step_ms, executed, traffic, hbm),
+        "hbm_roofline": hbm,
         "stages_ms_per_step": {k: round(v, 3) for k, v in m["stages"].items()},
         "p_done": round(m["p_done"], 5),
         "preroll_steps": args.preroll,
@@ -484,14 +519,16 @@ def run_headline(args):
     config = {"workload": f"headline: full wrapper stack, {n} envs of 1-1", "envs": n, "level": "1-1",
               "rom": rom_name, "rom_sha1": rom_sha, "seed": 0, **kw,
               "actions": "uniform {0..6}, torch.Generator seed 0 (preroll: its own seed-0 generator)"}
-    out = env_line(args, METRIC, n, m, f"headline/{n}envs/1-1/rom:{rom_sha}", config)
+    out = env_line(args, METRIC, n, m, f"headline/{n}envs/1-1/rom:{rom_sha}", config,
+                   "k_step_sq_counters_headline.md")
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         import numpy as np
         rng = np.random.default_rng(0)
         out["cpu_baseline"] = cpu_baseline_env({"vanilla": rom}, dict(seed=0, **kw), ["1-1"] * args.cpu_envs,
                                                ["vanilla"] * args.cpu_envs, args.cpu_seconds, args.cpu_envs,
-                                               lambda k: rng.integers(0, 7, k), "headline settings, 1-1")
+                                               lambda k: rng.integers(0, 7, k), "headline settings, 1-1",
+                                               args.preroll)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
@@ -535,16 +572,16 @@ def run_stress(args):
               "roms": names, "rom_sha1": rom_sha, "seed": 0, **kw,
               "actions": "per env and step: 2 with p=0.5 else uniform {0..6}; torch.Generator seed 0"}
     metric = f"agent env-steps/sec (skip=4) at {n} envs, divergence stress (32 levels x 4 rom modes) on 1 MI355X"
-    out = env_line(args, metric, n, m, f"stress/{n}envs/rom:{rom_sha}", config)
+    out = env_line(args, metric, n, m, f"stress/{n}envs/rom:{rom_sha}", config, "k_step_sq_counters_stress.md")
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         rng = np.random.default_rng(0)
-        ncpu = args.cpu_envs if args.cpu_envs != 32768 else 8192
+        ncpu = args.cpu_envs
 
         def act(k):
             return np.where(rng.random(k) < 0.5, 2, rng.integers(0, 7, k))
         out["cpu_baseline"] = cpu_baseline_env(roms, dict(seed=0, **kw), levels, modes, args.cpu_seconds, ncpu, act,
-                                               "the first envs of the stress configuration")
+                                               "the first envs of the stress configuration", args.preroll)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
@@ -571,7 +608,8 @@ def run_raw(args):
     tab = torch.tensor(SIMPLE_BUTTONS, dtype=torch.uint8, device=dev)
     rng = np.random.default_rng(1)
     sched = [torch.full((n,), 8 if f % 2 == 0 else 0, dtype=torch.uint8, device=dev) for f in range(prologue)]
-    draws = torch.from_numpy(rng.integers(0, 7, (args.warmup + frames, n))).to(dev)
+    draws_np = rng.integers(0, 7, (args.warmup + frames, n))
+    draws = torch.from_numpy(draws_np).to(dev)
     buttons = tab[draws]                                          # (W + K, n) button bytes on the device
 
     def one(b):
@@ -607,6 +645,11 @@ def run_raw(args):
     # rendered palette screen written
     k_bytes = n * (2 * STATE_BYTES + 1 + 240 * 256)
     achieved = k_bytes / (k_raw_ms * 1e-3) / 1e9
+    hbm = {"bound": "hbm", "kernel": "k_raw", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+           "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
+           "algorithmic_bytes_per_launch": k_bytes,
+           "note": "console state read + written, buttons, palette screen written, over k_raw's live launch time"}
+    workload_key = f"raw/{n}consoles/rom:{rom_sha}"
     out = {
         "metric": f"raw emulator env-frames/sec (skip=1, every frame rendered, RGB24 + RAM out) at {n} consoles on 1 MI355X",
         "value": round(n * frames / dt, 1), "unit": "env-frames/s", "n_gpus": 1, "steps": frames, "warmup": args.warmup,
@@ -615,11 +658,9 @@ def run_raw(args):
         "config": {"workload": f"raw: {n} consoles, 1-1 via a {prologue}-frame Start/none prologue, then SIMPLE_MOVEMENT "
                                f"buttons from default_rng(1) per console and frame", "envs": n, "rom": rom_name,
                    "rom_sha1": rom_sha, "outputs_per_frame": "RGB24 screen (184,320 B) + RAM (2,048 B) per console"},
-        "roofline": {"bound": "hbm", "kernel": "k_raw", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
-                     "algorithmic_bytes_per_launch": k_bytes,
-                     "note": "console state read + written, buttons, palette screen written; like k_step, k_raw is "
-                             "an interpreter bound by VALU issue and dependent latency"},
+        "roofline": valu_roofline("k_raw", "k_raw_sq_counters_raw.md", workload_key, k_raw_ms, (instr - ff) / frames,
+                                  None, hbm),
+        "hbm_roofline": hbm,
         "k_raw_ms": round(k_raw_ms, 4),
         "instructions_per_frame": round(instr / (n * frames), 1),
         "executed_instructions_per_frame": round((instr - ff) / (n * frames), 1),
@@ -629,7 +670,9 @@ def run_raw(args):
     del con
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        out["cpu_baseline"] = cpu_baseline_raw(rom, n, prologue, args.cpu_seconds)
+        host_rows = np.array(SIMPLE_BUTTONS, np.uint8)[draws_np]
+        out["cpu_baseline"] = cpu_baseline_raw(rom, min(n, args.cpu_raw_consoles), prologue,
+                                               (host_rows[:args.warmup], host_rows[args.warmup:]), 4 * args.cpu_seconds)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
@@ -648,7 +691,10 @@ def main():
                     help="before the steps, copy a buffer of this many MiB once (a kernel of known traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--cpu-envs", type=int, default=32768, help="envs of the CPU baseline sample (host RAM allowing)")
+    ap.add_argument("--cpu-envs", type=int, default=4096,
+                    help="envs of the CPU baseline sample (host RAM allowing); it takes the GPU run's preroll first")
+    ap.add_argument("--cpu-raw-consoles", type=int, default=256,
+                    help="consoles of the raw workload's CPU baseline (it runs the GPU run's own frames)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["headline", "stress", "raw", "ppo", "replay"], default="headline")
     ap.add_argument("--ppo-steps", type=int, default=128, help="rollout length of --workload ppo")
