@@ -27,6 +27,8 @@ static inline int __all(int p) { return p != 0; }
 // signed int (widening its result to 64 bits sign-extends it, on the host as on the device)
 static inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
 #define __builtin_amdgcn_wave_barrier() ((void)0)
+// a wave's issue priority orders nothing on the host
+#define __builtin_amdgcn_s_setprio(p) ((void)(p))
 #define __builtin_amdgcn_fence(order, scope) ((void)0)
 // the optimization barrier of Console::in_register, with a host register constraint
 #define MH_REG_BARRIER(x) asm volatile("" : "+r"(x))
