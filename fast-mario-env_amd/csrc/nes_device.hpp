@@ -223,12 +223,18 @@ __device__ __constant__ static const dec::Table kDecode{};
 // control flow fold to the few scalar instructions the opcode needs. Measured on one console running a loop of
 // register instructions: 0.33 us per instruction, against 0.67 us for a body that takes the decode word's
 // fields at run time (inline, as a switch per field).
-// The registers of a lone run, wave-uniform: pc, a, x, y, sp, p, exec_at (ex) and zero_skip (zs).
-struct LoneRegs { uint32_t pc, a, x, y, sp, p; int32_t ex; uint32_t zs, n; };   // n: instructions run (output)
+// The registers of a lone run, wave-uniform: pc, a, x, y, sp, p, exec_at (ex), zero_skip (zs), the PPU's v and t
+// (vt: v | t << 16), fine x and write toggle (px: fine_x | first_write << 8; outputs: bit 16, the run wrote the
+// name tables through $2007, and bit 17, it wrote a PPU register), and n, the instructions run (an output).
+struct LoneRegs { uint32_t pc, a, x, y, sp, p; int32_t ex; uint32_t zs, vt, px, n; };
+// LoneCore::pflags: the PPU register writes a lone run may make ($2005, $2006, $2007 to the pattern and name
+// tables) while rendering is off, and the PPUCTRL bits they need
+constexpr uint32_t LP_WRITES = 1u, LP_INC32 = 2u, LP_NT_SHIFT = 4;
 struct LoneCore {
     LoneRegs r;
     uint8_t* mem;                              // the console's RAM row 0 (row stride np), the same in every active lane
-    uint32_t np;
+    uint8_t* vmem;                             // its VRAM word 0 (word stride 4 np)
+    uint32_t np, pflags;
     const MH_SCALAR_CONST uint32_t* gprg;      // PRG image (read only): scalar loads
     __device__ __forceinline__ uint32_t ram(uint32_t ad) const {
         return __builtin_amdgcn_readfirstlane(mem[(size_t)((ad & 0x7ffu) * np)]);
@@ -244,6 +250,38 @@ struct LoneCore {
     __device__ __forceinline__ static bool reads_ok(uint32_t ad) { return (ad - 0x2000u) >= 0x2000u && (ad | 1u) != 0x4017u; }
     __device__ __forceinline__ static bool writes_ok(uint32_t ad) { return (ad - 0x2000u) >= 0x2000u && (ad & ~2u) != 0x4014u; }
     __device__ __forceinline__ uint32_t read(uint32_t ad) const { return ad < 0x2000u ? ram(ad) : ad >= 0x8000u ? prg(ad) : 0u; }
+    // While rendering is off (both PPUMASK show bits clear), the catch-up PPU neither moves v nor draws anything
+    // but the universal background colour, so the scroll and address writes and the $2007 writes to the pattern
+    // or name tables do not depend on where the PPU has been caught up to, and a lone run makes them without the
+    // catch-up that frame() takes before a PPU register access (a lone run stops before the NMI point, and before
+    // any other PPU register access, $2001 included). $2007 writes to the palette ($3EFF-$3FFE) change that
+    // colour: left to frame().
+    __device__ __forceinline__ bool ppu_write_ok(uint32_t ad) const {
+        if (!(pflags & LP_WRITES) || (ad - 0x2000u) >= 0x2000u) return false;
+        const uint32_t reg = ad & 7u, v = r.vt & 0xffffu;
+        return reg == 5u || reg == 6u || (reg == 7u && (v - 0x3effu) >= 0x100u);
+    }
+    // scroll_write, addr_write and data_write (+ its sp_line reset), as Console does them
+    __device__ __forceinline__ void ppu_write(uint32_t reg, uint32_t d) {
+        uint32_t v = r.vt & 0xffffu, t = r.vt >> 16, fx = r.px & 0xffu, fw = (r.px >> 8) & 1u, dirty = r.px >> 16;
+        if (reg == 5u) {
+            if (fw) { t = (t & ~0x1fu) | (d >> 3); fx = d & 7u; fw = 0; }
+            else { t = (t & ~0x73e0u) | ((d & 7u) << 12) | ((d & 0xf8u) << 2); fw = 1; }
+        } else if (reg == 6u) {
+            if (fw) { t = (t & 0x00ffu) | ((d & 0x3fu) << 8); fw = 0; }
+            else { t = (t & 0xff00u) | d; v = t; fw = 1; }
+        } else {
+            if (v >= 0x2000u && v < 0x3effu) {   // name table (nt_row()): below $2000 the CHR ROM ignores writes
+                const uint32_t k = v < 0x2400u ? 0u : v < 0x2800u ? 1u : v < 0x2c00u ? 2u : 3u;
+                const uint32_t i = ((((pflags >> LP_NT_SHIFT) >> k) & 1u) << 10) | (v & 0x3ffu);
+                vmem[(size_t)((i >> 2) * 4u * np) + (i & 3u)] = (uint8_t)d;
+            }
+            v = (v + ((pflags & LP_INC32) ? 32u : 1u)) & 0xffffu;
+            dirty = 1;
+        }
+        r.vt = v | t << 16;
+        r.px = fx | fw << 8 | dirty << 16 | 1u << 17;
+    }
 };
 
 // One instruction of opcode OP (operand bytes b1, b2) on a lone console; false, with no effect, if it needs
@@ -278,7 +316,7 @@ __device__ __forceinline__ bool lone_op(LoneCore& c, uint32_t b1, uint32_t b2) {
             if (!LoneCore::reads_ok(absv) || !LoneCore::reads_ok(p2)) return false;
         } else {
             if constexpr (rd && am != M_IMM && !zpm) if (!LoneCore::reads_ok(ea)) return false;
-            if constexpr (wr && !zpm) if (!LoneCore::writes_ok(ea)) return false;
+            if constexpr (wr && !zpm) if (!LoneCore::writes_ok(ea) && !c.ppu_write_ok(ea)) return false;
         }
         if constexpr (pen && (am == M_ABSX || am == M_ABSY || am == M_INDY)) sk = ((base ^ ea) & 0xff00u) ? 1 : 0;
         uint32_t m = b1;
@@ -317,7 +355,11 @@ __device__ __forceinline__ bool lone_op(LoneCore& c, uint32_t b1, uint32_t b2) {
         if constexpr (dst == D_X) r.x = res;
         if constexpr (dst == D_Y) r.y = res;
         if constexpr (dst == D_SP) r.sp = res;
-        if constexpr (wr) { if (zpm || ea < 0x2000u) c.set_ram(ea, res); }   // writes elsewhere are ignored
+        if constexpr (wr) {
+            if (zpm || ea < 0x2000u) c.set_ram(ea, res);
+            else if ((ea - 0x2000u) < 0x2000u) c.ppu_write(ea & 7u, res);   // admitted above (ppu_write_ok)
+            // writes elsewhere are ignored
+        }
         // control flow
         const uint32_t ret = (r.pc + 2u) & 0xffffu;
         uint32_t npc = (r.pc + (am == M_NONE ? 1u : (am == M_ABS || am == M_ABSX || am == M_ABSY) ? 3u : 2u)) & 0xffffu;
@@ -387,17 +429,20 @@ __device__ __forceinline__ uint64_t lone_uniform64(uint64_t v) {
 // Runs lone instructions from r until one needs frame(): its catch-up point 3 (ex + 1) past lim, its opcode or
 // operands outside PRG, the idle `JMP *`, or what lone_op() refuses. Returns the registers after the last one
 // run and, in n, how many ran. Not inlined: its registers are its own, not the frame loop's.
-__device__ __attribute__((noinline)) LoneRegs lone_long(LoneRegs in, int32_t lim, uint8_t* mem, uint32_t np,
-                                                        const uint8_t* gprg) {
+__device__ __attribute__((noinline)) LoneRegs lone_long(LoneRegs in, int32_t lim, uint8_t* mem, uint8_t* vmem,
+                                                        uint32_t np, uint32_t pflags, const uint8_t* gprg) {
     LoneCore c;
     c.r.pc = __builtin_amdgcn_readfirstlane(in.pc); c.r.a = __builtin_amdgcn_readfirstlane(in.a);
     c.r.x = __builtin_amdgcn_readfirstlane(in.x); c.r.y = __builtin_amdgcn_readfirstlane(in.y);
     c.r.sp = __builtin_amdgcn_readfirstlane(in.sp); c.r.p = __builtin_amdgcn_readfirstlane(in.p);
     c.r.ex = (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)in.ex);
     c.r.zs = __builtin_amdgcn_readfirstlane(in.zs);
+    c.r.vt = __builtin_amdgcn_readfirstlane(in.vt); c.r.px = __builtin_amdgcn_readfirstlane(in.px);
     lim = (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)lim);
     c.mem = (uint8_t*)lone_uniform64((uint64_t)mem);
+    c.vmem = (uint8_t*)lone_uniform64((uint64_t)vmem);
     c.np = __builtin_amdgcn_readfirstlane(np);
+    c.pflags = __builtin_amdgcn_readfirstlane(pflags);
     c.gprg = (const MH_SCALAR_CONST uint32_t*)(const void*)lone_uniform64((uint64_t)gprg);
     uint32_t n = 0;
     for (;;) {
@@ -1428,13 +1473,22 @@ struct Console {
         int32_t lim = nmi - 1 > calls ? nmi - 1 : calls;
         lim = lim < last ? lim : last;
         lim = lim < 3 * end ? lim : 3 * end;
-        const LoneRegs o = lone_long(LoneRegs{pc, a, x, y, sp, p, exec_at, zero_skip, 0u}, lim, mem, np, cart.gprg);
+        const uint32_t pflags = ((ppu_flags & (PF_SHOW_BG | PF_SHOW_SPR)) ? 0u : LP_WRITES) |
+                                ((ppu_flags & PF_INC32) ? LP_INC32 : 0u) | cart.nt_bits << LP_NT_SHIFT;
+        const LoneRegs o = lone_long(LoneRegs{pc, a, x, y, sp, p, exec_at, zero_skip, (uint32_t)v | (uint32_t)t << 16,
+                                              (uint32_t)fine_x | (uint32_t)first_write << 8, 0u},
+                                     lim, mem, vmem, np, pflags, cart.gprg);
         if (o.n) {
             pc = (uint16_t)o.pc;
             a = o.a; x = o.x; y = o.y; sp = o.sp;
             p = (uint8_t)o.p;
             exec_at = o.ex;
             zero_skip = o.zs;
+            if (o.px >> 17) {   // the run wrote a PPU register
+                v = o.vt & 0xffffu; t = o.vt >> 16;
+                fine_x = o.px & 0xffu; first_write = (o.px >> 8) & 1u;
+                if (o.px & 0x10000u) { bg_key = -1; sp_line = -1; }   // name tables written: the tile-row and sprite-line caches
+            }
             instructions += o.n;
         }
         return o.n;

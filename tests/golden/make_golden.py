@@ -36,13 +36,15 @@ def digest(*arrays) -> str:
 
 # ---------------------------------------------------------------- schedules
 RAW_CASES = ([("mini_smb", 0, 300)] + [(f"program_{s}", s, 240) for s in range(8)] +
-             [(f"random_{s}", s, 120) for s in range(8)])
+             [(f"random_{s}", s, 120) for s in range(8)] + [(f"screenoff_{s}", s, 240) for s in range(4)])
 
 
 def raw_rom(name: str) -> bytes:
     if name == "mini_smb":
         return open(rom_path("vanilla"), "rb").read()
     kind, seed = name.split("_")
+    if kind == "screenoff":
+        return fuzz.program_rom(int(seed), screen_off=True)
     return fuzz.program_rom(int(seed)) if kind == "program" else fuzz.random_rom(int(seed))
 
 

@@ -11,6 +11,10 @@ Two families, both fully determined by a seed:
   balanced stack traffic, subroutine calls, the SMB-shaped sprite-0 poll loop
   (`LDA $2002 / AND #$40 / BEQ`), and ends each pass with either `JMP *` (the idle loop the emulators
   fast-forward) or a jump back. The NMI handler does OAM DMA, VRAM / palette / scroll / control writes.
+  With ``screen_off`` the NMI handler turns rendering off first (as Super Mario Bros.' does), makes its
+  VRAM, scroll and address writes in that state (some with +32 increments, one a bulk $2007 loop) and
+  turns rendering back on at its end, so the next frame draws with the fine x, v and name tables written
+  while the screen was off.
 """
 from __future__ import annotations
 
@@ -101,7 +105,7 @@ class _Gen:
             self.op(mn, mode, a)
 
 
-def program_rom(seed: int, length: int = 400) -> bytes:
+def program_rom(seed: int, length: int = 400, screen_off: bool = False) -> bytes:
     rng = np.random.default_rng(seed)
     g = _Gen(rng)
     # ---- CHR: tile 1 is solid, the rest random
@@ -181,9 +185,22 @@ def program_rom(seed: int, length: int = 400) -> bytes:
     g.emit(0x48, 0x8A, 0x48, 0x98, 0x48)                      # PHA TXA PHA TYA PHA
     g.emit(0xA9, 0x00, 0x8D, 0x03, 0x20)
     g.emit(0xA9, int(rng.choice([0x02, 0x02, 0x03, 0x07])), 0x8D, 0x14, 0x40)
+    if screen_off:
+        g.emit(0xA9, 0x00, 0x8D, 0x01, 0x20)                  # rendering off
+        g.emit(0xA9, 0x90 | int(rng.integers(0, 2)) << 2, 0x8D, 0x00, 0x20)   # NMI on, +1 or +32 increments
+        a = int(rng.integers(0x2000, 0x3000))                 # bulk $2007 run: LDX #n / STA $2007 / DEX / BNE
+        g.emit(0xA9, a >> 8, 0x8D, 0x06, 0x20, 0xA9, a & 0xFF, 0x8D, 0x06, 0x20,
+               0xA9, int(rng.integers(0, 256)), 0xA2, int(rng.integers(1, 256)))
+        top = g.pc
+        g.emit(0x8D, 0x07, 0x20, 0xCA, 0xD0, (top - (top + 6)) & 0xFF)
     for _ in range(int(rng.integers(2, 12))):
         k = rng.random()
-        if k < 0.4:                                           # VRAM byte at a random nametable address
+        if screen_off and k < 0.15:                           # scroll pair (fine x) or a lone $2006 write
+            if rng.random() < 0.5:
+                g.emit(0xA9, int(rng.integers(0, 256)), 0x8D, 0x05, 0x20, 0xA9, int(rng.integers(0, 256)), 0x8D, 0x05, 0x20)
+            else:
+                g.emit(0xA9, int(rng.integers(0, 256)), 0x8D, 0x06, 0x20)
+        elif k < 0.4:                                           # VRAM byte at a random nametable address
             a = int(rng.integers(0x2000, 0x3000))
             g.emit(0xAD, 0x02, 0x20, 0xA9, a >> 8, 0x8D, 0x06, 0x20, 0xA9, a & 0xFF, 0x8D, 0x06, 0x20,
                    0xA9, int(rng.integers(0, 256)), 0x8D, 0x07, 0x20)

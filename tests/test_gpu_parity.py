@@ -77,6 +77,14 @@ def test_raw_program_fuzz_two_waves():
     _raw_run(fuzz.program_rom(3), 40, scaled(40), seed=3, backup_p=0.05)
 
 
+@pytest.mark.parametrize("seed", [0, 1, 3])
+def test_raw_screen_off_fuzz(seed):
+    # an NMI handler that makes its VRAM, scroll and address writes with rendering off (a bulk $2007 loop among
+    # them) and turns rendering on at its end; 40 consoles, so a console often runs alone in its wave and its
+    # lone runs make those writes themselves
+    _raw_run(fuzz.program_rom(seed, screen_off=True), 40, scaled(60), seed=seed, backup_p=0.05)
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_raw_random_fuzz(seed):
     _raw_run(fuzz.random_rom(seed), 4, scaled(40), seed=seed, render_p=0.5, backup_p=0.05)
