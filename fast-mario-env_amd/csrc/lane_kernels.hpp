@@ -294,7 +294,7 @@ struct LaneCtx {
 // console e of the memory block `mem` (np consoles), on CHR bank `bank` of the staged cartridge
 __device__ __forceinline__ void attach(Console& c, const LaneCtx& x, uint8_t* mem, uint32_t np, uint32_t e,
                                        uint32_t bank = 0) {
-    c.mem = mem + e; c.vmem = mem + vram_word_offset(np, e, 0); c.np = np;
+    c.mbase = mem; c.eo = e; c.vo = (uint32_t)vram_word_offset(np, e, 0); c.np = np;
     c.cart = x.cart; c.cart.chr += bank * 0x2000u; c.lut = x.lut; c.lds_sp = x.sp; c.lds_gp = x.gp;
     c.lds_bg = x.gp + LDS_GP_WORDS * LDS_LANES; c.bg_key = -1;
     c.lds_oam = x.gp + (LDS_GP_WORDS + LDS_BG_WORDS) * LDS_LANES;

@@ -732,6 +732,7 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
         g_err = "invalid arguments";
         return nullptr;
     }
+    if ((uint32_t)n > MAX_ENVS) { g_err = "too many envs (at most 979,648: console memory takes 32-bit offsets)"; return nullptr; }
     // the cartridge image: ROM 0's PRG, then the CHR of every ROM; the ROMs must agree on PRG and mirroring
     std::vector<uint8_t> img;
     uint16_t nt[4];
@@ -1061,6 +1062,7 @@ int64_t mh_env_bytes(MhEnv* h) {
 MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     g_err.clear();
     if (n < 1) { g_err = "invalid arguments"; return nullptr; }
+    if ((uint32_t)n > MAX_ENVS) { g_err = "too many consoles (at most 979,648: console memory takes 32-bit offsets)"; return nullptr; }
     std::vector<uint8_t> img;
     uint16_t nt[4];
     if (!load_cart(rom, rom_len, img, nt)) return nullptr;

@@ -24,6 +24,10 @@
 namespace mh {
 
 constexpr int ROW_RAM = 0, ROW_VRAM = 2048, ROW_OAM = 4096, ROW_PAL = 4352, MEM_ROWS = 4384;
+// Most envs (consoles) of one instance: the padded count np (a multiple of 64) keeps MEM_ROWS * np below
+// 2^32, so every byte of the console memory has a 32-bit offset from its base.
+constexpr uint32_t MAX_ENVS = (uint32_t)((0xffffffffull / MEM_ROWS) & ~63ull);
+static_assert(MAX_ENVS == 979648 && (uint64_t)MEM_ROWS * MAX_ENVS <= 0xffffffffull, "32-bit console memory offsets");
 // Emulator launch shape. Each env runs on LANES_PER_ENV lanes of a 64-lane wave (its parts: lanes
 // s, s + ENVS_PER_WAVE, ...), so a wave carries ENVS_PER_WAVE = 64 / LANES_PER_ENV envs, and a block of
 // WAVES_PER_BLOCK waves holds LDS_LANES = 128 env slots sharing one LDS copy of the cartridge. The parts run
@@ -483,8 +487,11 @@ struct Cart {
 
 struct Console {
     // ---- memory views
-    uint8_t* mem;            // MEM + e (row stride np)
-    uint8_t* vmem;           // this env's VRAM word 0 (word stride 4 np)
+    // Addresses are a wave-uniform base and a 32-bit per-lane byte offset (the MEM array is below 4 GiB:
+    // MAX_ENVS), so a load or store is one address add into the offset and the base stays in scalar registers.
+    uint8_t* mbase;          // MEM: row r of env e at byte r * np + e
+    uint32_t eo;             // e
+    uint32_t vo;             // byte offset of this env's VRAM word 0 (word w at vo + 4 w np)
     uint32_t np;
     Cart cart;
     uint8_t* gray;           // GRAY slot + 4 e: pixels 4i..4i+3 in the 32-bit word at gray + 4 i np
@@ -534,8 +541,8 @@ struct Console {
     uint32_t* lds_oam;       // per-lane OAM (same word stride): the live copy between load()/power_on() and store()
 
     // ------------------------------------------------------------ interleaved memory
-    __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mem[(size_t)__umul24(row, np)]; }
-    __device__ __forceinline__ void st(uint32_t row, uint8_t val) { mem[(size_t)__umul24(row, np)] = val; }
+    __device__ __forceinline__ uint8_t ld(uint32_t row) const { return mbase[(uint32_t)__umul24(row, np) + eo]; }
+    __device__ __forceinline__ void st(uint32_t row, uint8_t val) { mbase[(uint32_t)__umul24(row, np) + eo] = val; }
     __device__ __forceinline__ uint8_t ram(uint32_t a) const { return ld(ROW_RAM + (a & 0x7ff)); }
     __device__ __forceinline__ uint8_t oam(uint32_t i) const {
         i &= 0xff;
@@ -549,17 +556,17 @@ struct Console {
     __device__ __forceinline__ uint32_t oam_sprite(int k) const { return lds_oam[k * LDS_LANES]; }
     __device__ __forceinline__ uint8_t pal(uint32_t i) const { return ld(ROW_PAL + (i & 0x1f)); }
     // VRAM is word-interleaved: byte i of this env is byte i % 4 of 32-bit word i / 4, and word w sits at
-    // vmem + 4 w np (vmem: this env's word 0), so a name-table row is 8 word loads
+    // byte vo + 4 w np of MEM, so a name-table row is 8 word loads
     __device__ __forceinline__ uint8_t vram(uint32_t i) const {
         i &= 0x7ff;
-        return vmem[(size_t)__umul24(i >> 2, 4 * np) + (i & 3)];
+        return mbase[vo + (uint32_t)__umul24(i >> 2, 4 * np) + (i & 3)];
     }
     __device__ __forceinline__ void set_vram(uint32_t i, uint8_t d) {
         i &= 0x7ff;
-        vmem[(size_t)__umul24(i >> 2, 4 * np) + (i & 3)] = d;
+        mbase[vo + (uint32_t)__umul24(i >> 2, 4 * np) + (i & 3)] = d;
     }
     __device__ __forceinline__ uint32_t vram_word(uint32_t w) const {
-        return *(const uint32_t*)(vmem + (size_t)__umul24(w & 0x1ff, 4 * np));
+        return *(const uint32_t*)(mbase + (vo + (uint32_t)__umul24(w & 0x1ff, 4 * np)));
     }
     __device__ __forceinline__ uint8_t sl(int k) const {
         return (uint8_t)((k < 4 ? sl_lo >> (8 * k) : sl_hi >> (8 * (k - 4))) & 0xff);
@@ -638,7 +645,7 @@ struct Console {
     __device__ void power_on() {
         for (uint32_t r = 0; r < MEM_ROWS; r++)
             if (r < ROW_VRAM || r >= ROW_VRAM + 2048) st(r, 0);
-        for (uint32_t w = 0; w < 512; w++) *(uint32_t*)(vmem + (size_t)__umul24(w, 4 * np)) = 0;
+        for (uint32_t w = 0; w < 512; w++) *(uint32_t*)(mbase + (vo + (uint32_t)__umul24(w, 4 * np))) = 0;
         iter_lo = iter_hi = 0; exec_at = 0; ppu_calls = 0;
         joy_strobe = 3; joy = 0;
         zero_skip = 0; a = x = y = 0; p = 0x34;
@@ -1084,7 +1091,6 @@ struct Console {
         uint32_t bp0 = lds_gp[0], bp1 = lds_gp[LDS_LANES], bp2 = lds_gp[2 * LDS_LANES], bp3 = lds_gp[3 * LDS_LANES];
         // keep them in registers: a select of these loads must not become a load from a selected address
         in_register(bp0); in_register(bp1); in_register(bp2); in_register(bp3);
-        const uint32_t ubg = bp0 & 0xffu;                // palette address 0: the universal background
         uint32_t sp0 = 0, sp1 = 0, sp2 = 0, sp3 = 0;
         if (spr) {
             sp0 = lds_gp[4 * LDS_LANES]; sp1 = lds_gp[5 * LDS_LANES];
@@ -1112,11 +1118,13 @@ struct Console {
         bg_planes(tile_of(pg + 1), fy, bgpal, blo, bhi, bgt);
         bg_planes(tile_of(pg + 2), fy, bgpal, clo, chi, cgt);
         uint32_t nxa = tile_of(pg + S), nxb = tile_of(pg + S + 1), nxc = tile_of(pg + S + 2);
-        if (!show_bg()) { alo = ahi = blo = bhi = clo = chi = 0; agt = bgt = cgt = ubg; }
         const int ws0 = 2 * pg < 60 ? 2 * pg : 60;
         uint32_t s0 = lds_sp[ws0 * LDS_LANES], s1 = lds_sp[(ws0 + 1) * LDS_LANES];   // the pair's sprite bytes
         uint32_t s2 = lds_sp[(ws0 + 2) * LDS_LANES], s3 = lds_sp[(ws0 + 3) * LDS_LANES];
-        if (!spr) s0 = s1 = s2 = s3 = 0;
+        // A layer that is off is masked out of every pixel rather than zeroed at its fetch: with the background
+        // pattern masked to 0 a pixel takes byte 0 of its tile's gray table, the universal background, as it
+        // does with the background off; with the sprite bytes masked no sprite pixel is taken.
+        const uint32_t keep_bg = show_bg() ? ~0u : 0u, keep_sp = spr ? ~0u : 0u;
         uint32_t* wp = (uint32_t*)gray + ((size_t)py * 64 + 2 * pg) * np;   // word of pixels 8pg .. 8pg+3
         // the two words of the group drawn from tiles (lo0, hi0, gt0) and (lo1, hi1, gt1) with sprite bytes ca, cb
         auto group_words = [&](uint32_t lo0, uint32_t hi0, uint32_t gt0, uint32_t lo1, uint32_t hi1, uint32_t gt1,
@@ -1174,17 +1182,17 @@ struct Console {
             const uint32_t t2 = lds_sp[(ws + 2) * LDS_LANES], t3 = lds_sp[(ws + 3) * LDS_LANES];
             uint32_t out0[2], out1[2];
             // pixels 0-7 may hide either layer
-            group_words(alo, ahi, agt, blo, bhi, bgt, s0, s1, (pg == 0 && hide_edge_bg()) ? 0u : ~0u,
-                        (pg == 0 && hide_edge_spr()) ? 0u : ~0u, out0);
-            group_words(blo, bhi, bgt, clo, chi, cgt, s2, s3, ~0u, ~0u, out1);
+            group_words(alo, ahi, agt, blo, bhi, bgt, s0, s1, (pg == 0 && hide_edge_bg()) ? 0u : keep_bg,
+                        (pg == 0 && hide_edge_spr()) ? 0u : keep_sp, out0);
+            group_words(blo, bhi, bgt, clo, chi, cgt, s2, s3, keep_bg, keep_sp, out1);
             store_group(8 * pg, wp, out0);
             store_group(8 * pg + 8, wp + 2 * np, out1);
             wp += 2 * S * np;
-            alo = show_bg() ? dlo : 0u; ahi = show_bg() ? dhi : 0u; agt = show_bg() ? dgt : ubg;
-            blo = show_bg() ? elo : 0u; bhi = show_bg() ? ehi : 0u; bgt = show_bg() ? egt : ubg;
-            clo = show_bg() ? flo : 0u; chi = show_bg() ? fhi : 0u; cgt = show_bg() ? fgt : ubg;
+            alo = dlo; ahi = dhi; agt = dgt;
+            blo = elo; bhi = ehi; bgt = egt;
+            clo = flo; chi = fhi; cgt = fgt;
             nxa = na; nxb = nb; nxc = nc;
-            s0 = spr ? t0 : 0u; s1 = spr ? t1 : 0u; s2 = spr ? t2 : 0u; s3 = spr ? t3 : 0u;
+            s0 = t0; s1 = t1; s2 = t2; s3 = t3;
         }
     }
 
@@ -1477,7 +1485,7 @@ struct Console {
                                 ((ppu_flags & PF_INC32) ? LP_INC32 : 0u) | cart.nt_bits << LP_NT_SHIFT;
         const LoneRegs o = lone_long(LoneRegs{pc, a, x, y, sp, p, exec_at, zero_skip, (uint32_t)v | (uint32_t)t << 16,
                                               (uint32_t)fine_x | (uint32_t)first_write << 8, 0u},
-                                     lim, mem, vmem, np, pflags, cart.gprg);
+                                     lim, mbase + eo, mbase + vo, np, pflags, cart.gprg);
         if (o.n) {
             pc = (uint16_t)o.pc;
             a = o.a; x = o.x; y = o.y; sp = o.sp;

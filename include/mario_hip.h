@@ -40,7 +40,8 @@ const char* mh_last_error(void);
  *   levels        3*n ints (world, stage, area) per env, host memory
  *   lut           256 bytes, palette value -> gray, host memory
  *   rng           6*n u64 per env: numpy PCG64 (state_hi, state_lo, inc_hi, inc_lo, has_uint32, uinteger)
- *   skip 1..16, frame_stack 1..16, maxpool 0/1, sticky in [0, 1], noop_max >= 0, max_steps >= 1.
+ *   skip 1..16, frame_stack 1..16, maxpool 0/1, sticky in [0, 1], noop_max >= 0, max_steps >= 1,
+ *   1 <= n <= 979648 (the console memory is addressed with 32-bit offsets).
  * Blocks until construction is finished. */
 MhEnv* mh_create(const uint8_t* rom, int64_t rom_len, int n, const int* levels, const uint8_t* lut,
                  int skip, int max_steps, double sticky, int noop_max, int maxpool, int frame_stack,
@@ -121,6 +122,7 @@ int64_t mh_state_bytes(void);
 int64_t mh_env_bytes(MhEnv* h);
 
 /* ---- raw consoles: frame stepping without the env layer (replaces fm_raw_*, fastmario.cpp:651-673) */
+/* 1 <= n <= 979648 consoles (32-bit offsets into the console memory) */
 MhRaw*  mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device);
 /* one frame of every console; d_buttons: n u8 device pointer; render != 0 draws the screen */
 int     mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream);

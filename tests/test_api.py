@@ -124,6 +124,28 @@ def test_create_roms_validates_before_the_gpu():
         fme.HipVecEnv("1-1", 5, rom_mode=["vanilla", "pixel", "downsample", "rectangle", "other"])
 
 
+def test_create_rejects_more_envs_than_32bit_offsets_address():
+    """The console memory (4,384 rows of np bytes) is addressed with 32-bit offsets from its base: both
+    creators refuse more than 979,648 envs, with a message, before they touch a device."""
+    L = ctypes.CDLL(_native.lib_path())
+    L.mh_create_roms.restype = ctypes.c_void_p
+    L.mh_raw_create.restype = ctypes.c_void_p
+    L.mh_last_error.restype = ctypes.c_char_p
+    P = ctypes.c_void_p
+    n = 979_649
+    mini = open(rom_path("vanilla"), "rb").read()
+    blob = np.frombuffer(mini, np.uint8).copy()
+    lens = np.array([len(mini)], np.int64)
+    lv = np.ones(3 * n, np.int32)
+    rng = np.zeros(6 * n, np.uint64)
+    lut = fme.gray_lut()
+    assert not L.mh_create_roms(P(blob.ctypes.data), P(lens.ctypes.data), 1, None, n, P(lv.ctypes.data),
+                                P(lut.ctypes.data), 4, 2000, ctypes.c_double(0.0), 0, 0, 4, P(rng.ctypes.data), 0)
+    assert b"too many envs" in L.mh_last_error()
+    assert not L.mh_raw_create(P(blob.ctypes.data), ctypes.c_int64(len(mini)), n, 0)
+    assert b"too many consoles" in L.mh_last_error()
+
+
 @pytest.mark.skipif(HAVE_GPU, reason="checks the no-GPU error path")
 def test_no_cpu_fallback():
     """Without a GPU the product raises; there is no silent CPU path."""
