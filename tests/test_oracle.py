@@ -247,3 +247,23 @@ def test_alu_textbook(seed):
         i = bad[0] // 2
         pytest.fail(f"case {i} {alu_rom.cases(seed)[i]}: got {got[2*i:2*i+2]} want {expect[2*i:2*i+2]}")
     assert con.bad_ops() == 0
+
+
+# ---------------------------------------------------------------- committed GPU fidelity records
+def test_fidelity_records():
+    """The committed fidelity records (tests/fidelity/*.jsonl, written on the GPU by the scripts beside them) hold
+    the runs they claim, with no mismatch: 512 envs over the 32 levels x 1,500 steps in each of 5 configurations
+    (every env every step against the oracle), and 512 raw consoles x 20,040 frames (RAM and machine state every
+    frame, the screen every 4th)."""
+    import json
+    d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "fidelity")
+    env = [json.loads(l) for l in open(os.path.join(d, "env_fidelity.jsonl"))]
+    assert [r["config"] for r in env] == ["default", "sticky_noop", "short_timelimit", "headline", "runner"]
+    for r in env:
+        assert r["n"] == 512 and r["steps"] == 1500 and r["ok"] and not r["mismatches"], r["config"]
+        assert r["bad_ops"] == 0 and r["oracle_bad_ops"] == 0 and r["episodes"] > 1000
+    assert sum(r["flags"] for r in env) > 0          # the runner reaches the flagpole
+    assert env[3]["reemulations"]["pair"] > 0 and env[3]["reemulations"]["k2"] > 0
+    raw = [json.loads(l) for l in open(os.path.join(d, "raw_fidelity.jsonl"))]
+    assert len(raw) == 1 and raw[0]["ok"] and not raw[0]["mismatches"]
+    assert raw[0]["consoles"] == 512 and raw[0]["frames"] == 20040 and raw[0]["bad_ops"] == 0
