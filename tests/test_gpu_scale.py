@@ -174,9 +174,11 @@ def test_headline_4096_envs_mixed_levels():
 def test_divergence_stress_65536_envs():
     """The divergence-stress instance at its full size: 65,536 envs, levels drawn from default_rng(7) over the 32
     world-stage pairs, rom_mode cycled over the four variants per env, sticky 0.25, no-op 30, skip 4, no
-    max-pool; per env, action 2 (right + A) with p = 0.5, else uniform over 0..6."""
+    max-pool; per env, action 2 (right + A) with p = 0.5, else uniform over 0..6. 330 steps: as far as bench.py's
+    stress line (300 preroll steps, then its warm-up and timed window), where busy runs in one env of a wave set the
+    kernel's time."""
     from fast_mario_env_amd import ALL_LEVELS
-    n, T = 65536, 30
+    n, T = 65536, 330
     lv = np.random.default_rng(7).integers(0, 32, n)
     names = [ALL_LEVELS[k] for k in lv]
     modes = [MODES[i % 4] for i in range(n)]
@@ -184,7 +186,7 @@ def test_divergence_stress_65536_envs():
     acts = np.where(rng.random((T, n)) < 0.5, 2, rng.integers(0, 7, (T, n)))
     actions = torch.from_numpy(acts).to("cuda:0")
     n_done, eps, re = _run(names, modes, STRESS, 0, actions, stride=1021, extra=24, two_pass=True)
-    assert n_done > 0 and eps > 0
+    assert n_done > 1000 and eps >= 24, (n_done, eps)
     assert re["one"] > 0, re
 
 
