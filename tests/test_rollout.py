@@ -126,6 +126,60 @@ def test_rollout_vs_oracle():
 
 
 @pytest.mark.gpu
+def test_rollout_2048_envs_full_length_vs_oracle():
+    """A full-length rollout (T = 128, the reference trainer's n_steps) of 2,048 envs over the 32 levels with the
+    headline wrappers and a 100-step time limit (episodes end by death and by truncation inside the rollout, and
+    the k_step waves beyond the first 64 compute their observations in-kernel): every env's stored observation
+    stack, action-stepped reward (with the timeout bootstrap) and episode start against 16 oracle instances of
+    128 envs on their own PCG64 streams (env_offset), stepping the rollout's recorded actions on a thread pool."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    from build_roms import rom_path
+    from cpu_libs import OracleVec
+    from fast_mario_env_amd import ALL_LEVELS, HipVecEnv, decode_level
+    from fast_mario_env_amd.rollout import make_net
+    rom = open(rom_path("vanilla"), "rb").read()
+    names = [ALL_LEVELS[i % 32] for i in range(2048)]
+    kw = dict(sticky=0.25, noop_max=30, max_steps=100, skip=4, frame_stack=4, maxpool=True)
+    n, T, gamma, m = len(names), 128, 0.99, 128
+    env = HipVecEnv(names, n, rom=rom, seed=0, **kw)
+    env.reset()
+    net = make_net(seed=0)
+    ro = Rollout(env, net, T=T, seed=4, gamma=gamma)
+    ro.collect()
+    pool = ThreadPoolExecutor(min(16, os.cpu_count() or 1))
+    cpu = list(pool.map(lambda k: OracleVec(rom, [decode_level(x) for x in names[k:k + m]], m, seed=0, env_offset=k,
+                                            **kw), range(0, n, m)))
+    list(pool.map(lambda c: c.reset(), cpu))
+    acts = ro.act.cpu().numpy()
+    n_boot = n_term = 0
+    for t in range(T):
+        o = np.concatenate([c.obs for c in cpu])
+        bad = np.flatnonzero((ro.obs(t).cpu().numpy() != o).reshape(n, -1).any(1))
+        assert bad.size == 0, (t, "obs of envs", bad[:8].tolist())
+        outs = list(pool.map(lambda kc: [x.copy() for x in kc[1].step(acts[t, kc[0]:kc[0] + m])[1:4]] + [kc[1].fin.copy()],
+                             zip(range(0, n, m), cpu)))
+        rew, term, trunc, fin = (np.concatenate(z) for z in zip(*outs))
+        want = torch.from_numpy(rew).cuda()
+        boot = np.flatnonzero(trunc & ~term)
+        if boot.size:
+            n_boot += boot.size
+            with torch.no_grad():
+                _, v = net(torch.from_numpy(fin[boot]).cuda())
+            want[torch.from_numpy(boot).cuda()] += gamma * v
+        n_term += int(term.sum())
+        # rewards are integers; the bootstrap term's bf16 trunk may take another convolution algorithm here
+        assert torch.allclose(ro.rew[t], want, rtol=0, atol=2e-3), t
+        nxt = ro.start[t + 1] if t + 1 < T else ro.next_start
+        assert np.array_equal(nxt.cpu().numpy(), term | trunc), t
+    pool.shutdown()
+    assert n_boot > 0 and n_term > 0, (n_boot, n_term)
+    assert env.bad_ops() == 0
+    env.close()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("k,n", [(4, 97), (1, 5), (2, 3), (8, 2)])
 def test_policy_input_kernel_matches_torch_scaling(k, n):
     # mh_policy_input against torch's own float32 scaling cast to bf16 (round to nearest even), bit for bit,
