@@ -191,14 +191,69 @@ __global__ void EMU_BOUNDS k_cache(CacheArgs A) {
     if (ci < A.nc) cache_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), ci);
 }
 
-__global__ void EMU_BOUNDS k_step(StepArgs A) {
+// k_step's launch order for the next step. When k_step has more blocks than the GPU has CUs (past 32,768 envs on
+// 256 CUs), a block that starts late and runs long holds the kernel's end, and a block holds its CU until its slowest
+// env is done. A group's busy run (an area transition, a death, a level load) lasts several steps, so the last step's
+// work predicts the next one's: the groups run in order of their slowest env's executed 6502 instructions in the
+// last step, most first, and the cheap ones fill the CUs they free (longest-first list scheduling).
+// k_work: each group's slowest env's executed instructions since the last call, from the env counters.
+__global__ __launch_bounds__(LDS_LANES) void k_work(const uint32_t* ev, uint32_t np, int n, uint64_t* prev,
+                                                    uint32_t* work) {
+    const uint32_t e = blockIdx.x * LDS_LANES + threadIdx.x;
+    uint32_t w = 0;
+    if (e < (uint32_t)n) {
+        auto counter = [&](int lo) {
+            return (uint64_t)ev[(size_t)lo * np + e] | (uint64_t)ev[(size_t)(lo + 1) * np + e] << 32;
+        };
+        const uint64_t c = counter(E_INSTR_LO) - counter(E_FF_LO);
+        const uint64_t d = c - prev[e];
+        w = d > 0xffffffffull ? 0xffffffffu : (uint32_t)d;
+        prev[e] = c;
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)w, off);
+        w = o > w ? o : w;
+    }
+    __shared__ uint32_t wmax[LDS_LANES / 64];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = w;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < LDS_LANES / 64; k++) w = wmax[k] > w ? wmax[k] : w;
+        work[blockIdx.x] = w;
+    }
+}
+// k_order: one block; a bitonic sort of (work, ~index) keys in LDS (ties: the lower index first).
+constexpr int ORDER_MAX = 8192;   // groups: MAX_ENVS / LDS_LANES fits
+__global__ __launch_bounds__(1024) void k_order(const uint32_t* work, uint32_t* perm, int ng) {
+    __shared__ uint64_t key[ORDER_MAX];
+    int P = 1;
+    while (P < ng) P <<= 1;
+    for (int i = threadIdx.x; i < P; i += blockDim.x)
+        key[i] = i < ng ? ((uint64_t)work[i] << 32 | (uint32_t)~(uint32_t)i) : 0ull;   // padding sorts last
+    __syncthreads();
+    for (int k = 2; k <= P; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < P; i += blockDim.x) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const uint64_t a = key[i], b = key[l];
+                    if ((i & k) == 0 ? a < b : a > b) { key[i] = b; key[l] = a; }   // descending overall
+                }
+            }
+            __syncthreads();
+        }
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) perm[i] = ~(uint32_t)key[i];
+}
+static_assert(MAX_ENVS / LDS_LANES <= ORDER_MAX, "k_order holds every group");
+
+__device__ __forceinline__ void step_block(const StepArgs& A, uint32_t base) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
     // The frame loop issues ahead of the observations of the waves that have finished it (on a SIMD, the two
     // waves' instructions are arbitrated by this priority first).
     __builtin_amdgcn_s_setprio(2);
     const int slot = lane_slot();
-    const uint32_t e = block_base() + (uint32_t)slot;
+    const uint32_t e = base + (uint32_t)slot;
     const bool live = e < (uint32_t)A.n;
     uint32_t bits = 0;
     if (live) bits = step_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
@@ -215,6 +270,13 @@ __global__ void EMU_BOUNDS k_step(StepArgs A) {
         __builtin_amdgcn_s_setprio(0);
         obs_tail<12>(A.gray, A.np, A.fresh, A.boot_obs, e, lane_part(), bits, 0);
     }
+}
+
+// base: the first env slot of the block's group (blocks of blockDim.x / 64 waves)
+__global__ void EMU_BOUNDS k_step(StepArgs A) { step_block(A, block_base()); }
+// k_step in the launch order of k_order: block b runs group perm[b]
+__global__ void EMU_BOUNDS k_step_ordered(StepArgs A, const uint32_t* perm) {
+    step_block(A, perm[blockIdx.x] * ((blockDim.x >> 6) * ENVS_PER_WAVE));
 }
 
 // The observations of the envs of the waves that finished k_step's frame loop last (obs_tail, one wave per
@@ -661,6 +723,10 @@ struct MhEnv {
     AreaTables* T = nullptr;
     uint8_t *mem = nullptr, *gray = nullptr, *fresh = nullptr;
     uint32_t* obs_order = nullptr;     // k_step's finish counter and the deferred waves (k_obs_late)
+    // k_step's launch order (k_work, k_order), when it has more blocks than the GPU has CUs: null otherwise
+    uint32_t *grp_work = nullptr, *grp_perm = nullptr;
+    uint64_t* grp_prev = nullptr;      // each env's executed-instruction count at the last k_work
+    int n_groups = 0;
     uint32_t *sc = nullptr, *ev = nullptr;
     uint8_t* snap_mem = nullptr;     // 2 snapshot slots of the live consoles (early-termination re-emulation)
     uint32_t* snap_sc = nullptr;
@@ -808,6 +874,15 @@ MhEnv* mh_create_roms(const uint8_t* roms, const int64_t* rom_lens, int n_roms, 
     h->snap_sc = B.alloc<uint32_t>((size_t)2 * S_COUNT * h->np, good);
     h->fresh = B.alloc<uint8_t>((size_t)OBS_PIX * h->np, good);
     h->obs_order = B.alloc<uint32_t>(1 + OBS_LATE_MAX, good);
+    {
+        const EmuLaunch ls = emu_launch(h->n, h->cus);
+        if ((int)ls.grid.x > h->cus) {   // more than one block per CU: the launch order decides what runs last
+            h->n_groups = (int)ls.grid.x;
+            h->grp_work = B.alloc<uint32_t>(h->n_groups, good);
+            h->grp_perm = B.alloc<uint32_t>(h->n_groups, good);
+            h->grp_prev = B.alloc<uint64_t>(h->np, good);
+        }
+    }
     h->boot_mem = B.alloc<uint8_t>((size_t)MEM_ROWS * h->nlp, good);
     h->boot_sc = B.alloc<uint32_t>((size_t)S_COUNT * h->nlp, good);
     h->boot_gray = B.alloc<uint8_t>((size_t)GRAY_PIX * h->nlp, good);
@@ -945,7 +1020,14 @@ int mh_step_async(MhEnv* h, const int64_t* d_actions, void* stream) {
                 h->rew, h->term, h->trunc, h->info, h->ep_ret, h->ep_len, h->key_bank, h->slot_env, h->fresh,
                 h->boot_obs, h->obs_order, (uint32_t)(waves - late), (uint32_t)waves};
     const EmuLaunch ls = emu_launch(h->n, h->cus);
-    hipLaunchKernelGGL(k_step, ls.grid, ls.block, 0, s, sa);
+    if (h->grp_perm) {   // this step's launch order, from the last step's work
+        hipLaunchKernelGGL(k_work, dim3((unsigned)h->n_groups), dim3(LDS_LANES), 0, s, h->ev, h->np, h->n,
+                           h->grp_prev, h->grp_work);
+        hipLaunchKernelGGL(k_order, dim3(1), dim3(1024), 0, s, h->grp_work, h->grp_perm, h->n_groups);
+        hipLaunchKernelGGL(k_step_ordered, ls.grid, ls.block, 0, s, sa, (const uint32_t*)h->grp_perm);
+    } else {
+        hipLaunchKernelGGL(k_step, ls.grid, ls.block, 0, s, sa);
+    }
     CK(hipGetLastError());
     if (mark(h, s, 1)) return -1;
     const ObsLateArgs la{h->n, h->np, late, h->ev, h->gray, h->fresh, h->boot_obs, h->obs_order};

@@ -190,6 +190,39 @@ def test_divergence_stress_65536_envs():
     assert re["one"] > 0, re
 
 
+def test_ordered_launch_40960_envs_every_env_vs_oracle():
+    """Past 32,768 envs on 256 CUs k_step has more blocks than CUs, and each step launches its block groups in the
+    order k_work and k_order derive from the last step's work (k_step_ordered): 40,960 envs (320 groups) of mixed
+    levels, every env's observation, reward, done flags and info against 16 oracle instances each step, so a group
+    that ran twice or not at all in a step would show."""
+    from fast_mario_env_amd import ALL_LEVELS, HipVecEnv
+    n, T, m = 40960, 6, 2560
+    lv = np.random.default_rng(13).integers(0, 32, n)
+    names = [ALL_LEVELS[k] for k in lv]
+    gpu = HipVecEnv(names, n, seed=2, rom=ROMS["vanilla"], device="cuda:0", **HEADLINE)
+    pool = ThreadPoolExecutor(min(16, os.cpu_count() or 1))
+    cpu = list(pool.map(lambda k: OracleVec(ROMS["vanilla"], _levels(names[k:k + m]), m, seed=2, env_offset=k,
+                                            **HEADLINE), range(0, n, m)))
+    o1 = np.concatenate(list(pool.map(lambda c: c.reset().copy(), cpu)))
+    assert np.array_equal(o1, gpu.reset().cpu().numpy()), "reset obs"
+    rng = np.random.default_rng(29)
+    for t in range(T):
+        a = np.where(rng.random(n) < 0.5, 2, rng.integers(0, 7, n))
+        outs = list(pool.map(lambda kc: [x.copy() for x in kc[1].step(a[kc[0]:kc[0] + m])], zip(range(0, n, m), cpu)))
+        o1, r1, te1, tr1, i1 = (np.concatenate(z) for z in zip(*outs))
+        o2, r2, te2, tr2, _ = gpu.step(torch.from_numpy(a).to("cuda:0"))
+        o2, r2, te2, tr2, i2 = (x.cpu().numpy() for x in (o2, r2, te2, tr2, gpu.info_t))
+        assert np.array_equal(r1, r2) and np.array_equal(te1, te2) and np.array_equal(tr1, tr2), (t, "reward/done")
+        assert np.array_equal(i1, i2), (t, "info", np.flatnonzero((i1 != i2).any(1))[:8].tolist())
+        bad = np.flatnonzero((o1 != o2).reshape(n, -1).any(1))
+        assert bad.size == 0, (t, "obs of envs", bad[:8].tolist())
+    pool.shutdown()
+    assert gpu.frames == sum(c.frames() for c in cpu)
+    assert gpu.instructions() == sum(c.instructions() for c in cpu)
+    assert gpu.bad_ops() == 0
+    gpu.close()
+
+
 def test_headline_32768_envs_bench_stream():
     """The measured configuration itself: 32,768 envs of 1-1 with the headline wrappers (sticky 0.25, no-op 30,
     skip 4, max-pool, stack 4, seed 0), launched as bench.py launches it (2,048 waves in 256 workgroups of 8 waves,
