@@ -370,6 +370,7 @@ struct RawArgs {
     int render;
     uint32_t* bad; uint32_t* instr; uint32_t* ff;
     int power_on;
+    int cpw;                     // consoles per wave (k_raw): 1, 2, 4, 8 or ENVS_PER_WAVE
 };
 
 // ------------------------------------------------------------------ env words

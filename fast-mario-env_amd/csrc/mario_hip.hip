@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <tuple>
 #include <cstring>
 #include <map>
@@ -73,6 +74,22 @@ static inline EmuLaunch emu_launch(int count, int cus) {
     waves = waves < 1 ? 1 : waves > WAVES_PER_BLOCK ? WAVES_PER_BLOCK : waves;
     const int slots = waves * ENVS_PER_WAVE;
     return EmuLaunch{dim3((unsigned)((count + slots - 1) / slots)), dim3((unsigned)(64 * waves))};
+}
+// Launch shape of k_raw over `count` consoles: fewer consoles per wave (a power of two, cpw) where the count is too
+// small to give every SIMD two waves of 16. A raw batch of 4,096 consoles is then 2,048 waves of 2 instead of 256
+// waves of 16 (one per CU, three of its four SIMDs idle): a wave's iterations follow the union of its consoles'
+// instruction streams and slice waits, so fewer consoles per wave also means fewer iterations per console, and
+// the lanes a wave leaves idle would have had no SIMD to run on anyway. force > 0 sets cpw instead (one of 1, 2, 4,
+// 8, 16: the MH_RAW_CONSOLES_PER_WAVE environment variable at mh_raw_create).
+static inline EmuLaunch raw_launch(int count, int cus, int force, int& cpw) {
+    const int target = 4 * EMU_WAVES_PER_SIMD * (cus > 0 ? cus : 1);   // waves that fill every SIMD
+    cpw = ENVS_PER_WAVE;
+    while (force <= 0 && cpw > 1 && (count + cpw / 2 - 1) / (cpw / 2) <= target) cpw /= 2;
+    if (force > 0) cpw = force;
+    const int waves = (count + cpw - 1) / cpw;
+    int wpb = (waves + (cus > 0 ? cus : 1) - 1) / (cus > 0 ? cus : 1);   // waves per block: spread over the CUs
+    wpb = wpb < 1 ? 1 : wpb > WAVES_PER_BLOCK ? WAVES_PER_BLOCK : wpb;
+    return EmuLaunch{dim3((unsigned)((waves + wpb - 1) / wpb)), dim3((unsigned)(64 * wpb))};
 }
 // first console slot of this block (blocks of blockDim.x / 64 waves)
 __device__ __forceinline__ uint32_t block_base() { return blockIdx.x * ((blockDim.x >> 6) * ENVS_PER_WAVE); }
@@ -301,12 +318,15 @@ __global__ void __launch_bounds__(256) k_obs_late(ObsLateArgs A) {
     obs_tail<1>(A.gray, A.np, A.fresh, A.boot_obs, e, lane / ENVS_PER_WAVE, bits, u % 12);
 }
 
+// A wave carries A.cpw consoles (raw_launch): its lanes l, l + 16, l + 32, l + 48 with l < cpw run console
+// wave * cpw + l of the block; the others idle.
 __global__ void EMU_BOUNDS k_raw(RawArgs A) {
     ROM_LDS
     stage_rom(A.R, s_rom, s_lut, s_dec);
-    const int slot = lane_slot();
-    const uint32_t e = block_base() + (uint32_t)slot;
-    if (e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
+    const int in_wave = (int)(threadIdx.x & (ENVS_PER_WAVE - 1));
+    const int slot = (int)(threadIdx.x >> 6) * A.cpw + in_wave;
+    const uint32_t e = blockIdx.x * ((blockDim.x >> 6) * (uint32_t)A.cpw) + (uint32_t)slot;
+    if (in_wave < A.cpw && e < (uint32_t)A.n) raw_lane(A, lane_ctx(A.R, s_rom, s_lut, s_dec, s_sp, s_gp, slot), e);
 }
 
 // One wave of 64 envs per block: each lane draws its env's reset, then the wave copies the chosen cache
@@ -769,7 +789,8 @@ static void launch_stack(const MhEnv* h, hipStream_t s, int mode) {
 }
 
 struct MhRaw {
-    int n = 0, device = 0, cus = 0;
+    int n = 0, device = 0, cus = 0, cpw = 0;
+    EmuLaunch lr{};                // k_raw's launch shape, with cpw consoles per wave (raw_launch)
     uint32_t np = 0;
     DevBufs B;
     RomArgs R{};
@@ -1145,6 +1166,14 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     g_err.clear();
     if (n < 1) { g_err = "invalid arguments"; return nullptr; }
     if ((uint32_t)n > MAX_ENVS) { g_err = "too many consoles (at most 979,648: console memory takes 32-bit offsets)"; return nullptr; }
+    int force = 0;
+    if (const char* f = getenv("MH_RAW_CONSOLES_PER_WAVE"); f && *f) {
+        force = atoi(f);
+        if (force != 1 && force != 2 && force != 4 && force != 8 && force != ENVS_PER_WAVE) {
+            g_err = "MH_RAW_CONSOLES_PER_WAVE must be 1, 2, 4, 8 or 16";
+            return nullptr;
+        }
+    }
     std::vector<uint8_t> img;
     uint16_t nt[4];
     if (!load_cart(rom, rom_len, img, nt)) return nullptr;
@@ -1152,6 +1181,7 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     MhRaw* h = new MhRaw();
     bool good = true;
     h->n = n; h->np = pad64(n); h->device = device; h->cus = device_cus(device);
+    h->lr = raw_launch(n, h->cus, force, h->cpw);
     auto& B = h->B;
     uint8_t* d_rom = B.alloc<uint8_t>(0xa000, good);
     uint8_t* d_lut = B.alloc<uint8_t>(256, good);
@@ -1171,17 +1201,15 @@ MhRaw* mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device) {
     h->R.rom = d_rom; h->R.lut = d_lut; h->R.n_chr = 1;
     h->R.nt_bits = 0;
     for (int i = 0; i < 4; i++) h->R.nt_bits |= (nt[i] ? 1u : 0u) << i;
-    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, h->ff, 1};
-    const EmuLaunch lr = emu_launch(h->n, h->cus);
-    hipLaunchKernelGGL(k_raw, lr.grid, lr.block, 0, 0, ra);
+    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, nullptr, 0, h->bad, h->instr, h->ff, 1, h->cpw};
+    hipLaunchKernelGGL(k_raw, h->lr.grid, h->lr.block, 0, 0, ra);
     if (!ok(hipDeviceSynchronize(), "raw power-on")) { delete h; return nullptr; }
     return h;
 }
 int mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream) {
     if (!h || !d_buttons) return -1;
-    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, d_buttons, render, h->bad, h->instr, h->ff, 0};
-    const EmuLaunch lr = emu_launch(h->n, h->cus);
-    hipLaunchKernelGGL(k_raw, lr.grid, lr.block, 0, (hipStream_t)stream, ra);
+    RawArgs ra{h->R, h->n, h->np, h->mem, h->sc, h->screen, d_buttons, render, h->bad, h->instr, h->ff, 0, h->cpw};
+    hipLaunchKernelGGL(k_raw, h->lr.grid, h->lr.block, 0, (hipStream_t)stream, ra);
     CK(hipGetLastError());
     return 0;
 }

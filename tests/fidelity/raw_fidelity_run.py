@@ -1,7 +1,8 @@
 """GPU-vs-oracle fidelity record of the raw consoles over a long horizon (test infrastructure; the product path is the
 HIP library).
 
-    python tests/fidelity/raw_fidelity_run.py [--consoles 512] [--frames 5000] [--out tests/fidelity/raw_fidelity.jsonl]
+    python tests/fidelity/raw_fidelity_run.py [--consoles 512] [--frames 5000] [--cpw auto|1|2|4|8|16]
+        [--out tests/fidelity/raw_fidelity.jsonl]
 
 The reference publishes a 100k-frame raw run with RAM every frame (README.md:166-170). Here HipRawNES runs the
 consoles on the GPU and the CPU checker (oracle/liboracle.so) runs one console each on a thread pool, with the
@@ -10,7 +11,8 @@ console and frame from default_rng(1), every frame rendered. Every console every
 whole machine state (the canonical dump); the palette screen every 4th frame; at the end the bad-opcode and
 retired-instruction counts. Past frame ~200 the consoles are out of phase (deaths, level reloads and game-over
 screens at different points of a frame), the regime whose long single-console instruction runs set the raw
-kernel's time. One JSON line per ROM.
+kernel's time. --cpw sets k_raw's consoles per wave (MH_RAW_CONSOLES_PER_WAVE; "auto": the library's choice, one
+per wave at 512 consoles). One JSON line per ROM.
 """
 from __future__ import annotations
 
@@ -37,7 +39,7 @@ PROLOGUE = 40
 BUTTONS = np.array([0x00, 0x80, 0x81, 0x82, 0x83, 0x01, 0x40], np.uint8)   # SIMPLE_MOVEMENT as joypad bytes
 
 
-def run(mode, n, frames, log):
+def run(mode, n, frames, cpw, log):
     import torch
 
     from fast_mario_env_amd import HipRawNES
@@ -75,7 +77,8 @@ def run(mode, n, frames, log):
     instr_c = sum(c.instructions() for c in cpu)
     if gpu.instructions() != instr_c:
         mism.append({"frame": len(sched), "what": "instructions"})
-    rec = {"rom": f"synthetic stand-in (tests/golden/roms, {mode})", "consoles": n, "frames": len(sched),
+    rec = {"rom": f"synthetic stand-in (tests/golden/roms, {mode})", "consoles": n, "consoles_per_wave": cpw,
+           "frames": len(sched),
            "prologue": PROLOGUE, "console_frames": n * len(sched), "screens_compared": screens,
            "instructions": int(gpu.instructions()), "ff_instructions": int(gpu.ff_instructions()),
            "bad_ops": int(gpu.bad_ops()), "oracle_bad_ops": int(bad_c), "mismatches": mism, "ok": not mism,
@@ -89,12 +92,15 @@ def main():
     ap.add_argument("--consoles", type=int, default=512)
     ap.add_argument("--frames", type=int, default=5000)
     ap.add_argument("--modes", default="vanilla")
+    ap.add_argument("--cpw", default="auto")
     ap.add_argument("--out", default=os.path.join(HERE, "raw_fidelity.jsonl"))
     args = ap.parse_args()
     log = lambda m: print(m, flush=True)  # noqa: E731
+    if args.cpw != "auto":
+        os.environ["MH_RAW_CONSOLES_PER_WAVE"] = args.cpw
     recs = []
     for mode in args.modes.split(","):
-        rec = run(mode, args.consoles, args.frames, log)
+        rec = run(mode, args.consoles, args.frames, args.cpw, log)
         log(json.dumps(rec))
         recs.append(rec)
     with open(args.out, "w") as f:

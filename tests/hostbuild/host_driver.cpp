@@ -88,7 +88,7 @@ int run_raw(const char* rom_file) {
     std::vector<uint8_t> mem((size_t)MEM_ROWS * np), bk_mem(mem.size()), screen((size_t)GRAY_PIX * np);
     std::vector<uint32_t> sc((size_t)S_COUNT * np), bk_sc(sc.size()), bad(np), instr(np), ff(np);
     std::vector<uint8_t> buttons(np);
-    RawArgs A{L.R, n, np, mem.data(), sc.data(), screen.data(), buttons.data(), 0, bad.data(), instr.data(), ff.data(), 1};
+    RawArgs A{L.R, n, np, mem.data(), sc.data(), screen.data(), buttons.data(), 0, bad.data(), instr.data(), ff.data(), 1, 1};
     raw_lane(A, L.ctx(0), 0);
     A.power_on = 0;
     for (;;) {

@@ -146,6 +146,20 @@ def test_create_rejects_more_envs_than_32bit_offsets_address():
     assert b"too many consoles" in L.mh_last_error()
 
 
+@pytest.mark.parametrize("value", ["3", "32", "0", "x"])
+def test_raw_create_rejects_bad_consoles_per_wave(monkeypatch, value):
+    """MH_RAW_CONSOLES_PER_WAVE (k_raw's consoles per wave, a power of two up to 16) is checked at creation,
+    before the device is touched."""
+    L = ctypes.CDLL(_native.lib_path())
+    L.mh_raw_create.restype = ctypes.c_void_p
+    L.mh_last_error.restype = ctypes.c_char_p
+    monkeypatch.setenv("MH_RAW_CONSOLES_PER_WAVE", value)
+    mini = open(rom_path("vanilla"), "rb").read()
+    blob = np.frombuffer(mini, np.uint8).copy()
+    assert not L.mh_raw_create(ctypes.c_void_p(blob.ctypes.data), ctypes.c_int64(len(mini)), 4, 0)
+    assert b"MH_RAW_CONSOLES_PER_WAVE must be" in L.mh_last_error()
+
+
 @pytest.mark.skipif(HAVE_GPU, reason="checks the no-GPU error path")
 def test_no_cpu_fallback():
     """Without a GPU the product raises; there is no silent CPU path."""

@@ -17,6 +17,9 @@ from cpu_libs import OracleRaw, OracleVec
 pytestmark = pytest.mark.gpu
 
 MINI = open(rom_path("vanilla"), "rb").read()
+# k_raw's consoles per wave: "auto" lets the library choose (few consoles: one per wave, every SIMD busy), 16 fills
+# every wave, so that lanes of one wave run different consoles and force catch-ups on each other
+CPW = ["auto", "16"]
 
 
 def _first_diff(a, b):
@@ -24,11 +27,13 @@ def _first_diff(a, b):
     return d[:8].tolist()
 
 
-def _raw_run(rom, n, frames, seed, render_p=0.5, backup_p=0.0, rgb=False):
+def _raw_run(rom, n, frames, seed, render_p=0.5, backup_p=0.0, rgb=False, cpw="auto", monkeypatch=None):
     import torch
 
     from fast_mario_env_amd import HipRawNES, palette_rgb
     pal = palette_rgb()
+    if cpw != "auto":
+        monkeypatch.setenv("MH_RAW_CONSOLES_PER_WAVE", cpw)
     gpu = HipRawNES(rom, n)
     cpu = [OracleRaw(rom) for _ in range(n)]
     rng = np.random.default_rng(seed)
@@ -62,8 +67,9 @@ def _raw_run(rom, n, frames, seed, render_p=0.5, backup_p=0.0, rgb=False):
     assert gpu.instructions() == sum(c.instructions() for c in cpu)
 
 
-def test_raw_mini_smb():
-    _raw_run(MINI, 8, scaled(120), seed=1, rgb=True)
+@pytest.mark.parametrize("cpw", CPW)
+def test_raw_mini_smb(cpw, monkeypatch):
+    _raw_run(MINI, 8, scaled(120), seed=1, rgb=True, cpw=cpw, monkeypatch=monkeypatch)
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
@@ -71,18 +77,21 @@ def test_raw_program_fuzz(seed):
     _raw_run(fuzz.program_rom(seed), 4, scaled(80), seed=seed, backup_p=0.05)
 
 
-def test_raw_program_fuzz_two_waves():
-    # 40 consoles: two full 16-console waves and a partial one, so catch-ups that one lane forces on the others
-    # of its wave (PPU register accesses at different points) are compared across many lanes
-    _raw_run(fuzz.program_rom(3), 40, scaled(40), seed=3, backup_p=0.05)
+@pytest.mark.parametrize("cpw", CPW + ["4"])
+def test_raw_program_fuzz_two_waves(cpw, monkeypatch):
+    # 40 consoles; with 16 per wave two full waves and a partial one, so catch-ups that one lane forces on the
+    # others of its wave (PPU register accesses at different points) are compared across many lanes
+    _raw_run(fuzz.program_rom(3), 40, scaled(40), seed=3, backup_p=0.05, cpw=cpw, monkeypatch=monkeypatch)
 
 
+@pytest.mark.parametrize("cpw", CPW)
 @pytest.mark.parametrize("seed", [0, 1, 3])
-def test_raw_screen_off_fuzz(seed):
+def test_raw_screen_off_fuzz(seed, cpw, monkeypatch):
     # an NMI handler that makes its VRAM, scroll and address writes with rendering off (a bulk $2007 loop among
-    # them) and turns rendering on at its end; 40 consoles, so a console often runs alone in its wave and its
-    # lone runs make those writes themselves
-    _raw_run(fuzz.program_rom(seed, screen_off=True), 40, scaled(60), seed=seed, backup_p=0.05)
+    # them) and turns rendering on at its end; 40 consoles: a console often runs alone in its wave (always, with
+    # one console per wave) and its lone runs make those writes themselves
+    _raw_run(fuzz.program_rom(seed, screen_off=True), 40, scaled(60), seed=seed, backup_p=0.05, cpw=cpw,
+             monkeypatch=monkeypatch)
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2])

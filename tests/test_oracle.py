@@ -254,7 +254,7 @@ def test_fidelity_records():
     """The committed fidelity records (tests/fidelity/*.jsonl, written on the GPU by the scripts beside them) hold
     the runs they claim, with no mismatch: 512 envs over the 32 levels x 1,500 steps in each of 5 configurations
     (every env every step against the oracle), and 512 raw consoles x 20,040 frames (RAM and machine state every
-    frame, the screen every 4th)."""
+    frame, the screen every 4th), once with the library's launch shape and once with 16 consoles per wave."""
     import json
     d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "fidelity")
     env = [json.loads(l) for l in open(os.path.join(d, "env_fidelity.jsonl"))]
@@ -265,5 +265,7 @@ def test_fidelity_records():
     assert sum(r["flags"] for r in env) > 0          # the runner reaches the flagpole
     assert env[3]["reemulations"]["pair"] > 0 and env[3]["reemulations"]["k2"] > 0
     raw = [json.loads(l) for l in open(os.path.join(d, "raw_fidelity.jsonl"))]
-    assert len(raw) == 1 and raw[0]["ok"] and not raw[0]["mismatches"]
-    assert raw[0]["consoles"] == 512 and raw[0]["frames"] == 20040 and raw[0]["bad_ops"] == 0
+    assert [r["consoles_per_wave"] for r in raw] == ["auto", "16"]     # k_raw's launch shapes: 1 and 16 per wave
+    for r in raw:
+        assert r["ok"] and not r["mismatches"] and r["consoles"] == 512 and r["frames"] == 20040
+        assert r["bad_ops"] == 0 and r["instructions"] == raw[0]["instructions"]
