@@ -219,6 +219,11 @@ __device__ __constant__ static const dec::Table kDecode{};
 #ifndef MH_SCALAR_CONST
 #define MH_SCALAR_CONST __attribute__((address_space(4)))
 #endif
+// Device memory addressed as such (global loads and stores: no flat-address aperture check, and their waits
+// count only vector memory, not the scalar loads in flight beside them)
+#ifndef MH_GLOBAL
+#define MH_GLOBAL __attribute__((address_space(1)))
+#endif
 
 // ---------------------------------------------------------------- long lone runs
 // A console that is the only one of its wave with instructions to run (Console::lone_run()) runs them in
@@ -236,8 +241,8 @@ struct LoneRegs { uint32_t pc, a, x, y, sp, p; int32_t ex; uint32_t zs, vt, px, 
 constexpr uint32_t LP_WRITES = 1u, LP_INC32 = 2u, LP_NT_SHIFT = 4;
 struct LoneCore {
     LoneRegs r;
-    uint8_t* mem;                              // the console's RAM row 0 (row stride np), the same in every active lane
-    uint8_t* vmem;                             // its VRAM word 0 (word stride 4 np)
+    MH_GLOBAL uint8_t* mem;                    // the console's RAM row 0 (row stride np), the same in every active lane
+    MH_GLOBAL uint8_t* vmem;                   // its VRAM word 0 (word stride 4 np)
     uint32_t np, pflags;
     const MH_SCALAR_CONST uint32_t* gprg;      // PRG image (read only): scalar loads
     __device__ __forceinline__ uint32_t ram(uint32_t ad) const {
@@ -443,8 +448,8 @@ __device__ __attribute__((noinline)) LoneRegs lone_long(LoneRegs in, int32_t lim
     c.r.zs = __builtin_amdgcn_readfirstlane(in.zs);
     c.r.vt = __builtin_amdgcn_readfirstlane(in.vt); c.r.px = __builtin_amdgcn_readfirstlane(in.px);
     lim = (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)lim);
-    c.mem = (uint8_t*)lone_uniform64((uint64_t)mem);
-    c.vmem = (uint8_t*)lone_uniform64((uint64_t)vmem);
+    c.mem = (MH_GLOBAL uint8_t*)(void*)lone_uniform64((uint64_t)mem);
+    c.vmem = (MH_GLOBAL uint8_t*)(void*)lone_uniform64((uint64_t)vmem);
     c.np = __builtin_amdgcn_readfirstlane(np);
     c.pflags = __builtin_amdgcn_readfirstlane(pflags);
     c.gprg = (const MH_SCALAR_CONST uint32_t*)(const void*)lone_uniform64((uint64_t)gprg);

@@ -17,6 +17,7 @@
 #define __forceinline__ inline __attribute__((always_inline))
 // host memory has one address space
 #define MH_SCALAR_CONST
+#define MH_GLOBAL
 
 // a one-lane wave
 static inline unsigned __lane_id() { return 0u; }
