@@ -308,6 +308,8 @@ __device__ __forceinline__ bool lone_op(LoneCore& c, uint32_t b1, uint32_t b2) {
         return false;
     } else {
         LoneRegs& r = c.r;
+        if constexpr (OP == 0x4cu)
+            if ((b1 | b2 << 8) == r.pc) return false;   // JMP *: frame()'s idle fast-forward
         const uint32_t absv = b1 | b2 << 8;
         const uint32_t p2 = (absv & 0xff00u) | ((absv + 1u) & 0xffu);   // JMP (ind): high byte, page wrap
         uint32_t ea = 0, base = absv;
@@ -453,18 +455,19 @@ __device__ __attribute__((noinline)) LoneRegs lone_long(LoneRegs in, int32_t lim
     c.np = __builtin_amdgcn_readfirstlane(np);
     c.pflags = __builtin_amdgcn_readfirstlane(pflags);
     c.gprg = (const MH_SCALAR_CONST uint32_t*)(const void*)lone_uniform64((uint64_t)gprg);
+    // the catch-up test 3 (ex + 1) > lim as ex > exlim, exlim = floor((lim - 3) / 3)
+    const int32_t l3 = lim - 3;
+    const int32_t exlim = l3 / 3 - (l3 % 3 < 0 ? 1 : 0);
     uint32_t n = 0;
     for (;;) {
-        if (3 * c.r.ex + 3 > lim) break;                   // parks or catches up in frame()
+        if (c.r.ex > exlim) break;                         // parks or catches up in frame()
         if (c.r.pc - 0x8000u > 0x7ffdu) break;             // opcode or operands through the bus
         const uint32_t pa = c.r.pc & 0x7fffu;
         const uint64_t w = (uint64_t)c.gprg[(pa >> 2) + 1] << 32 | c.gprg[pa >> 2];
         const uint32_t b0 = (uint32_t)(w >> (8 * (pa & 3u)));   // bytes pc .. pc + 3
         const uint32_t op = b0 & 0xffu, b1 = (b0 >> 8) & 0xffu, b2 = (b0 >> 16) & 0xffu;
-        if (op == 0x4cu && (b1 | b2 << 8) == c.r.pc) break;  // JMP *: frame()'s idle fast-forward
-        bool ran = false;
-        switch (op) {
-#define MH_LONE_CASE(i) case i: ran = lone_op<i>(c, b1, b2); break;
+        switch (op) {   // an opcode that needs frame() (lone_op() false) ends the run
+#define MH_LONE_CASE(i) case i: if (!lone_op<i>(c, b1, b2)) goto done; break;
 #define MH_LONE_CASE4(i) MH_LONE_CASE(i) MH_LONE_CASE(i + 1) MH_LONE_CASE(i + 2) MH_LONE_CASE(i + 3)
 #define MH_LONE_CASE16(i) MH_LONE_CASE4(i) MH_LONE_CASE4(i + 4) MH_LONE_CASE4(i + 8) MH_LONE_CASE4(i + 12)
 #define MH_LONE_CASE64(i) MH_LONE_CASE16(i) MH_LONE_CASE16(i + 16) MH_LONE_CASE16(i + 32) MH_LONE_CASE16(i + 48)
@@ -473,11 +476,11 @@ __device__ __attribute__((noinline)) LoneRegs lone_long(LoneRegs in, int32_t lim
 #undef MH_LONE_CASE16
 #undef MH_LONE_CASE4
 #undef MH_LONE_CASE
-            default: break;
+            default: goto done;
         }
-        if (!ran) break;
         n++;
     }
+done:
     c.r.n = n;
     return c.r;
 }
