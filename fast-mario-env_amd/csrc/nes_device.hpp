@@ -55,6 +55,12 @@ constexpr int LDS_OAM_WORDS = 64;                  // words per lane: OAM (sprit
 constexpr int LDS_XCHG_WORDS = LANES_PER_ENV;     // words per env slot: the parts' pieces of the sprite-range mask
 constexpr int LDS_GP_REGION = LDS_GP_WORDS + LDS_BG_WORDS + LDS_OAM_WORDS + LDS_XCHG_WORDS;   // palette, tile row, OAM, exchange
 constexpr int FRAME_ITERS = 29781;                 // CPU iterations per nes-py Emulator::step
+#ifndef MH_LONE_MAX_ENVS
+#define MH_LONE_MAX_ENVS 6
+#endif
+// Lone runs (Console::lone_run) take over a wave's instructions once at most this many of its consoles have any
+// left in the current stretch: those consoles' runs follow one another.
+constexpr int LONE_MAX_ENVS = MH_LONE_MAX_ENVS;
 // Render lines per frame slice (a power of two). A wave runs its lanes' CPUs to the end of a group of
 // this many lines and then catches their PPUs up together; a wave iteration costs the slowest lane's
 // instruction, so longer slices let the lanes' per-line instruction counts average out, while a lane
@@ -1639,13 +1645,19 @@ struct Console {
             bool act = !parked;
             if (act && (j >= end || tgt > slice)) { parked = true; act = false; }
             if (act && tgt >= nmi_thresh && ppu_calls < tgt) { want = tgt; act = false; }
-            {   // one console left to run instructions and no catch-up asked for: its run of lone instructions
+            {   // at most LONE_MAX_ENVS consoles left to run instructions and no catch-up asked for: each one's
+                // run of lone instructions, one console after the other (its own lanes only)
                 const uint64_t go = __ballot(act);
-                const uint64_t env = PART_LANES << (__builtin_ctzll(go | (1ull << 63)) & (ENVS_PER_WAVE - 1));
                 // (a run of at least one instruction is this iteration's action: no early `continue`, whose
                 // extra path into the loop top would make the compiler merge the console state there)
-                if (go && !(go & ~env) && !__any(want >= 0)) {
-                    if (act && lone_run(end, slice) != 0) act = false;
+                if (go && __popcll(go) <= LONE_MAX_ENVS * LANES_PER_ENV && !__any(want >= 0)) {
+                    uint64_t rest = go;
+                    do {   // wave-uniform: rest is a ballot
+                        const uint64_t env = PART_LANES << (__builtin_ctzll(rest) & (ENVS_PER_WAVE - 1));
+                        if ((env >> __lane_id()) & 1u)
+                            if (act && lone_run(end, slice) != 0) act = false;
+                        rest &= ~env;
+                    } while (rest);
                 }
             }
             // PRG bytes pc .. pc + 6 for the fast paths, from three aligned LDS words and two byte-aligns (the

@@ -24,6 +24,7 @@ static inline unsigned __lane_id() { return 0u; }
 static inline uint64_t __ballot(int p) { return p ? 1ull : 0ull; }
 static inline int __any(int p) { return p != 0; }
 static inline int __all(int p) { return p != 0; }
+static inline int __popcll(unsigned long long v) { return __builtin_popcountll(v); }
 // a one-lane wave's first active lane is the lane itself; like the device builtin, it takes and returns a
 // signed int (widening its result to 64 bits sign-extends it, on the host as on the device)
 static inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
