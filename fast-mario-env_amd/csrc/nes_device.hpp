@@ -232,12 +232,14 @@ __device__ __constant__ static const dec::Table kDecode{};
 #endif
 
 // ---------------------------------------------------------------- long lone runs
-// A console that is the only one of its wave with instructions to run (Console::lone_run()) runs them in
-// lone_long(): out of line, in registers of its own (not the frame loop's), wave-uniform, with one body per
-// opcode whose decode word is known at compile time, so that the addressing, the operation, its flags and its
-// control flow fold to the few scalar instructions the opcode needs. Measured on one console running a loop of
-// register instructions: 0.33 us per instruction, against 0.67 us for a body that takes the decode word's
-// fields at run time (inline, as a switch per field).
+// A console that is one of the last few of its wave with instructions to run (at most LONE_MAX_ENVS; the frame
+// loop calls Console::lone_run() for each of them in turn, under its own lanes) runs them in lone_long(): out of
+// line, in registers of its own (not the frame loop's), wave-uniform, with one body per opcode whose decode word
+// is known at compile time, so that the addressing, the operation, its flags and its control flow fold to the
+// few scalar instructions the opcode needs. Measured on one console running a loop of register instructions:
+// 0.18 us per instruction (built with the structurizer skipping uniform regions, which leaves the opcode switch a
+// plain compare tree; 0.37 us without), against 0.67 us for a body that takes the decode word's fields at run
+// time (inline, as a switch per field).
 // The registers of a lone run, wave-uniform: pc, a, x, y, sp, p, exec_at (ex), zero_skip (zs), the PPU's v and t
 // (vt: v | t << 16), fine x and write toggle (px: fine_x | first_write << 8; outputs: bit 16, the run wrote the
 // name tables through $2007, and bit 17, it wrote a PPU register), and n, the instructions run (an output).
@@ -1474,10 +1476,12 @@ struct Console {
     }
 
     // ------------------------------------------------------------ a lone console's instruction run
-    // While a console is the only one of its wave with an instruction to run (the others parked at their slice
-    // end, or out of the frame loop), an iteration of frame()'s loop costs about what it costs a full wave: every
-    // opcode's work as selects, the wave votes and the catch-up checks. lone_run() runs that console's
-    // instructions back to back instead, in lone_long(), with its registers wave-uniform and one body per opcode.
+    // While a console is one of the last few of its wave with an instruction to run (at most LONE_MAX_ENVS; the
+    // others parked at their slice end, or out of the frame loop), an iteration of frame()'s loop costs about
+    // what it costs a full wave: every opcode's work as selects, the wave votes and the catch-up checks.
+    // lone_run() runs that console's instructions back to back instead (the frame loop calls it for those
+    // consoles one after the other, each under its own lanes' exec mask), in lone_long(), with its registers
+    // wave-uniform and one body per opcode.
     // It runs the instructions whose opcode and operands are in PRG and whose bus accesses touch only RAM, PRG,
     // or addresses that read as 0 or ignore writes ($4000-$7FFF but the joypads and OAM DMA), as instruction()
     // would; it stops before any other instruction (PPU register, joypad or DMA access, invalid opcode), before

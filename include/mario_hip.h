@@ -122,7 +122,9 @@ int64_t mh_state_bytes(void);
 int64_t mh_env_bytes(MhEnv* h);
 
 /* ---- raw consoles: frame stepping without the env layer (replaces fm_raw_*, fastmario.cpp:651-673) */
-/* 1 <= n <= 979648 consoles (32-bit offsets into the console memory) */
+/* 1 <= n <= 979648 consoles (32-bit offsets into the console memory). The consoles run 1 to 16 per wave (the
+   most that still give every SIMD two waves); MH_RAW_CONSOLES_PER_WAVE=1|2|4|8|16 in the environment at this
+   call sets it instead (any other value: NULL, with mh_last_error()). Results do not depend on it. */
 MhRaw*  mh_raw_create(const uint8_t* rom, int64_t rom_len, int n, int device);
 /* one frame of every console; d_buttons: n u8 device pointer; render != 0 draws the screen */
 int     mh_raw_frame(MhRaw* h, const uint8_t* d_buttons, int render, void* stream);
